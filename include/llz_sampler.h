@@ -1,0 +1,160 @@
+/*
+ * llz_sampler.h -- C ABI of the MI355X token-sampling library (libllzsample.so).
+ *
+ * Drop-in replacement for llama.zig's sampler (src/sampler.zig).  The
+ * reference's Zig API is
+ *     Sampler.init(cfg: SamplerConfig) Sampler                      sampler.zig:19-24
+ *     Sampler.sample(self, allocator, logits, prev_tokens) !TokenID sampler.zig:26-28
+ *     sampleArgmax(logits) TokenID                                  sampler.zig:31-41
+ * and its decode loop calls them at main.zig:508-518 and main.zig:667.
+ * This header exposes:
+ *   - llz_sample_rows / llz_argmax_rows: batched, device-resident, async on a
+ *     HIP stream; the kernels behind them reproduce sampleWithRandom
+ *     (sampler.zig:43-169) bit for bit given the same uniform per row;
+ *   - llz_sampler_*: a host-side object with the reference's Sampler
+ *     semantics (seed fallback, one PRNG stream, a draw consumed only when the
+ *     reference draws), for a one-line swap in main.zig;
+ *   - llz_rng_*: the reference's PRNG (std.Random.DefaultPrng seeded by
+ *     SplitMix64, Random.float(f32)), so callers can generate per-row
+ *     uniforms from the same seeded stream.
+ *
+ * Conventions: plain pointers and sizes; `stream` is a hipStream_t passed as
+ * void* (NULL = the default stream); device pointers are marked d_.  Every
+ * function returns 0 (LLZ_OK) or a negative LLZ_E* code; llz_strerror names
+ * it.  llz_sample_rows and llz_argmax_rows never allocate: the caller passes
+ * the workspace sized by llz_sample_workspace_bytes.
+ */
+#ifndef LLZ_SAMPLER_H
+#define LLZ_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    LLZ_OK = 0,
+    LLZ_E_INVALID_ARG = -1,   /* null pointer, rows/vocab <= 0, NaN temperature, ... */
+    LLZ_E_WORKSPACE = -2,     /* workspace missing or smaller than required          */
+    LLZ_E_HIP = -3,           /* a HIP runtime call failed                           */
+    LLZ_E_OOM = -4,           /* host-side object could not allocate                 */
+    LLZ_E_NO_DEVICE = -5      /* no usable HIP device                                */
+};
+
+/* Mirror of SamplerConfig (sampler.zig:4-13).  Field meanings and defaults
+ * are the reference's: temperature 0.8, top_k 0, top_p 0.9, min_p 0.0,
+ * typical_p 1.0, seed 0 (-> 0xDEADBEEF), repetition_window 32,
+ * repetition_penalty 1.1.  A filter is active exactly when the reference's
+ * test is true: 0 < top_k < vocab, 0 < top_p < 1, min_p > 0,
+ * 0 < typical_p < 1, repetition_penalty != 1 with a non-empty window. */
+typedef struct llz_sampler_config {
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    float min_p;
+    float typical_p;
+    uint32_t repetition_window;
+    float repetition_penalty;
+    uint32_t reserved;          /* must be 0 */
+    uint64_t seed;
+} llz_sampler_config;
+
+/* Fills `cfg` with SamplerConfig's defaults (sampler.zig:4-13). */
+void llz_sampler_config_default(llz_sampler_config *cfg);
+
+/* Optional per-row outputs of llz_sample_rows.  Any pointer may be NULL. */
+typedef struct llz_sample_extras {
+    uint32_t *d_kept_count;     /* [rows] size of the final kept set                        */
+    uint32_t *d_kept_ids;       /* [rows][kept_cap] kept ids in (p desc, id asc) order       */
+    float *d_kept_probs;        /* [rows][kept_cap] their normalised probabilities          */
+    int32_t kept_cap;           /* capacity per row of the two arrays above                 */
+    int32_t reserved;
+    float *d_row_stats;         /* [rows][4]: max logit, normaliser, entropy, total kept     */
+} llz_sample_extras;
+
+/* Bytes of device workspace llz_sample_rows needs for this shape and
+ * configuration (0 on invalid input).  n_prev is the repetition window
+ * length per row that will be passed. */
+size_t llz_sample_workspace_bytes(int32_t rows, int32_t vocab, const llz_sampler_config *cfg,
+                                  int32_t n_prev);
+
+/* Samples one token per row from `rows` fp32 logit rows of length `vocab`
+ * (row r at d_logits + r * row_stride), replacing Sampler.sample /
+ * sampleWithRandom (sampler.zig:26-28, :43-169) for a batch.
+ *   d_prev_tokens: repetition history, n_prev ids per row, rows prev_stride
+ *                  apart (prev_stride 0 = one history shared by all rows);
+ *                  may be NULL when n_prev == 0.
+ *   d_uniforms:    [rows] the value random.float(f32) would return at
+ *                  sampler.zig:162 for that row.
+ *   d_tokens:      [rows] sampled TokenID (sampler.zig's return value).
+ *   d_consumed:    [rows] 1 when the row reached the draw (sampler.zig:162)
+ *                  and so consumed its uniform, 0 on the early exits
+ *                  (temperature <= 0, sum <= 0, empty kept set).  May be NULL.
+ * The call is asynchronous on `stream`. */
+int llz_sample_rows(const float *d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                    const llz_sampler_config *cfg, const uint32_t *d_prev_tokens, int32_t n_prev,
+                    int64_t prev_stride, const float *d_uniforms, uint32_t *d_tokens,
+                    uint8_t *d_consumed, const llz_sample_extras *extras, void *d_workspace,
+                    size_t workspace_bytes, void *stream);
+
+/* sampleArgmax (sampler.zig:31-41) per row: the first index of the
+ * strict maximum, scanning from index 0.  Replaces the greedy GPU path
+ * executeTopK / topk_bda.glsl (compute_graph.zig:948-984), keeping the
+ * reference sampler's tie-break.  Asynchronous on `stream`. */
+int llz_argmax_rows(const float *d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                    uint32_t *d_tokens, void *stream);
+
+/* ---- the reference's PRNG (std.Random.DefaultPrng, sampler.zig:17,22,162) ---- */
+
+/* state <- Xoshiro256.init(seed): four successive SplitMix64 outputs. */
+void llz_rng_seed(uint64_t state[4], uint64_t seed);
+/* One xoshiro256++ output. */
+uint64_t llz_rng_next(uint64_t state[4]);
+/* Random.float(f32). */
+float llz_rng_float(uint64_t state[4]);
+/* count successive Random.float(f32) draws into out (host memory). */
+void llz_rng_uniforms(uint64_t state[4], float *out, int64_t count);
+
+/* ---- host-side Sampler with the reference's lifecycle (sampler.zig:15-28) ---- */
+
+typedef struct llz_sampler llz_sampler;
+
+/* Sampler.init: keeps cfg, seeds the PRNG with seed != 0 ? seed : 0xDEADBEEF.
+ * `device` selects the HIP device the sampler runs on. */
+int llz_sampler_create(const llz_sampler_config *cfg, int32_t device, llz_sampler **out);
+void llz_sampler_destroy(llz_sampler *s);
+
+/* Sampler.sample for one row.  `logits` may be host or device memory
+ * (length n); `prev_tokens` is host memory (may be NULL when n_prev == 0).
+ * Synchronous: returns after *token is written.  The PRNG advances by one
+ * Random.float(f32) only when the row reaches the draw, exactly as
+ * sampler.zig:162. */
+int llz_sampler_sample(llz_sampler *s, const float *logits, int32_t n,
+                       const uint32_t *prev_tokens, int32_t n_prev, uint32_t *token);
+
+/* PRNG state snapshot / restore (checkpointing a generation). */
+void llz_sampler_get_state(const llz_sampler *s, uint64_t state[4]);
+void llz_sampler_set_state(llz_sampler *s, const uint64_t state[4]);
+
+/* Test hook (no counterpart in the reference): evaluates the device's f32
+ * exp and log -- the functions the kernels use in place of std.math.exp and
+ * @log (sampler.zig:85,131,136) -- on n inputs.  d_exp / d_log may be NULL.
+ * Used by the parity tests to compare the GPU math with the CPU oracle. */
+int llz_debug_math(const float *d_in, float *d_exp, float *d_log, int64_t n, void *stream);
+
+/* Measurement hook (no counterpart in the reference): while set, every
+ * llz_sample_rows call records `begin_event` right before and `end_event`
+ * right after its per-row sampling kernel, on the call's stream (both are
+ * hipEvent_t).  NULL, NULL clears.  Process-wide, not thread-safe; used by
+ * the benchmark to time the dominant kernel alone. */
+int llz_debug_kernel_events(void *begin_event, void *end_event);
+
+/* Name of a return code. */
+const char *llz_strerror(int code);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLZ_SAMPLER_H */

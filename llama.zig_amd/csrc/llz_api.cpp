@@ -1,0 +1,392 @@
+// llz_api.cpp -- C ABI of libllzsample.so (declared in include/llz_sampler.h).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+
+#include "../../include/llz_sampler.h"
+#include "llz_internal.h"
+
+using namespace llz;
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+// measurement hook: events recorded around k_sample (see llz_debug_kernel_events)
+hipEvent_t g_ev_begin = nullptr;
+hipEvent_t g_ev_end = nullptr;
+
+bool penalty_active(const llz_sampler_config* cfg, int32_t n_prev) {
+  return cfg->repetition_penalty != 1.0f && n_prev > 0 && cfg->repetition_window > 0;
+}
+
+// Workspace layout of one llz_sample_rows call.
+struct Layout {
+  size_t maxpart, status, penal, fb, fb_mask, total;
+  bool has_penal;
+};
+
+Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int32_t n_prev) {
+  Layout L{};
+  const size_t r = (size_t)rows, n = (size_t)vocab;
+  size_t off = 0;
+  L.maxpart = off; off = align_up(off + r * (size_t)max_parts(vocab) * sizeof(float));
+  L.status = off;  off = align_up(off + r * sizeof(uint32_t));
+  L.has_penal = penalty_active(cfg, n_prev);
+  L.penal = off;   if (L.has_penal) off = align_up(off + r * n * sizeof(float));
+  L.fb = off;      off = align_up(off + 6 * r * n * sizeof(uint32_t));
+  L.fb_mask = off; off = align_up(off + r * n);
+  L.total = off;
+  return L;
+}
+
+// Candidate threshold on e = exp((v - max) / T).  Every element that can be
+// kept must satisfy e >= theta, or the row takes the full fallback.
+float candidate_theta(const llz_sampler_config* cfg, int32_t vocab) {
+  if (vocab <= kCandCap) return 0.0f;  // the whole row fits the list
+  float theta = 0x1p-16f;
+  if (cfg->min_p > 0.0f) {
+    // p < RN(RN(1/S) * min_p) for every e < min_p * (1 - 2^-20)
+    theta = (float)((double)cfg->min_p * (1.0 - 0x1p-20));
+    theta = std::nextafter(theta, 0.0f);
+  }
+  // the row maximum (e == 1) and its probability ties must stay certified
+  if (!(theta <= 0.5f)) theta = 0.5f;
+  return theta;
+}
+
+int check_common(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab) {
+  if (!d_logits || rows <= 0 || vocab <= 0 || row_stride < vocab) return LLZ_E_INVALID_ARG;
+  return LLZ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void llz_sampler_config_default(llz_sampler_config* cfg) {
+  if (!cfg) return;
+  std::memset(cfg, 0, sizeof(*cfg));
+  cfg->temperature = 0.8f;
+  cfg->top_k = 0;
+  cfg->top_p = 0.9f;
+  cfg->min_p = 0.0f;
+  cfg->typical_p = 1.0f;
+  cfg->seed = 0;
+  cfg->repetition_window = 32;
+  cfg->repetition_penalty = 1.1f;
+}
+
+const char* llz_strerror(int code) {
+  switch (code) {
+    case LLZ_OK: return "ok";
+    case LLZ_E_INVALID_ARG: return "invalid argument";
+    case LLZ_E_WORKSPACE: return "workspace missing or too small";
+    case LLZ_E_HIP: return "HIP runtime error";
+    case LLZ_E_OOM: return "out of memory";
+    case LLZ_E_NO_DEVICE: return "no HIP device";
+    default: return "unknown error";
+  }
+}
+
+size_t llz_sample_workspace_bytes(int32_t rows, int32_t vocab, const llz_sampler_config* cfg,
+                                  int32_t n_prev) {
+  if (!cfg || rows <= 0 || vocab <= 0 || n_prev < 0) return 0;
+  return layout_of(rows, vocab, cfg, n_prev).total;
+}
+
+int llz_argmax_rows(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                    uint32_t* d_tokens, void* stream) {
+  int rc = check_common(d_logits, row_stride, rows, vocab);
+  if (rc) return rc;
+  if (!d_tokens) return LLZ_E_INVALID_ARG;
+  hipError_t e = launch_argmax(d_logits, row_stride, rows, vocab, d_tokens, nullptr, nullptr,
+                               (hipStream_t)stream);
+  return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
+}
+
+int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                    const llz_sampler_config* cfg, const uint32_t* d_prev_tokens, int32_t n_prev,
+                    int64_t prev_stride, const float* d_uniforms, uint32_t* d_tokens,
+                    uint8_t* d_consumed, const llz_sample_extras* extras, void* d_workspace,
+                    size_t workspace_bytes, void* stream) {
+  int rc = check_common(d_logits, row_stride, rows, vocab);
+  if (rc) return rc;
+  if (!cfg || !d_tokens || n_prev < 0 || prev_stride < 0) return LLZ_E_INVALID_ARG;
+  if (cfg->temperature != cfg->temperature) return LLZ_E_INVALID_ARG;  // NaN
+  if (n_prev > 0 && !d_prev_tokens) return LLZ_E_INVALID_ARG;
+  if (extras && (extras->d_kept_ids || extras->d_kept_probs) && extras->kept_cap <= 0)
+    return LLZ_E_INVALID_ARG;
+  hipStream_t st = (hipStream_t)stream;
+
+  // sampler.zig:50 -- greedy rows never draw
+  if (cfg->temperature <= 0.0f) {
+    hipError_t e = launch_argmax(d_logits, row_stride, rows, vocab, d_tokens, d_consumed,
+                                 extras ? extras->d_kept_count : nullptr, st);
+    return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
+  }
+  if (!d_uniforms) return LLZ_E_INVALID_ARG;
+  if (penalty_active(cfg, n_prev) && cfg->repetition_penalty != cfg->repetition_penalty)
+    return LLZ_E_INVALID_ARG;
+
+  const Layout L = layout_of(rows, vocab, cfg, n_prev);
+  if (!d_workspace || workspace_bytes < L.total) return LLZ_E_WORKSPACE;
+  char* ws = (char*)d_workspace;
+
+  const float* src = d_logits;
+  int64_t src_stride = row_stride;
+  if (L.has_penal) {
+    float* pen = (float*)(ws + L.penal);
+    hipError_t e = launch_penalty(d_logits, row_stride, rows, vocab, d_prev_tokens, n_prev, prev_stride,
+                                  (int)cfg->repetition_window, cfg->repetition_penalty, pen, st);
+    if (e != hipSuccess) return LLZ_E_HIP;
+    src = pen;
+    src_stride = vocab;
+  }
+  const bool vec = ((uintptr_t)src % 16 == 0) && (src_stride % 4 == 0);
+  float* maxpart = (float*)(ws + L.maxpart);
+  hipError_t e = launch_rowmax(src, src_stride, rows, vocab, vec, maxpart, st);
+  if (e != hipSuccess) return LLZ_E_HIP;
+
+  RowParams P{};
+  P.temperature = cfg->temperature;
+  P.top_p = cfg->top_p;
+  P.min_p = cfg->min_p;
+  P.typical_p = cfg->typical_p;
+  P.top_k = cfg->top_k;
+  P.cand_theta = candidate_theta(cfg, vocab);
+  P.n = vocab;
+  P.rows = rows;
+  P.nparts = max_parts(vocab);
+  P.kept_cap = extras ? extras->kept_cap : 0;
+  P.src_stride = src_stride;
+  P.orig_stride = row_stride;
+  P.flags = (cfg->temperature == 1.0f ? kFlagTIsOne : 0u) | (vec ? kFlagVecSrc : 0u) | kFlagFallback;
+
+  RowPtrs Q{};
+  Q.src = src;
+  Q.orig = d_logits;
+  Q.maxpart = maxpart;
+  Q.uniforms = d_uniforms;
+  Q.tokens = d_tokens;
+  Q.consumed = d_consumed;
+  if (extras) {
+    Q.kept_count = extras->d_kept_count;
+    Q.kept_ids = extras->d_kept_ids;
+    Q.kept_probs = extras->d_kept_probs;
+    Q.row_stats = extras->d_row_stats;
+  }
+  Q.status = (uint32_t*)(ws + L.status);
+  Q.fb = (uint32_t*)(ws + L.fb);
+  Q.fb_mask = (uint8_t*)(ws + L.fb_mask);
+  if (g_ev_begin && hipEventRecord(g_ev_begin, st) != hipSuccess) return LLZ_E_HIP;
+  e = launch_sample(P, Q, st);
+  if (e != hipSuccess) return LLZ_E_HIP;
+  if (g_ev_end && hipEventRecord(g_ev_end, st) != hipSuccess) return LLZ_E_HIP;
+  return LLZ_OK;
+}
+
+int llz_debug_kernel_events(void* begin_event, void* end_event) {
+  g_ev_begin = (hipEvent_t)begin_event;
+  g_ev_end = (hipEvent_t)end_event;
+  return LLZ_OK;
+}
+
+int llz_debug_math(const float* d_in, float* d_exp, float* d_log, int64_t n, void* stream) {
+  if (!d_in || n < 0 || n > ((int64_t)1 << 40)) return LLZ_E_INVALID_ARG;
+  if (n == 0) return LLZ_OK;
+  hipError_t e = launch_math_probe(d_in, d_exp, d_log, n, (hipStream_t)stream);
+  return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
+}
+
+// ---------------------------------------------------------------------------
+// The reference's PRNG: std.Random.DefaultPrng (xoshiro256++) seeded through
+// SplitMix64, and Random.float(f32) (sampler.zig:17,22,162).
+// ---------------------------------------------------------------------------
+static uint64_t splitmix_next(uint64_t& x) {
+  x += 0x9e3779b97f4a7c15ull;
+  uint64_t z = x;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+void llz_rng_seed(uint64_t state[4], uint64_t seed) {
+  uint64_t x = seed;
+  for (int i = 0; i < 4; ++i) state[i] = splitmix_next(x);
+}
+
+uint64_t llz_rng_next(uint64_t state[4]) {
+  auto rotl = [](uint64_t v, int k) { return (v << k) | (v >> (64 - k)); };
+  const uint64_t out = rotl(state[0] + state[3], 23) + state[0];
+  const uint64_t t = state[1] << 17;
+  state[2] ^= state[0];
+  state[3] ^= state[1];
+  state[1] ^= state[2];
+  state[0] ^= state[3];
+  state[2] ^= t;
+  state[3] = rotl(state[3], 45);
+  return out;
+}
+
+float llz_rng_float(uint64_t state[4]) {
+  // 23 uniform mantissa bits; exponent from the count of leading zero bits
+  // of the same draw (extended with further draws when 41 or more are zero)
+  const uint64_t r = llz_rng_next(state);
+  int lz = r ? __builtin_clzll(r) : 64;
+  if (lz >= 41) {
+    const uint64_t r2 = llz_rng_next(state);
+    lz = 41 + (r2 ? __builtin_clzll(r2) : 64);
+    if (lz == 41 + 64) lz += __builtin_clz((uint32_t)llz_rng_next(state) | 0x7ffu);
+  }
+  const uint32_t bits = ((uint32_t)(126 - lz) << 23) | (uint32_t)(r & 0x7fffffu);
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+void llz_rng_uniforms(uint64_t state[4], float* out, int64_t count) {
+  for (int64_t i = 0; i < count; ++i) out[i] = llz_rng_float(state);
+}
+
+// ---------------------------------------------------------------------------
+// Host-side Sampler (sampler.zig:15-28).
+// ---------------------------------------------------------------------------
+struct llz_sampler {
+  llz_sampler_config cfg;
+  uint64_t prng[4];
+  int device;
+  hipStream_t stream;
+  int32_t cap_n;       // capacity (vocab) of the buffers below
+  int32_t cap_prev;
+  float* d_logits;     // staging for host logits
+  uint32_t* d_prev;
+  float* d_u;
+  uint32_t* d_token;
+  uint8_t* d_consumed;
+  void* d_ws;
+  size_t ws_bytes;
+};
+
+static void sampler_free_buffers(llz_sampler* s) {
+  (void)hipFree(s->d_logits);
+  (void)hipFree(s->d_prev);
+  (void)hipFree(s->d_u);
+  (void)hipFree(s->d_token);
+  (void)hipFree(s->d_consumed);
+  (void)hipFree(s->d_ws);
+  s->d_logits = nullptr; s->d_prev = nullptr; s->d_u = nullptr; s->d_token = nullptr;
+  s->d_consumed = nullptr; s->d_ws = nullptr; s->ws_bytes = 0; s->cap_n = 0; s->cap_prev = 0;
+}
+
+int llz_sampler_create(const llz_sampler_config* cfg, int32_t device, llz_sampler** out) {
+  if (!cfg || !out) return LLZ_E_INVALID_ARG;
+  if (cfg->temperature != cfg->temperature) return LLZ_E_INVALID_ARG;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) {
+    (void)hipGetLastError();
+    return LLZ_E_NO_DEVICE;
+  }
+  if (device < 0 || device >= ndev) return LLZ_E_INVALID_ARG;
+  llz_sampler* s = new (std::nothrow) llz_sampler();
+  if (!s) return LLZ_E_OOM;
+  s->cfg = *cfg;
+  llz_rng_seed(s->prng, cfg->seed != 0 ? cfg->seed : 0xDEADBEEFull);
+  s->device = device;
+  if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&s->stream) != hipSuccess) {
+    delete s;
+    return LLZ_E_HIP;
+  }
+  *out = s;
+  return LLZ_OK;
+}
+
+void llz_sampler_destroy(llz_sampler* s) {
+  if (!s) return;
+  (void)hipSetDevice(s->device);
+  sampler_free_buffers(s);
+  (void)hipStreamDestroy(s->stream);
+  delete s;
+}
+
+void llz_sampler_get_state(const llz_sampler* s, uint64_t state[4]) {
+  if (s && state) std::memcpy(state, s->prng, sizeof(s->prng));
+}
+
+void llz_sampler_set_state(llz_sampler* s, const uint64_t state[4]) {
+  if (s && state) std::memcpy(s->prng, state, sizeof(s->prng));
+}
+
+static bool is_device_ptr(const void* p) {
+  hipPointerAttribute_t a;
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return a.type == hipMemoryTypeDevice;
+}
+
+int llz_sampler_sample(llz_sampler* s, const float* logits, int32_t n, const uint32_t* prev_tokens,
+                       int32_t n_prev, uint32_t* token) {
+  if (!s || !logits || n <= 0 || !token || n_prev < 0 || (n_prev > 0 && !prev_tokens))
+    return LLZ_E_INVALID_ARG;
+  if (hipSetDevice(s->device) != hipSuccess) return LLZ_E_HIP;
+  const size_t need_ws = llz_sample_workspace_bytes(1, n, &s->cfg, n_prev);
+  if (n > s->cap_n || n_prev > s->cap_prev || need_ws > s->ws_bytes) {
+    sampler_free_buffers(s);
+    const int32_t cn = n, cp = n_prev > 0 ? n_prev : 1;
+    if (hipMalloc(&s->d_logits, (size_t)cn * sizeof(float)) != hipSuccess ||
+        hipMalloc(&s->d_prev, (size_t)cp * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc(&s->d_u, sizeof(float)) != hipSuccess ||
+        hipMalloc(&s->d_token, sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc(&s->d_consumed, 1) != hipSuccess ||
+        hipMalloc(&s->d_ws, need_ws) != hipSuccess) {
+      sampler_free_buffers(s);
+      return LLZ_E_OOM;
+    }
+    s->cap_n = cn;
+    s->cap_prev = cp;
+    s->ws_bytes = need_ws;
+  }
+  // draw as if the row reached sampler.zig:162; undo below if it did not
+  uint64_t snap[4];
+  std::memcpy(snap, s->prng, sizeof(snap));
+  const float u = llz_rng_float(s->prng);
+
+  const float* d_in = logits;
+  if (!is_device_ptr(logits)) {
+    if (hipMemcpyAsync(s->d_logits, logits, (size_t)n * sizeof(float), hipMemcpyHostToDevice,
+                       s->stream) != hipSuccess)
+      return LLZ_E_HIP;
+    d_in = s->d_logits;
+  }
+  if (n_prev > 0 && hipMemcpyAsync(s->d_prev, prev_tokens, (size_t)n_prev * sizeof(uint32_t),
+                                   hipMemcpyHostToDevice, s->stream) != hipSuccess)
+    return LLZ_E_HIP;
+  if (hipMemcpyAsync(s->d_u, &u, sizeof(float), hipMemcpyHostToDevice, s->stream) != hipSuccess)
+    return LLZ_E_HIP;
+  int rc = llz_sample_rows(d_in, n, 1, n, &s->cfg, n_prev > 0 ? s->d_prev : nullptr, n_prev, 0,
+                           s->d_u, s->d_token, s->d_consumed, nullptr, s->d_ws, s->ws_bytes,
+                           s->stream);
+  if (rc != LLZ_OK) {
+    std::memcpy(s->prng, snap, sizeof(snap));
+    return rc;
+  }
+  uint32_t tok = 0;
+  uint8_t consumed = 0;
+  if (hipMemcpyAsync(&tok, s->d_token, sizeof(tok), hipMemcpyDeviceToHost, s->stream) != hipSuccess ||
+      hipMemcpyAsync(&consumed, s->d_consumed, 1, hipMemcpyDeviceToHost, s->stream) != hipSuccess ||
+      hipStreamSynchronize(s->stream) != hipSuccess) {
+    std::memcpy(s->prng, snap, sizeof(snap));
+    return LLZ_E_HIP;
+  }
+  if (!consumed || s->cfg.temperature <= 0.0f) std::memcpy(s->prng, snap, sizeof(snap));
+  *token = tok;
+  return LLZ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,120 @@
+// llz_exact.h -- exact, parallel emulation of a sequential f32 accumulation.
+//
+// The reference sampler accumulates in f32, one term at a time, in a fixed
+// order (src/sampler.zig:83-88 normaliser, :112-117 top-p, :129-132 entropy,
+// :148-153 typical cum, :156-159 total, :162-166 the draw).  Summing the same
+// terms "more accurately" in parallel changes the result, so the kernels
+// reproduce the sequential rounding exactly:
+//
+//   While the running value s stays in one binade [2^j, 2^(j+1)) its grid is
+//   u = 2^(j-23), s = N*u with N an integer, and fl(s + x) = (N + RN(x/u))*u
+//   unless x/u is an exact half-integer (a tie, resolved by the parity of
+//   the running N) or the result leaves the binade.  Between such events the
+//   accumulation is an integer sum of per-term roundings, which is
+//   associative.  Each tile is therefore summed with one workgroup
+//   reduction; only tiles containing an event take a slower path that
+//   locates the first event with a prefix scan, performs that single f32
+//   operation literally, and continues with the new grid.
+//
+// The subtractive chain of the draw (r -= p, stop at r <= 0) uses the same
+// grid argument downwards: events are ties and results at or below the
+// binade's base.
+#pragma once
+
+#include <stdint.h>
+
+#ifdef __HIPCC__
+#include <hip/hip_runtime.h>
+#define LLZ_HD __host__ __device__ __forceinline__
+#else
+#include <string.h>
+#define LLZ_HD static inline
+#endif
+
+namespace llz {
+
+constexpr uint32_t kGridTop = 1u << 24;  // N reaching this leaves the binade (add)
+constexpr uint32_t kGridBase = 1u << 23; // N at or below this leaves it (subtract)
+constexpr uint32_t kSat = 1u << 25;      // saturation cap for rounded terms / sums
+
+LLZ_HD uint32_t as_bits(float f) {
+#ifdef __HIPCC__
+  return __float_as_uint(f);
+#else
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+#endif
+}
+LLZ_HD float as_float(uint32_t u) {
+#ifdef __HIPCC__
+  return __uint_as_float(u);
+#else
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+#endif
+}
+
+// Grid of a running value s >= 0: j = max(exponent(s), -126) and
+// N = s / 2^(j-23) (exact).  Zero and subnormals share the grid 2^-149.
+struct Grid {
+  int j;
+  uint32_t N;
+};
+
+LLZ_HD Grid grid_of(float s) {
+  const uint32_t b = as_bits(s) & 0x7fffffffu;
+  const uint32_t E = b >> 23;
+  Grid g;
+  g.j = (int)(E == 0 ? 1u : E) - 127;
+  g.N = E == 0 ? (b & 0x7fffffu) : ((b & 0x7fffffu) | 0x800000u);
+  return g;
+}
+
+// 2^(j-23) as a float (j >= -126, so the value is >= 2^-149).
+LLZ_HD float grid_ulp(int j) {
+  const int e = j - 23;
+  return e >= -126 ? as_float((uint32_t)(e + 127) << 23) : as_float(1u << (e + 149));
+}
+
+// N * 2^(j-23) as a float; exact for N < 2^24 (or a subnormal on the grid).
+LLZ_HD float grid_value(uint32_t N, int j) { return (float)N * grid_ulp(j); }
+
+// RN(x / 2^(j-23)) for a finite x >= 0 (sign bit ignored), saturated at
+// kSat, and whether x / 2^(j-23) is an exact half-integer (a tie).
+LLZ_HD uint32_t grid_round(float x, int j, bool& tie) {
+  const uint32_t b = as_bits(x) & 0x7fffffffu;
+  const uint32_t XE = b >> 23;
+  const uint32_t m = XE == 0 ? (b & 0x7fffffu) : ((b & 0x7fffffu) | 0x800000u);
+  const int xe = (int)(XE == 0 ? 1u : XE) - 127;  // x = m * 2^(xe-23)
+  const int d = j - xe;
+  tie = false;
+  if (d <= 0) {
+    if (d == 0) return m;
+    return m == 0 ? 0u : kSat;  // x >= 2^(j+1): leaves the binade on its own
+  }
+  if (d >= 25) return 0u;  // x < 2^(j-24) = u/2, strictly
+  const uint32_t q = m >> d;
+  const uint32_t rem = m & ((1u << d) - 1u);
+  const uint32_t half = 1u << (d - 1);
+  tie = rem == half;
+  return q + (rem > half ? 1u : 0u);
+}
+
+// Largest integer T with T * 2^(j-23) <= thr, or 0xffffffff when thr is at
+// or above 2^(j+1) (the running value cannot exceed it inside the binade).
+// thr >= 0.
+LLZ_HD uint32_t grid_floor(float thr, int j) {
+  const float top = (j + 1 <= 127) ? as_float((uint32_t)(j + 1 + 127) << 23) : 3.0e38f;
+  if (!(thr < top)) return 0xffffffffu;
+  // thr / u < 2^24: scale by an exact power of two, then truncate
+  const int e = 23 - j;  // thr * 2^e
+  float scaled = thr;
+  int k = e;
+  while (k > 100) { scaled *= 0x1p100f; k -= 100; }
+  scaled *= as_float((uint32_t)(k + 127) << 23);
+  return (uint32_t)scaled;  // scaled >= 0, < 2^24: truncation == floor
+}
+
+}  // namespace llz

@@ -1,0 +1,66 @@
+// llz_internal.h -- types shared by the kernels and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llz {
+
+constexpr int kCandCap = 2048;  // candidate list capacity per row (power of two)
+
+// RowParams.flags
+constexpr uint32_t kFlagTIsOne = 1u;    // temperature == 1.0f exactly: (v - m) / T == v - m
+constexpr uint32_t kFlagVecSrc = 2u;    // 16-byte loads are legal on the rows the chain reads
+constexpr uint32_t kFlagFallback = 4u;  // the full-row fallback buffers are present
+
+// per-row status bits (diagnostics)
+constexpr uint32_t kPathSumLe0 = 1u;
+constexpr uint32_t kPathEntropy = 2u;
+constexpr uint32_t kPathFallback = 4u;
+constexpr uint32_t kPathError = 0x80000000u;
+
+struct RowParams {
+  float temperature;
+  float top_p;
+  float min_p;
+  float typical_p;
+  uint32_t top_k;
+  float cand_theta;   // e >= cand_theta enters the candidate list
+  int32_t n;          // vocab
+  int32_t rows;
+  int32_t nparts;     // partial maxima per row
+  int32_t kept_cap;
+  int64_t src_stride;
+  int64_t orig_stride;
+  uint32_t flags;
+  uint32_t pad;
+};
+
+struct RowPtrs {
+  const float* src;       // rows the chain reads (penalised copy or the caller's)
+  const float* orig;      // the caller's rows (sampleArgmax exits)
+  const float* maxpart;   // [rows][nparts]
+  const float* uniforms;  // [rows]
+  uint32_t* tokens;
+  uint8_t* consumed;
+  uint32_t* kept_count;
+  uint32_t* kept_ids;
+  float* kept_probs;
+  float* row_stats;
+  uint32_t* status;
+  uint32_t* fb;           // 6 x [rows][n] u32 (fallback sort buffers)
+  uint8_t* fb_mask;       // [rows][n]
+};
+
+int max_parts(int n);
+hipError_t launch_penalty(const float* logits, int64_t stride, int rows, int n, const uint32_t* prev,
+                          int n_prev, int64_t prev_stride, int window, float penalty, float* out,
+                          hipStream_t st);
+hipError_t launch_rowmax(const float* logits, int64_t stride, int rows, int n, bool vec, float* part,
+                         hipStream_t st);
+hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t* tokens,
+                         uint8_t* consumed, uint32_t* kept_count, hipStream_t st);
+hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipStream_t st);
+hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, int64_t n, hipStream_t st);
+
+}  // namespace llz

@@ -1,0 +1,122 @@
+// llz_math.h -- bit-exact f32 exp/log for the sampling kernels.
+//
+// The reference sampler computes std.math.exp (src/sampler.zig:85) and @log
+// (src/sampler.zig:131,136) in f32.  Zig lowers both to its compiler_rt
+// expf/logf, which implement the FreeBSD msun e_expf.c / e_logf.c algorithms
+// (Sun Microsystems 1993; musl <= 1.1.19 carries the same control flow).
+// These device functions follow those published algorithms operation for
+// operation.  Each f32 operation must round exactly once, so every file that
+// includes this header is compiled with -ffp-contract=off, f32 denormals on,
+// and IEEE (correctly rounded) division.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llz {
+
+__device__ __forceinline__ uint32_t fbits(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float bitsf(uint32_t u) { return __uint_as_float(u); }
+
+// RN(y * 2^k): two exact power-of-two steps, then one rounding multiply.
+__device__ __forceinline__ float scale_pow2(float y, int k) {
+  if (k > 127) {
+    y *= 0x1p127f;
+    k -= 127;
+    if (k > 127) {
+      y *= 0x1p127f;
+      k -= 127;
+      if (k > 127) k = 127;
+    }
+  } else if (k < -126) {
+    y *= 0x1p-102f;
+    k += 102;
+    if (k < -126) {
+      y *= 0x1p-102f;
+      k += 102;
+      if (k < -126) k = -126;
+    }
+  }
+  return y * bitsf((uint32_t)(0x7f + k) << 23);
+}
+
+// exp(x) for f32, e_expf.c algorithm: reduce x = k ln2 + r with a two-part
+// ln2, evaluate the degree-2 rational approximation of r, scale by 2^k.
+__device__ __forceinline__ float exp_f32(float x) {
+  const float ln2hi = 6.9314575195e-1f;   // 0x3f317200
+  const float ln2lo = 1.4286067653e-6f;   // 0x35bfbe8e
+  const float invln2 = 1.4426950216e+0f;  // 0x3fb8aa3b
+  const float P1 = 1.6666625440e-1f;      // 0x3e2aaa8f
+  const float P2 = -2.7667332906e-3f;     // 0xbb355215
+
+  uint32_t hx = fbits(x);
+  const int sign = (int)(hx >> 31);
+  hx &= 0x7fffffffu;
+  if (hx >= 0x42aeac50u) {                // |x| >= 87.33655, inf or NaN
+    if (hx > 0x7f800000u) return x;        // NaN
+    if (hx >= 0x42b17218u && !sign) return x * 0x1p127f;  // overflow
+    if (sign && hx >= 0x42cff1b5u) return 0.0f;           // underflow to 0
+  }
+  float hi, lo;
+  int k;
+  if (hx > 0x3eb17218u) {                 // |x| > ln2/2
+    if (hx > 0x3f851592u)                  // |x| > 1.5 ln2
+      k = (int)(invln2 * x + (sign ? -0.5f : 0.5f));
+    else
+      k = 1 - sign - sign;
+    hi = x - (float)k * ln2hi;
+    lo = (float)k * ln2lo;
+    x = hi - lo;
+  } else if (hx > 0x39000000u) {          // |x| > 2^-13
+    k = 0;
+    hi = x;
+    lo = 0.0f;
+  } else {
+    return 1.0f + x;
+  }
+  const float xx = x * x;
+  const float c = x - xx * (P1 + xx * P2);
+  const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
+  return k == 0 ? y : scale_pow2(y, k);
+}
+
+// log(x) for f32, e_logf.c algorithm: x = 2^k (1+f) with 1+f in
+// [sqrt(2)/2, sqrt(2)), log(1+f) = f - hfsq + s (hfsq + R(z)).
+__device__ __forceinline__ float log_f32(float x) {
+  const float ln2_hi = 6.9313812256e-01f;  // 0x3f317180
+  const float ln2_lo = 9.0580006145e-06f;  // 0x3717f7d1
+  const float Lg1 = 0xaaaaaa.0p-24f;
+  const float Lg2 = 0xccce13.0p-25f;
+  const float Lg3 = 0x91e9ee.0p-25f;
+  const float Lg4 = 0xf89e26.0p-26f;
+
+  uint32_t ix = fbits(x);
+  int k = 0;
+  if (ix < 0x00800000u || (ix >> 31)) {
+    if ((ix << 1) == 0) return -__builtin_inff();
+    if (ix >> 31) return __builtin_nanf("");
+    k -= 25;
+    x *= 0x1p25f;
+    ix = fbits(x);
+  } else if (ix >= 0x7f800000u) {
+    return x;
+  } else if (ix == 0x3f800000u) {
+    return 0.0f;
+  }
+  ix += 0x3f800000u - 0x3f3504f3u;
+  k += (int)(ix >> 23) - 0x7f;
+  ix = (ix & 0x007fffffu) + 0x3f3504f3u;
+  x = bitsf(ix);
+  const float f = x - 1.0f;
+  const float s = f / (2.0f + f);
+  const float z = s * s;
+  const float w = z * z;
+  const float t1 = w * (Lg2 + w * Lg4);
+  const float t2 = z * (Lg1 + w * Lg3);
+  const float R = t2 + t1;
+  const float hfsq = 0.5f * f * f;
+  const float dk = (float)k;
+  return s * (hfsq + R) + dk * ln2_lo - hfsq + f + dk * ln2_hi;
+}
+
+}  // namespace llz

@@ -1,0 +1,344 @@
+"""Python binding of libllzsample.so, the MI355X sampler for llama.zig.
+
+The names mirror the reference's sampler API (src/sampler.zig):
+
+* ``SamplerConfig``  -- SamplerConfig (sampler.zig:4-13), same defaults;
+* ``Sampler``        -- Sampler.init / Sampler.sample (sampler.zig:15-28), with
+  the reference's PRNG lifecycle (seed fallback 0xDEADBEEF, one stream, a
+  draw consumed only when the row reaches sampler.zig:162);
+* ``sample_argmax``  -- sampleArgmax (sampler.zig:31-41);
+* ``sample_rows``    -- the batched device entry point behind them.
+
+Device memory and streams come from PyTorch (plumbing only); every compute
+call goes through the C ABI declared in include/llz_sampler.h.  There is no
+CPU fallback: a missing or unloadable library raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+import os
+from typing import Optional, Tuple
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "libllzsample.so")
+
+LLZ_OK = 0
+LLZ_E_INVALID_ARG = -1
+LLZ_E_WORKSPACE = -2
+LLZ_E_HIP = -3
+LLZ_E_OOM = -4
+LLZ_E_NO_DEVICE = -5
+
+# Public symbols of include/llz_sampler.h.
+EXPORTED = (
+    "llz_sampler_config_default", "llz_sample_workspace_bytes", "llz_sample_rows",
+    "llz_argmax_rows", "llz_rng_seed", "llz_rng_next", "llz_rng_float", "llz_rng_uniforms",
+    "llz_sampler_create", "llz_sampler_destroy", "llz_sampler_sample", "llz_sampler_get_state",
+    "llz_sampler_set_state", "llz_debug_math", "llz_debug_kernel_events", "llz_strerror",
+)
+
+
+class LlzError(RuntimeError):
+    def __init__(self, code: int, what: str = ""):
+        self.code = code
+        msg = _lib().llz_strerror(code).decode() if _LIB is not None else str(code)
+        super().__init__(f"{what}: {msg} ({code})" if what else f"{msg} ({code})")
+
+
+class CConfig(C.Structure):
+    _fields_ = [
+        ("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
+        ("min_p", C.c_float), ("typical_p", C.c_float), ("repetition_window", C.c_uint32),
+        ("repetition_penalty", C.c_float), ("reserved", C.c_uint32), ("seed", C.c_uint64),
+    ]
+
+
+class CExtras(C.Structure):
+    _fields_ = [
+        ("d_kept_count", C.c_void_p), ("d_kept_ids", C.c_void_p), ("d_kept_probs", C.c_void_p),
+        ("kept_cap", C.c_int32), ("reserved", C.c_int32), ("d_row_stats", C.c_void_p),
+    ]
+
+
+@dataclasses.dataclass
+class SamplerConfig:
+    """SamplerConfig (src/sampler.zig:4-13), same field names and defaults."""
+
+    temperature: float = 0.8
+    top_k: int = 0
+    top_p: float = 0.9
+    min_p: float = 0.0
+    typical_p: float = 1.0
+    seed: int = 0
+    repetition_window: int = 32
+    repetition_penalty: float = 1.1
+
+    def to_c(self) -> CConfig:
+        return CConfig(float(self.temperature), int(self.top_k), float(self.top_p),
+                       float(self.min_p), float(self.typical_p), int(self.repetition_window),
+                       float(self.repetition_penalty), 0, int(self.seed))
+
+    @classmethod
+    def of(cls, params, seed: int = 0) -> "SamplerConfig":
+        return cls(params.temperature, params.top_k, params.top_p, params.min_p, params.typical_p,
+                   seed, params.repetition_window, params.repetition_penalty)
+
+
+_LIB = None
+
+
+def _lib():
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        vp, i32, i64, u64 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64
+        L.llz_sampler_config_default.argtypes = [C.POINTER(CConfig)]
+        L.llz_sampler_config_default.restype = None
+        L.llz_sample_workspace_bytes.argtypes = [i32, i32, C.POINTER(CConfig), i32]
+        L.llz_sample_workspace_bytes.restype = C.c_size_t
+        L.llz_sample_rows.argtypes = [vp, i64, i32, i32, C.POINTER(CConfig), vp, i32, i64, vp, vp,
+                                      vp, C.POINTER(CExtras), vp, C.c_size_t, vp]
+        L.llz_sample_rows.restype = C.c_int
+        L.llz_argmax_rows.argtypes = [vp, i64, i32, i32, vp, vp]
+        L.llz_argmax_rows.restype = C.c_int
+        L.llz_rng_seed.argtypes = [C.POINTER(u64), u64]
+        L.llz_rng_seed.restype = None
+        L.llz_rng_next.argtypes = [C.POINTER(u64)]
+        L.llz_rng_next.restype = u64
+        L.llz_rng_float.argtypes = [C.POINTER(u64)]
+        L.llz_rng_float.restype = C.c_float
+        L.llz_rng_uniforms.argtypes = [C.POINTER(u64), C.POINTER(C.c_float), i64]
+        L.llz_rng_uniforms.restype = None
+        L.llz_sampler_create.argtypes = [C.POINTER(CConfig), i32, C.POINTER(vp)]
+        L.llz_sampler_create.restype = C.c_int
+        L.llz_sampler_destroy.argtypes = [vp]
+        L.llz_sampler_destroy.restype = None
+        L.llz_sampler_sample.argtypes = [vp, vp, i32, C.POINTER(C.c_uint32), i32,
+                                         C.POINTER(C.c_uint32)]
+        L.llz_sampler_sample.restype = C.c_int
+        L.llz_sampler_get_state.argtypes = [vp, C.POINTER(u64)]
+        L.llz_sampler_get_state.restype = None
+        L.llz_sampler_set_state.argtypes = [vp, C.POINTER(u64)]
+        L.llz_sampler_set_state.restype = None
+        L.llz_debug_math.argtypes = [vp, vp, vp, i64, vp]
+        L.llz_debug_math.restype = C.c_int
+        L.llz_debug_kernel_events.argtypes = [vp, vp]
+        L.llz_debug_kernel_events.restype = C.c_int
+        L.llz_strerror.argtypes = [C.c_int]
+        L.llz_strerror.restype = C.c_char_p
+        _LIB = L
+    return _LIB
+
+
+def library():
+    """The loaded ctypes library (raises if it is not built)."""
+    return _lib()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != LLZ_OK:
+        raise LlzError(rc, what)
+
+
+# ---------------------------------------------------------------------------
+# the reference's PRNG (std.Random.DefaultPrng + Random.float(f32))
+# ---------------------------------------------------------------------------
+class Prng:
+    """Xoshiro256 seeded through SplitMix64 (sampler.zig:22)."""
+
+    def __init__(self, seed: int):
+        self.state = (C.c_uint64 * 4)()
+        _lib().llz_rng_seed(self.state, C.c_uint64(seed))
+
+    def next_u64(self) -> int:
+        return int(_lib().llz_rng_next(self.state))
+
+    def float32(self) -> np.float32:
+        return np.float32(_lib().llz_rng_float(self.state))
+
+    def uniforms(self, count: int) -> np.ndarray:
+        out = np.empty(count, np.float32)
+        _lib().llz_rng_uniforms(self.state, out.ctypes.data_as(C.POINTER(C.c_float)), count)
+        return out
+
+
+def rng_uniforms(seed: int, count: int) -> np.ndarray:
+    """count successive Random.float(f32) draws from DefaultPrng.init(seed)."""
+    return Prng(seed).uniforms(count)
+
+
+# ---------------------------------------------------------------------------
+# device entry points (torch tensors are only the memory holders)
+# ---------------------------------------------------------------------------
+def _torch():
+    import torch  # noqa: PLC0415
+
+    return torch
+
+
+def _stream_ptr(stream) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def workspace_bytes(rows: int, vocab: int, cfg: SamplerConfig, n_prev: int = 0) -> int:
+    return int(_lib().llz_sample_workspace_bytes(rows, vocab, C.byref(cfg.to_c()), n_prev))
+
+
+@dataclasses.dataclass
+class SampleResult:
+    tokens: "object"                  # torch.uint32-as-int32 tensor [rows]
+    consumed: "object"                # torch.uint8 [rows]
+    kept_count: Optional[object] = None
+    kept_ids: Optional[object] = None
+    kept_probs: Optional[object] = None
+    row_stats: Optional[object] = None
+
+
+def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, kept_cap: int = 0,
+                stats: bool = False, workspace=None, stream=None, out=None) -> SampleResult:
+    """Batched Sampler.sample over device rows.
+
+    logits: float32 CUDA tensor [rows, vocab] (rows may be strided);
+    uniforms: float32 CUDA tensor [rows]; prev_tokens: int32 CUDA tensor
+    [n_prev] (shared) or [rows, n_prev].  Returns device tensors; the call is
+    asynchronous on ``stream`` (default: torch's current stream).
+    """
+    torch = _torch()
+    if not (logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2):
+        raise ValueError("logits must be a 2-D float32 CUDA tensor")
+    if logits.stride(1) != 1:
+        raise ValueError("logits rows must be contiguous")
+    rows, vocab = logits.shape
+    dev = logits.device
+    if uniforms.dtype != torch.float32 or not uniforms.is_cuda or uniforms.numel() < rows:
+        raise ValueError("uniforms must be a float32 CUDA tensor with one value per row")
+    n_prev, prev_stride, prev_ptr = 0, 0, None
+    if prev_tokens is not None and prev_tokens.numel() > 0:
+        if prev_tokens.dim() == 1:
+            n_prev, prev_stride = prev_tokens.shape[0], 0
+        else:
+            n_prev, prev_stride = prev_tokens.shape[1], prev_tokens.stride(0)
+        prev_ptr = prev_tokens.data_ptr()
+    if out is None:
+        tokens = torch.empty(rows, dtype=torch.int32, device=dev)
+        consumed = torch.empty(rows, dtype=torch.uint8, device=dev)
+    else:
+        tokens, consumed = out
+    res = SampleResult(tokens, consumed)
+    ex = None
+    if kept_cap > 0 or stats:
+        ex = CExtras()
+        res.kept_count = torch.empty(rows, dtype=torch.int32, device=dev)
+        ex.d_kept_count = res.kept_count.data_ptr()
+        if kept_cap > 0:
+            res.kept_ids = torch.full((rows, kept_cap), -1, dtype=torch.int32, device=dev)
+            res.kept_probs = torch.full((rows, kept_cap), float("nan"), dtype=torch.float32, device=dev)
+            ex.d_kept_ids = res.kept_ids.data_ptr()
+            ex.d_kept_probs = res.kept_probs.data_ptr()
+            ex.kept_cap = kept_cap
+        if stats:
+            res.row_stats = torch.zeros((rows, 4), dtype=torch.float32, device=dev)
+            ex.d_row_stats = res.row_stats.data_ptr()
+    c = cfg.to_c()
+    need = int(_lib().llz_sample_workspace_bytes(rows, vocab, C.byref(c), n_prev))
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    rc = _lib().llz_sample_rows(
+        logits.data_ptr(), logits.stride(0), rows, vocab, C.byref(c), prev_ptr, n_prev, prev_stride,
+        uniforms.data_ptr(), tokens.data_ptr(), consumed.data_ptr(),
+        C.byref(ex) if ex is not None else None, workspace.data_ptr(), workspace.numel(),
+        _stream_ptr(stream))
+    _check(rc, "llz_sample_rows")
+    return res
+
+
+def argmax_rows(logits, stream=None):
+    """sampleArgmax per row (sampler.zig:31-41) on a 2-D float32 CUDA tensor."""
+    torch = _torch()
+    rows, vocab = logits.shape
+    tokens = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    rc = _lib().llz_argmax_rows(logits.data_ptr(), logits.stride(0), rows, vocab, tokens.data_ptr(),
+                                _stream_ptr(stream))
+    _check(rc, "llz_argmax_rows")
+    return tokens
+
+
+def debug_math(x):
+    """Device exp/log of a float32 CUDA tensor (parity tests of the math)."""
+    torch = _torch()
+    e = torch.empty_like(x)
+    lg = torch.empty_like(x)
+    rc = _lib().llz_debug_math(x.data_ptr(), e.data_ptr(), lg.data_ptr(), x.numel(), _stream_ptr(None))
+    _check(rc, "llz_debug_math")
+    return e, lg
+
+
+def set_kernel_events(begin=None, end=None) -> None:
+    """Record torch.cuda.Event objects around the sampling kernel of every
+    following sample_rows call (None, None clears)."""
+    b = C.c_void_p(begin.cuda_event) if begin is not None else None
+    e = C.c_void_p(end.cuda_event) if end is not None else None
+    _check(_lib().llz_debug_kernel_events(b, e), "llz_debug_kernel_events")
+
+
+class Sampler:
+    """Sampler.init / Sampler.sample (src/sampler.zig:15-28) on one GPU."""
+
+    def __init__(self, cfg: SamplerConfig, device: int = 0):
+        self.cfg = cfg
+        self._h = C.c_void_p()
+        _check(_lib().llz_sampler_create(C.byref(cfg.to_c()), device, C.byref(self._h)),
+               "llz_sampler_create")
+
+    def sample(self, logits, prev_tokens=()) -> int:
+        """logits: host numpy float32 [n] or a float32 CUDA tensor [n]."""
+        prev = np.ascontiguousarray(np.asarray(prev_tokens, dtype=np.uint32))
+        if isinstance(logits, np.ndarray):
+            x = np.ascontiguousarray(logits, dtype=np.float32)
+            ptr, n = x.ctypes.data, x.shape[0]
+        else:
+            ptr, n = logits.data_ptr(), logits.numel()
+        tok = C.c_uint32()
+        rc = _lib().llz_sampler_sample(self._h, ptr, n, prev.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                       prev.shape[0], C.byref(tok))
+        _check(rc, "llz_sampler_sample")
+        return int(tok.value)
+
+    @property
+    def state(self) -> Tuple[int, int, int, int]:
+        st = (C.c_uint64 * 4)()
+        _lib().llz_sampler_get_state(self._h, st)
+        return tuple(int(v) for v in st)
+
+    @state.setter
+    def state(self, value) -> None:
+        st = (C.c_uint64 * 4)(*[int(v) for v in value])
+        _lib().llz_sampler_set_state(self._h, st)
+
+    def close(self) -> None:
+        if self._h:
+            _lib().llz_sampler_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
+
+
+def sample_argmax(logits) -> int:
+    """sampleArgmax (sampler.zig:31-41) of one row (host array or CUDA tensor)."""
+    torch = _torch()
+    if isinstance(logits, np.ndarray):
+        t = torch.from_numpy(np.ascontiguousarray(logits, dtype=np.float32)).cuda()
+    else:
+        t = logits
+    return int(argmax_rows(t.view(1, -1))[0].item())
