@@ -46,7 +46,7 @@ __device__ float tile_accumulate(float s, const float (&x)[V], int L, float thr,
       const uint32_t ws = wave_sum_sat(tsum, kSat);
       const bool wt = __ballot(ttie) != 0ull;
       if (lane_id() == 0) sh.red[bank][wave_id()] = ws | (wt ? 0x80000000u : 0u);
-      __syncthreads();
+      lds_barrier();
     }
     uint32_t total = 0;
     bool anytie = false;
@@ -108,6 +108,78 @@ __device__ float tile_accumulate(float s, const float (&x)[V], int L, float thr,
     s = s_post;
     done = (int)P;
     if (done >= L - 1) return s;
+  }
+}
+
+// Additive tile accumulation with implicit terms: R(k, j, tie) returns
+// RN(term_k / 2^(j-23)) (saturated at kSat) and sets tie; E(k) returns the
+// exact term, and is called only for the element at which an event is
+// resolved; present(k) is false for positions outside the sequence.  Lets a
+// caller supply roundings from a cheaper, exact-when-unambiguous estimate.
+template <int NT, int V, typename RFn, typename EFn, typename PFn>
+__device__ float tile_accumulate_fn(float s, RFn R, EFn E, PFn present, WgScratch<NT>& sh, int& bank) {
+  const int t = (int)threadIdx.x;
+  int done = -1;
+  for (;;) {
+    const Grid g = grid_of(s);
+    uint32_t r[V];
+    bool tie[V];
+    uint32_t tsum = 0;
+    bool ttie = false;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const int p = t * V + k;
+      r[k] = 0;
+      tie[k] = false;
+      if (p > done && present(k)) r[k] = R(k, g.j, tie[k]);
+      tsum = sat_add(tsum, r[k], kSat);
+      ttie = ttie || tie[k];
+    }
+    {
+      const uint32_t ws = wave_sum_sat(tsum, kSat);
+      const bool wt = __ballot(ttie) != 0ull;
+      if (lane_id() == 0) sh.red[bank][wave_id()] = ws | (wt ? 0x80000000u : 0u);
+      lds_barrier();
+    }
+    uint32_t total = 0;
+    bool anytie = false;
+#pragma unroll
+    for (int w = 0; w < WgScratch<NT>::W; ++w) {
+      const uint32_t v = sh.red[bank][w];
+      total = sat_add(total, v & 0x7fffffffu, kSat);
+      anytie = anytie || (v >> 31);
+    }
+    bank ^= 1;
+    if (!anytie && g.N + total < kGridTop) return grid_value(g.N + total, g.j);
+
+    const uint32_t excl = wg_excl_scan_sat<NT>(tsum, kSat, sh, bank);
+    uint32_t run = g.N + excl;
+    uint32_t my_evt = 0xffffffffu;
+    uint32_t my_before = 0;
+    int my_k = 0;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const int p = t * V + k;
+      if (p > done && present(k) && my_evt == 0xffffffffu) {
+        const uint32_t before = run;
+        run += r[k];
+        if (tie[k] || run >= kGridTop) {
+          my_evt = (uint32_t)p;
+          my_before = before;
+          my_k = k;
+        }
+      }
+    }
+    const uint32_t P = wg_min_u32<NT>(my_evt, sh, bank);
+    if (P == 0xffffffffu) return grid_value(g.N + total, g.j);
+    const bool owner = my_evt == P;
+    float s_post = 0.0f;
+    uint32_t unused = 0;
+    if (owner) s_post = grid_value(my_before, g.j) + E(my_k);
+    wg_bcast<NT>(owner, s_post, unused, sh, bank);
+    s = s_post;
+    done = (int)P;
+    if (done >= NT * V - 1) return s;
   }
 }
 

@@ -26,7 +26,7 @@ bool penalty_active(const llz_sampler_config* cfg, int32_t n_prev) {
 
 // Workspace layout of one llz_sample_rows call.
 struct Layout {
-  size_t maxpart, status, penal, fb, fb_mask, total;
+  size_t maxpart, status, rstate, cand, penal, fb, fb_mask, total;
   bool has_penal;
 };
 
@@ -36,6 +36,8 @@ Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int
   size_t off = 0;
   L.maxpart = off; off = align_up(off + r * (size_t)max_parts(vocab) * sizeof(float));
   L.status = off;  off = align_up(off + r * sizeof(uint32_t));
+  L.rstate = off;  off = align_up(off + r * 4 * sizeof(float));
+  L.cand = off;    off = align_up(off + r * (size_t)kCandCap * sizeof(uint64_t));
   L.has_penal = penalty_active(cfg, n_prev);
   L.penal = off;   if (L.has_penal) off = align_up(off + r * n * sizeof(float));
   L.fb = off;      off = align_up(off + 6 * r * n * sizeof(uint32_t));
@@ -159,6 +161,7 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   P.typical_p = cfg->typical_p;
   P.top_k = cfg->top_k;
   P.cand_theta = candidate_theta(cfg, vocab);
+  P.l2e_t = (float)(1.4426950408889634 / (double)cfg->temperature);
   P.n = vocab;
   P.rows = rows;
   P.nparts = max_parts(vocab);
@@ -181,13 +184,12 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
     Q.row_stats = extras->d_row_stats;
   }
   Q.status = (uint32_t*)(ws + L.status);
+  Q.cand = (uint64_t*)(ws + L.cand);
+  Q.row_state = (float*)(ws + L.rstate);
   Q.fb = (uint32_t*)(ws + L.fb);
   Q.fb_mask = (uint8_t*)(ws + L.fb_mask);
-  if (g_ev_begin && hipEventRecord(g_ev_begin, st) != hipSuccess) return LLZ_E_HIP;
-  e = launch_sample(P, Q, st);
-  if (e != hipSuccess) return LLZ_E_HIP;
-  if (g_ev_end && hipEventRecord(g_ev_end, st) != hipSuccess) return LLZ_E_HIP;
-  return LLZ_OK;
+  e = launch_sample(P, Q, g_ev_begin, g_ev_end, st);
+  return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }
 
 int llz_debug_kernel_events(void* begin_event, void* end_event) {

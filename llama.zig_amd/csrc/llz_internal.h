@@ -26,6 +26,7 @@ struct RowParams {
   float typical_p;
   uint32_t top_k;
   float cand_theta;   // e >= cand_theta enters the candidate list
+  float l2e_t;        // RN(log2(e) / temperature)
   int32_t n;          // vocab
   int32_t rows;
   int32_t nparts;     // partial maxima per row
@@ -48,6 +49,8 @@ struct RowPtrs {
   float* kept_probs;
   float* row_stats;
   uint32_t* status;
+  uint64_t* cand;         // [rows][kCandCap] candidate list (k_norm -> k_select)
+  float* row_state;       // [rows][4]: max, normaliser, candidate count (bits)
   uint32_t* fb;           // 6 x [rows][n] u32 (fallback sort buffers)
   uint8_t* fb_mask;       // [rows][n]
 };
@@ -60,7 +63,8 @@ hipError_t launch_rowmax(const float* logits, int64_t stride, int rows, int n, b
                          hipStream_t st);
 hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t* tokens,
                          uint8_t* consumed, uint32_t* kept_count, hipStream_t st);
-hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipStream_t st);
+hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_begin, hipEvent_t ev_end,
+                         hipStream_t st);
 hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, int64_t n, hipStream_t st);
 
 }  // namespace llz

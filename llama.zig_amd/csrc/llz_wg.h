@@ -14,42 +14,68 @@ constexpr int kWave = 64;
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 __device__ __forceinline__ int wave_id() { return (int)(threadIdx.x / kWave); }
 
+// Workgroup barrier that orders LDS only: outstanding global loads (for
+// example prefetches) stay in flight.  Code that hands data between threads
+// through global memory uses __syncthreads() (or __threadfence()) instead.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Saturating u32 add: results stay <= cap.
 __device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b, uint32_t cap) {
   uint32_t s = a + b;  // a, b <= cap <= 2^30, no wrap
   return s < cap ? s : cap;
 }
 
-template <typename T>
-__device__ __forceinline__ T wave_shfl_xor(T v, int m) { return __shfl_xor(v, m, kWave); }
-
-__device__ __forceinline__ uint32_t wave_sum_sat(uint32_t v, uint32_t cap) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = sat_add(v, wave_shfl_xor(v, m), cap);
-  return v;
+// DPP cross-lane moves (register speed, no LDS round trip).  CTRL values:
+// row_shr:n = 0x110+n, wave_shr:1 = 0x138, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143.  Lanes that are masked off, or that read outside
+// their row with bound_ctrl set, receive `old`.
+template <int CTRL, int ROW_MASK, int BANK_MASK, bool BC>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, BANK_MASK, BC);
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = max(v, (uint32_t)wave_shfl_xor(v, m));
-  return v;
+// Wave64 inclusive scan for an associative op with identity `id` (the
+// row_shr 1/2/3, row_shr 4 and 8, row_bcast 15 and 31 sequence).
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_incl_scan_op(uint32_t x, uint32_t id, Op op) {
+  uint32_t s = x;
+  s = op(s, dpp_u32<0x111, 0xf, 0xf, true>(id, x));
+  s = op(s, dpp_u32<0x112, 0xf, 0xf, true>(id, x));
+  s = op(s, dpp_u32<0x113, 0xf, 0xf, true>(id, x));
+  s = op(s, dpp_u32<0x114, 0xf, 0xe, false>(id, s));
+  s = op(s, dpp_u32<0x118, 0xf, 0xc, false>(id, s));
+  s = op(s, dpp_u32<0x142, 0xa, 0xf, false>(id, s));
+  s = op(s, dpp_u32<0x143, 0xc, 0xf, false>(id, s));
+  return s;
 }
 
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = min(v, (uint32_t)wave_shfl_xor(v, m));
-  return v;
+__device__ __forceinline__ uint32_t lane_readlast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, kWave - 1);
 }
 
 // Inclusive prefix (saturating) within a wave.
 __device__ __forceinline__ uint32_t wave_incl_scan_sat(uint32_t v, uint32_t cap) {
-  const int l = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    uint32_t o = __shfl_up(v, d, kWave);
-    if (l >= d) v = sat_add(v, o, cap);
-  }
-  return v;
+  return wave_incl_scan_op(v, 0u, [cap](uint32_t a, uint32_t b) { return sat_add(a, b, cap); });
+}
+
+// The previous lane's value (lane 0 gets 0).
+__device__ __forceinline__ uint32_t wave_shift_up1(uint32_t v) { return dpp_u32<0x138, 0xf, 0xf, true>(0u, v); }
+
+__device__ __forceinline__ uint32_t wave_sum_sat(uint32_t v, uint32_t cap) {
+  return lane_readlast(wave_incl_scan_sat(v, cap));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return lane_readlast(wave_incl_scan_op(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; }));
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  return lane_readlast(
+      wave_incl_scan_op(v, 0xffffffffu, [](uint32_t a, uint32_t b) { return a < b ? a : b; }));
 }
 
 // Shared scratch for the workgroup reductions.  Two banks alternate so a
@@ -67,7 +93,7 @@ template <int NT>
 __device__ __forceinline__ uint32_t wg_sum_sat(uint32_t v, uint32_t cap, WgScratch<NT>& sh, int& bank) {
   v = wave_sum_sat(v, cap);
   if (lane_id() == 0) sh.red[bank][wave_id()] = v;
-  __syncthreads();
+  lds_barrier();
   uint32_t t = 0;
 #pragma unroll
   for (int w = 0; w < WgScratch<NT>::W; ++w) t = sat_add(t, sh.red[bank][w], cap);
@@ -79,7 +105,7 @@ template <int NT>
 __device__ __forceinline__ uint32_t wg_max_u32(uint32_t v, WgScratch<NT>& sh, int& bank) {
   v = wave_max_u32(v);
   if (lane_id() == 0) sh.red[bank][wave_id()] = v;
-  __syncthreads();
+  lds_barrier();
   uint32_t t = 0;
 #pragma unroll
   for (int w = 0; w < WgScratch<NT>::W; ++w) t = max(t, sh.red[bank][w]);
@@ -91,7 +117,7 @@ template <int NT>
 __device__ __forceinline__ uint32_t wg_min_u32(uint32_t v, WgScratch<NT>& sh, int& bank) {
   v = wave_min_u32(v);
   if (lane_id() == 0) sh.red[bank][wave_id()] = v;
-  __syncthreads();
+  lds_barrier();
   uint32_t t = 0xffffffffu;
 #pragma unroll
   for (int w = 0; w < WgScratch<NT>::W; ++w) t = min(t, sh.red[bank][w]);
@@ -106,9 +132,8 @@ __device__ __forceinline__ uint32_t wg_excl_scan_sat(uint32_t v, uint32_t cap, W
   if (lane_id() == kWave - 1) sh.red[bank][wave_id()] = incl;
   // exclusive = the previous lane's inclusive value: exact whenever it is
   // below the cap (a saturated prefix only ever reads as "at least cap")
-  uint32_t excl_in_wave = __shfl_up(incl, 1, kWave);
-  if (lane_id() == 0) excl_in_wave = 0;
-  __syncthreads();
+  const uint32_t excl_in_wave = wave_shift_up1(incl);
+  lds_barrier();
   uint32_t before = 0;
   const int w = wave_id();
   for (int i = 0; i < w; ++i) before = sat_add(before, sh.red[bank][i], cap);
@@ -123,7 +148,7 @@ __device__ __forceinline__ void wg_bcast(bool writer, float& f, uint32_t& u, WgS
     sh.fb[bank][0] = f;
     sh.ub[bank][0] = u;
   }
-  __syncthreads();
+  lds_barrier();
   f = sh.fb[bank][0];
   u = sh.ub[bank][0];
   bank ^= 1;
@@ -145,7 +170,7 @@ __device__ void lds_bitonic_sort_u64(uint64_t* a, int n) {
           }
         }
       }
-      __syncthreads();
+      lds_barrier();
     }
   }
 }
