@@ -280,3 +280,47 @@ def test_reference_unit_tests_restated(cuda):
                              repetition_window=0, repetition_penalty=1.0)
     s = llz.Sampler(cfg2)
     assert [s.sample(np.array([2.0, 1.9, 1.8], np.float32)) for _ in range(16)] == [0] * 16
+
+
+# ---------------------------------------------------------------------------
+# the committed golden vectors (tests/golden/sampler_golden.npz)
+# ---------------------------------------------------------------------------
+def test_golden_vectors_on_gpu(cuda):
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "sampler_golden.npz"), allow_pickle=False)
+    for i, name in enumerate(g["name"]):
+        n, off = int(g["n"][i]), int(g["offset"][i])
+        x = g["logits"][off:off + n].reshape(1, n)
+        t, k, tp, mp, typ, win, rp = g["params"][i]
+        p = Params(temperature=float(t), top_k=int(k), top_p=float(tp), min_p=float(mp), typical_p=float(typ),
+                   repetition_window=int(win), repetition_penalty=float(rp))
+        prev = None
+        if g["n_prev"][i]:
+            po = int(g["prev_offset"][i])
+            prev = g["prev_tokens"][po:po + int(g["n_prev"][i])].reshape(1, -1)
+        cap = g["kept_ids"].shape[1]
+        r = run_gpu(x, p, g["u"][i:i + 1], cuda, prev=prev, kept_cap=cap)
+        assert r["tokens"][0] == g["token"][i], name
+        assert r["consumed"][0] == g["consumed"][i], name
+        if g["exit_path"][i] == O.EXIT_GREEDY:
+            continue
+        assert r["kept_count"][0] == g["kept_count"][i], name
+        kc = min(int(g["kept_count"][i]), cap)
+        assert np.array_equal(r["kept_ids"][0, :kc], g["kept_ids"][i, :kc]), name
+        assert np.array_equal(_f32bits(r["kept_probs"][0, :kc]), g["kept_probs_bits"][i, :kc]), name
+        sb = g["stats_bits"][i]
+        assert _f32bits(r["stats"][0, 0]) == sb[0] and _f32bits(r["stats"][0, 1]) == sb[1], name
+
+
+def test_golden_config1_full_vocab_on_gpu(cuda):
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "sampler_golden.npz"), allow_pickle=False)
+    w = WORKLOADS["c1"]
+    x = w.logits(1)
+    r = run_gpu(x, w.params, np.array([g["c1_u"]], np.float32), cuda, kept_cap=64)
+    assert (r["tokens"][0], r["consumed"][0], r["kept_count"][0]) == (g["c1_token"], g["c1_consumed"], g["c1_kept"])
+    k = g["c1_kept_ids"].size
+    assert np.array_equal(r["kept_ids"][0, :k], g["c1_kept_ids"])
+    assert _f32bits(r["stats"][0, 1]) == g["c1_stats_bits"][1]
