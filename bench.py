@@ -157,7 +157,7 @@ def main() -> int:
                    "typical_p": w.params.typical_p, "parallelism": "none (1 GPU)"},
         "gbps": round(alg / (ms_per_step * 1e-3) / 1e9, 1),
         "ms_per_step_events": round(ms_events, 5),
-        "roofline": {"bound": "hbm", "kernel": "k_norm", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_stats", "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
                      "traffic": traffic, "kernel_ms": round(k_avg, 5),
                      "algorithmic_bytes": alg},

@@ -151,8 +151,7 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   }
   const bool vec = ((uintptr_t)src % 16 == 0) && (src_stride % 4 == 0);
   float* maxpart = (float*)(ws + L.maxpart);
-  hipError_t e = launch_rowmax(src, src_stride, rows, vocab, vec, maxpart, st);
-  if (e != hipSuccess) return LLZ_E_HIP;
+  hipError_t e = hipSuccess;
 
   RowParams P{};
   P.temperature = cfg->temperature;

@@ -1,0 +1,213 @@
+// llz_fast.h -- single-pass row statistics: the row maximum, the exact
+// sequential f32 normaliser and the candidate list (sampler.zig:80-88) with
+// one HBM read per logit.
+//
+// One 512-thread workgroup owns a row.  Wave w owns the contiguous run of
+// 256-element segments [w*SPW, (w+1)*SPW); the first KV segments of the run
+// stay in VGPRs (one float4 per lane per segment), the next KL in LDS.
+//
+// Phase L (while the loads land): per-lane running maximum; the estimate
+//     q = exp2(v * RN(log2(e)/T) - c_w),   c_w = RN(m_w * RN(log2(e)/T))
+// with m_w the maximum of the wave's first segment, stored over v; the
+// segment sum of q.
+// Phase M: the row maximum m; R_w = exp2(c_w - m * RN(log2(e)/T)) turns q into
+// q * R_w ~ e = exp((v - m) / T).  A prefix of the segment sums predicts the
+// binade of the running sum at every segment; a segment whose predicted
+// range [P(1 - d), P_end(1 + d)] stays inside one binade j is PLAIN, any
+// other is EXACT.
+// Phase S: PLAIN segments round every term on the binade's grid
+// u = 2^(j-23): with sc = R_w 2^(23-j), fma(q, sc(1 -+ eps), 1.5*2^23) gives
+// RN(q sc (1 -+ eps)) as an integer.  When both agree the true RN(e / u) is
+// that integer and is not a tie; the others (and the large terms and the
+// candidates) are "special": re-read, evaluated with the exact exp
+// (llz_math.h) and corrected.  A special whose exact term is a tie turns its
+// segment EXACT.
+// Phase X: EXACT segments are re-read and evaluated exactly into LDS.
+// Phase C: one wave walks the segments in index order: runs of PLAIN
+// segments add their integer sums while the running sum stays in their
+// binade; EXACT segments are replayed term by term with the exact
+// parallel accumulation (wave_accumulate, llz_norm.h).
+//
+// Error bound of the estimate relative to the reference's term e =
+// exp(RN(RN(v - m) / T)) for the terms that can round to a non-zero integer
+// (X = (v - m) log2(e) / T, |X| <= 25 - j): the reference's own two
+// roundings of its argument and the rounding of log2(e)/T contribute
+// 3|X| 2^-24 (in log2 units), the rounding of v RN(log2(e)/T) - c_w at most
+// (|X| + 32) 2^-24 and that of the argument of R_w at most 32 2^-24 (the
+// kernel requires |(m - m_w) RN(log2(e)/T)| <= 32), so together
+// ln2 (4|X| + 64) 2^-24; the two hardware exp2 (<= 2^-23 each), the final
+// multiply (2^-24) and the reference exp (< 2^-23) add < 2^-21.  eps(j) is
+// twice that bound.  For |X| < 25 - j the terms are below 1/4 of the grid
+// and round to 0 on both sides.
+//
+// Anything the fast path cannot certify (an unpredicted binade crossing, a
+// grid mismatch, a queue overflow, a row longer than the resident capacity)
+// sets `fail`; the caller then runs the streaming normaliser instead.
+#pragma once
+
+#include "llz_accum.h"
+#include "llz_exact.h"
+#include "llz_internal.h"
+#include "llz_math.h"
+#include "llz_norm.h"
+#include "llz_wg.h"
+
+namespace llz {
+namespace fastp {
+constexpr int NT = 512;
+constexpr int W = NT / kWave;       // 8 waves
+constexpr int SEG = 256;            // elements per segment: one float4 per lane
+constexpr int KV = 45;              // register-resident segments per wave
+constexpr int KL = 18;              // LDS-resident segments per wave
+constexpr int SPWMAX = KV + KL;     // segments per wave at most (<= 64: one lane each)
+constexpr int GMAX = W * SPWMAX;    // 504 segments = 129024 logits
+constexpr int QCAP = 128;           // special queue capacity per wave (flushed when full)
+constexpr int DCAP = 48;            // EXACT segments evaluated per round
+constexpr float DELTA = 0x1p-10f;   // relative margin of the binade prediction
+constexpr float MAGIC = 12582912.0f;            // 1.5 * 2^23
+constexpr uint32_t MAGIC_BITS = 0x4b400000u;    // its bit pattern
+// PLAIN: integer sum on one grid; EXACT_PRED: predicted binade change, its
+// candidates not collected yet; EXACT_DONE: the same, collected; EXACT_TIE:
+// was PLAIN, holds a tie (its candidates came from the special queue).
+enum : uint8_t { PLAIN = 0, EXACT_PRED = 1, EXACT_TIE = 2, EXACT_DONE = 3 };
+static_assert(SPWMAX <= 64, "segment metadata is held one segment per lane");
+static_assert(DCAP <= 127, "slots are stored as int8");
+}  // namespace fastp
+
+// EXACT segments: exact terms, per-lane inclusive prefixes of their
+// roundings on grids sj and sj+1, and the lanes holding a tie.
+struct ExactSlots {
+  float dump[fastp::DCAP][fastp::SEG];
+  uint32_t pref[fastp::DCAP][2][kWave];
+  uint64_t tmask[fastp::DCAP][2];
+};
+
+struct FastShared {
+  union {
+    float data[fastp::W][fastp::KL][fastp::SEG];  // LDS-resident segments (q), phases L and S
+    ExactSlots x;                                 // after phase S
+  } u;
+  float aseg[fastp::GMAX];                      // segment sums of q
+  uint32_t ssum[fastp::GMAX];                   // PLAIN: integer sum on grid sj
+  int8_t sj[fastp::GMAX];                       // PLAIN: its binade; EXACT: first binade tabulated
+  uint8_t sflag[fastp::GMAX];
+  int8_t sdump[fastp::GMAX];                    // EXACT: slot in `dump`, or -1
+  uint32_t qpos[fastp::W][fastp::QCAP];         // special queue: position
+  float qq[fastp::W][fastp::QCAP];              //   and its estimate q
+  float mw[fastp::W];
+  float cw[fastp::W];
+  uint32_t nanw[fastp::W];
+  float wtot[fastp::W];     // per wave: sum of its scaled segment sums
+  uint32_t wflag[fastp::W]; //   bit 0: not certifiable, bit 1: candidate flood
+  int wnex[fastp::W];       //   number of its EXACT segments
+  uint32_t ncand;
+  uint32_t fail;
+  uint32_t flood;
+  int next_g;     // combine: first segment not consumed yet
+  float s_run;    // combine: running sum at next_g
+  int done;
+};
+
+typedef float llz_f4v __attribute__((ext_vector_type(4)));
+typedef int llz_i4v __attribute__((ext_vector_type(4)));
+
+// Raw buffer load of 16 bytes (buffer_load_dwordx4 ... offen): address =
+// resource base + voffset (VGPR) + soffset (SGPR); reads past the
+// resource's byte count return 0.  aux 2 = non-temporal.
+__device__ llz_i4v llz_raw_buffer_load_v4i32(llz_i4v rsrc, int voffset, int soffset,
+                                             int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+
+// Buffer resource over `bytes` bytes at `base` (wave-uniform): raw buffer,
+// stride 0, gfx9 word 3 (32-bit data format).
+__device__ __forceinline__ llz_i4v row_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  llz_i4v r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+  r.w = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane from global memory straight to LDS (lane i writes
+// lds_base + 16 i).  Written as inline asm on purpose: the compiler's wait
+// insertion does not see it, so it keeps counting only its own loads (issue
+// these before them: an older load only makes the compiler's waits
+// stronger).  The caller waits with s_waitcnt vmcnt(0) before reading LDS.
+__device__ __forceinline__ void dma16(const float* gaddr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_base) : "m0", "memory");
+}
+
+__device__ __forceinline__ float4 buf_ld4(llz_i4v rsrc, int voffset, int soffset) {
+  const llz_i4v v = llz_raw_buffer_load_v4i32(rsrc, voffset, soffset, 2);
+  return make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
+}
+
+__device__ __forceinline__ float4 ld_nt4(const float* p) {
+  const llz_f4v v = __builtin_nontemporal_load(reinterpret_cast<const llz_f4v*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// Segment load: a full, 16-byte aligned segment as one float4 per lane;
+// otherwise per element, absent positions (>= n) as -inf.
+__device__ __forceinline__ float4 ld_seg(const float* xr, int pos, int n, bool vec) {
+  if (vec && pos + 4 <= n) return ld_nt4(xr + pos);
+  float4 v;
+  v.x = pos + 0 < n ? xr[pos + 0] : -__builtin_inff();
+  v.y = pos + 1 < n ? xr[pos + 1] : -__builtin_inff();
+  v.z = pos + 2 < n ? xr[pos + 2] : -__builtin_inff();
+  v.w = pos + 3 < n ? xr[pos + 3] : -__builtin_inff();
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  const uint32_t r = wave_incl_scan_op(__float_as_uint(v), 0u, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  });
+  return __uint_as_float(lane_readlast(r));
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  const uint32_t r = wave_incl_scan_op(__float_as_uint(v), __float_as_uint(-__builtin_inff()),
+                                       [](uint32_t a, uint32_t b) {
+                                         return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+                                       });
+  return __uint_as_float(lane_readlast(r));
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  return lane_readlast(wave_incl_scan_op(v, 0u, [](uint32_t a, uint32_t b) { return a + b; }));
+}
+
+// Relative error bound of the estimate for terms that matter on grid j
+// (see the header comment), doubled.
+__device__ __forceinline__ float fast_eps(int j) {
+  const float ax = (float)(25 - j);
+  return 2.0f * (0.6931472f * (4.0f * ax + 64.0f) * 0x1p-24f + 0x1p-21f);
+}
+
+// A float with its mantissa LSB forced to 1 (see the no-tie argument: an
+// odd scale never makes q * scale an exact half-integer below 2^15).
+__device__ __forceinline__ float odd_mantissa(float x) { return __uint_as_float(__float_as_uint(x) | 1u); }
+
+// Per-grid constants of phase S.
+struct GridConst {
+  int j;
+  float sc_lo, sc_hi;  // R 2^(23-j) (1 -+ eps), odd mantissas
+  float tspec;         // rh >= tspec: large term or candidate
+};
+
+__device__ __forceinline__ GridConst grid_const(int j, float R, float theta) {
+  GridConst c;
+  c.j = j;
+  const float sc = ldexpf(R, 23 - j);
+  const float eps = fast_eps(j);
+  c.sc_lo = odd_mantissa(sc * (1.0f - eps));
+  c.sc_hi = odd_mantissa(sc * (1.0f + eps));
+  // candidates: e >= theta  =>  e / u >= theta 2^(23-j)
+  const float yc = fminf(floorf(ldexpf(theta, 23 - j)), 32768.0f);
+  c.tspec = fastp::MAGIC + fmaxf(yc - 1.0f, 0.0f);
+  return c;
+}
+
+}  // namespace llz

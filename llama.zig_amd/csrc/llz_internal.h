@@ -16,7 +16,8 @@ constexpr uint32_t kFlagFallback = 4u;  // the full-row fallback buffers are pre
 // per-row status bits (diagnostics)
 constexpr uint32_t kPathSumLe0 = 1u;
 constexpr uint32_t kPathEntropy = 2u;
-constexpr uint32_t kPathFallback = 4u;
+constexpr uint32_t kPathFallback = 4u;      // full-row radix sort in k_select
+constexpr uint32_t kPathNormFallback = 8u;  // streaming normaliser in k_select
 constexpr uint32_t kPathError = 0x80000000u;
 
 struct RowParams {
@@ -63,6 +64,7 @@ hipError_t launch_rowmax(const float* logits, int64_t stride, int rows, int n, b
                          hipStream_t st);
 hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t* tokens,
                          uint8_t* consumed, uint32_t* kept_count, hipStream_t st);
+hipError_t launch_stats(const RowParams& P, const RowPtrs& Q, hipStream_t st);
 hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_begin, hipEvent_t ev_end,
                          hipStream_t st);
 hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, int64_t n, hipStream_t st);

@@ -447,7 +447,7 @@ __device__ __forceinline__ bool wave_resolve(float& s, int& done, const SliceSta
 // sampler.zig:83-88: the exact sequential f32 normaliser of one row, plus the
 // candidate list (every element with e >= cand_theta).
 __device__ float row_normaliser(const float* xr, int n, const float* maxpart, const RowParams& P,
-                                SampleShared& sh, int& bank, float& m_out) {
+                                SampleShared& sh, int& bank, float& m_out, float m_known = 0.0f) {
   constexpr int W = kNT / kWave;
   constexpr int GE = W * kSlice;    // elements per group
   constexpr int NC = W * kSub;      // sub-chunks per group
@@ -461,7 +461,8 @@ __device__ float row_normaliser(const float* xr, int n, const float* maxpart, co
   // independent loads first: the max partials, the prologue's logits and the
   // first group
   float mp = -kInf;
-  for (int i = t; i < P.nparts; i += kNT) mp = fmaxf(mp, maxpart[i]);
+  if (maxpart == nullptr) mp = m_known;
+  else for (int i = t; i < P.nparts; i += kNT) mp = fmaxf(mp, maxpart[i]);
   const float vp = (w == 0 && lane < p0) ? xr[lane] : 0.0f;
   float vcur[kSub][kV], vnext[kSub][kV];
 #pragma unroll
@@ -759,16 +760,25 @@ __global__ __launch_bounds__(kNT) void k_select(RowParams P, RowPtrs Q) {
 
   // ---- 1-2. from k_norm: row maximum, normaliser, candidate list
   const float* rsn = Q.row_state + (int64_t)row * 4;
-  const float m = rsn[0];
-  const float S = rsn[1];
-  const uint32_t cc_in = __float_as_uint(rsn[2]);
-  {
+  float m = rsn[0];
+  float S = rsn[1];
+  uint32_t path = 0;
+  if (rsn[3] != 0.0f) {
+    // k_stats could not certify this row: the streaming normaliser
+    // (sampler.zig:83-88) fills the candidate list in LDS
+    if (t == 0) sh.cand_count = 0;
+    float m2;
+    S = row_normaliser(xr, n, nullptr, P, sh, bank, m2, m);
+    m = m2;
+    path |= kPathNormFallback;
+  } else {
+    const uint32_t cc_in = __float_as_uint(rsn[2]);
     const int c = cc_in > (uint32_t)kCap ? kCap : (int)cc_in;
     const uint64_t* gc = Q.cand + (int64_t)row * kCap;
     for (int i = t; i < c; i += kNT) sh.cand[i] = gc[i];
     if (t == 0) sh.cand_count = cc_in;
   }
-  uint32_t token = 0, consumed = 0, path = 0;
+  uint32_t token = 0, consumed = 0;
   float H = 0.0f, total = 0.0f;
   int K = 0;
 
@@ -785,6 +795,32 @@ __global__ __launch_bounds__(kNT) void k_select(RowParams P, RowPtrs Q) {
         rs[0] = m; rs[1] = S; rs[2] = 0.0f; rs[3] = 0.0f;
       }
       if (Q.status) Q.status[row] = path;
+    }
+    return;
+  }
+
+  // ---- a NaN normaliser (a NaN logit or an infinite maximum): every
+  // probability is NaN, so every comparison of the chain is false.  The
+  // stable sort keeps index order, top-k keeps the first k indices, top-p,
+  // min-p and typical-p keep everything, the total is NaN and the walk never
+  // stops: indices[0] = 0 after one draw (sampler.zig:96-168).
+  if (S != S) {
+    const int kept = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
+    if (Q.kept_ids || Q.kept_probs) {
+      for (int q = t; q < kept && q < P.kept_cap; q += kNT) {
+        if (Q.kept_ids) Q.kept_ids[(int64_t)row * P.kept_cap + q] = (uint32_t)q;
+        if (Q.kept_probs) Q.kept_probs[(int64_t)row * P.kept_cap + q] = __builtin_nanf("");
+      }
+    }
+    if (t == 0) {
+      Q.tokens[row] = 0;
+      if (Q.consumed) Q.consumed[row] = 1;
+      if (Q.kept_count) Q.kept_count[row] = (uint32_t)kept;
+      if (Q.row_stats) {
+        float* rs = Q.row_stats + (int64_t)row * 4;
+        rs[0] = m; rs[1] = S; rs[2] = 0.0f; rs[3] = __builtin_nanf("");
+      }
+      if (Q.status) Q.status[row] = 0;
     }
     return;
   }
@@ -1058,7 +1094,7 @@ hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, u
 hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_begin, hipEvent_t ev_end,
                          hipStream_t st) {
   if (ev_begin && hipEventRecord(ev_begin, st) != hipSuccess) return hipErrorUnknown;
-  hipLaunchKernelGGL(k_norm, dim3(P.rows), dim3(kNT), 0, st, P, Q);
+  if (launch_stats(P, Q, st) != hipSuccess) return hipErrorUnknown;
   if (ev_end && hipEventRecord(ev_end, st) != hipSuccess) return hipErrorUnknown;
   hipLaunchKernelGGL(k_select, dim3(P.rows), dim3(kNT), 0, st, P, Q);
   return hipGetLastError();

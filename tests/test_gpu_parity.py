@@ -324,3 +324,27 @@ def test_golden_config1_full_vocab_on_gpu(cuda):
     k = g["c1_kept_ids"].size
     assert np.array_equal(r["kept_ids"][0, :k], g["c1_kept_ids"])
     assert _f32bits(r["stats"][0, 1]) == g["c1_stats_bits"][1]
+
+
+def test_non_finite_rows(cuda):
+    """A NaN logit or an infinite maximum makes the reference's normaliser NaN:
+    every comparison is then false and sampler.zig returns index 0 after a draw."""
+    n, rows = 3000, 6
+    x = _rand_rows(rows, n, seed=21)
+    x[0, 17] = np.nan
+    x[1, :] = -np.inf
+    x[2, 5] = np.inf
+    x[3, :] = np.nan
+    x[4, 2999] = np.nan
+    x[5, ::2] = -np.inf  # finite maximum: an ordinary row
+    for params in (Params(temperature=0.8, top_k=0, top_p=0.9, repetition_penalty=1.0),
+                   Params(temperature=1.0, top_k=7, top_p=0.5, min_p=0.1, typical_p=0.9, repetition_penalty=1.0)):
+        u = llz.rng_uniforms(5, rows)
+        g = run_gpu(x, params, u, cuda, kept_cap=n)
+        for r in range(rows):
+            o = O.sample_row(x[r], params, u[r])
+            assert g["tokens"][r] == o.token, r
+            assert g["consumed"][r] == o.consumed, r
+            assert g["kept_count"][r] == o.kept_count, r
+            k = min(o.kept_count, g["cap"])
+            assert np.array_equal(g["kept_ids"][r, :k], o.kept_ids()[:k]), r
