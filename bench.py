@@ -48,17 +48,38 @@ def cpu_baseline(w, x_host, u_host, rows: int, threads: int) -> dict:
     }
 
 
+def calibrate_copy(mib: int) -> int:
+    """A plain device-to-device copy of known size (torch's copy kernel), so the
+    HBM counters' bytes per dispatch can be scaled against bytes actually moved."""
+    import torch
+
+    n = mib << 20
+    src = [torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(i + 1) for i in range(3)]
+    dst = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    torch.cuda.synchronize()
+    for i in range(6):
+        dst.copy_(src[i % 3])
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "dispatches": 6}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="headline")
-    ap.add_argument("--cpu-rows", type=int, default=1024)
+    ap.add_argument("--cpu-rows", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "k_sample_headline_traffic.json"),
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "k_stats_headline_traffic.json"),
                     help="HBM traffic per launch measured with rocprofv3 --pmc (JSON), if present")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark: launch a plain device copy of MIB MiB a few times, "
+                         "the known-size reference for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
