@@ -66,12 +66,14 @@ constexpr int DCAP = 48;            // EXACT segments evaluated per round
 constexpr float DELTA = 0x1p-10f;   // relative margin of the binade prediction
 constexpr float MAGIC = 12582912.0f;            // 1.5 * 2^23
 constexpr uint32_t MAGIC_BITS = 0x4b400000u;    // its bit pattern
-// PLAIN: integer sum on one grid; EXACT_PRED: predicted binade change, its
-// candidates not collected yet; EXACT_DONE: the same, collected; EXACT_TIE:
-// was PLAIN, holds a tie (its candidates came from the special queue).
-enum : uint8_t { PLAIN = 0, EXACT_PRED = 1, EXACT_TIE = 2, EXACT_DONE = 3 };
+constexpr int TCAP = 160;          // tie records per row
+// PLAIN: integer sum on one grid; PLAIN_TIE: the same with tie records;
+// EXACT_PRED: predicted binade change, its candidates not collected yet;
+// EXACT_DONE: the same, collected.
+enum : uint8_t { PLAIN = 0, EXACT_PRED = 1, PLAIN_TIE = 2, EXACT_DONE = 3 };
 static_assert(SPWMAX <= 64, "segment metadata is held one segment per lane");
 static_assert(DCAP <= 127, "slots are stored as int8");
+static_assert(GMAX <= 8 * 64, "the combine holds eight segments per lane");
 }  // namespace fastp
 
 // EXACT segments: exact terms, per-lane inclusive prefixes of their
@@ -82,18 +84,30 @@ struct ExactSlots {
   uint64_t tmask[fastp::DCAP][2];
 };
 
+// A special term whose exact value is an exact half-integer of its grid:
+// its rounding follows the parity of the running integer just before it.
+struct TieRec {
+  uint32_t pos;  // position in the row
+  uint32_t pre;  // integer sum of the segment's terms before it (exact roundings, ties down)
+  uint32_t k;    // its rounding, down
+};
+
 struct FastShared {
   union {
     float data[fastp::W][fastp::KL][fastp::SEG];  // LDS-resident segments (q), phases L and S
     ExactSlots x;                                 // after phase S
   } u;
-  float aseg[fastp::GMAX];                      // segment sums of q
+  union {
+    float aseg[fastp::GMAX];                    // segment sums of q (phases L, M)
+    TieRec tie[fastp::TCAP];                    // after phase M
+  } v;
   uint32_t ssum[fastp::GMAX];                   // PLAIN: integer sum on grid sj
   int8_t sj[fastp::GMAX];                       // PLAIN: its binade; EXACT: first binade tabulated
   uint8_t sflag[fastp::GMAX];
   int8_t sdump[fastp::GMAX];                    // EXACT: slot in `dump`, or -1
   uint32_t qpos[fastp::W][fastp::QCAP];         // special queue: position
-  float qq[fastp::W][fastp::QCAP];              //   and its estimate q
+  uint32_t qpre[fastp::W][fastp::QCAP];         //   and its segment's integer sum before it (lower bracket)
+  int16_t slotseg[fastp::DCAP];                 // segment held by each EXACT slot
   float mw[fastp::W];
   float cw[fastp::W];
   uint32_t nanw[fastp::W];
@@ -101,6 +115,8 @@ struct FastShared {
   uint32_t wflag[fastp::W]; //   bit 0: not certifiable, bit 1: candidate flood
   int wnex[fastp::W];       //   number of its EXACT segments
   uint32_t ncand;
+  uint32_t ntie;
+  int nslot;      // EXACT slots in use this round
   uint32_t fail;
   uint32_t flood;
   int next_g;     // combine: first segment not consumed yet

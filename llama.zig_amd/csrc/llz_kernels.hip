@@ -748,6 +748,28 @@ __global__ __launch_bounds__(kNT) void k_norm(RowParams P, RowPtrs Q) {
   }
 }
 
+// Rare paths of k_select, out of line so that the common path's register
+// allocation stays small.
+
+struct NormResult {
+  float S, m;
+  int bank;
+};
+
+// The streaming normaliser (sampler.zig:83-88) for a row k_stats could not
+// certify; fills the candidate list in LDS.
+__device__ __noinline__ NormResult select_norm_fallback(const RowParams P, const float* xr, SampleShared& sh,
+                                                        int bank, float m_known) {
+  if (threadIdx.x == 0) sh.cand_count = 0;
+  NormResult r;
+  r.S = row_normaliser(xr, P.n, nullptr, P, sh, bank, r.m, m_known);
+  r.bank = bank;
+  return r;
+}
+
+__device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q, SampleShared& sh, int bank,
+                                             float m, float S, uint32_t path);
+
 __global__ __launch_bounds__(kNT) void k_select(RowParams P, RowPtrs Q) {
   __shared__ SampleShared sh;
   int bank = 0;
@@ -766,10 +788,10 @@ __global__ __launch_bounds__(kNT) void k_select(RowParams P, RowPtrs Q) {
   if (rsn[3] != 0.0f) {
     // k_stats could not certify this row: the streaming normaliser
     // (sampler.zig:83-88) fills the candidate list in LDS
-    if (t == 0) sh.cand_count = 0;
-    float m2;
-    S = row_normaliser(xr, n, nullptr, P, sh, bank, m2, m);
-    m = m2;
+    const NormResult r = select_norm_fallback(P, xr, sh, bank, m);
+    S = r.S;
+    m = r.m;
+    bank = r.bank;
     path |= kPathNormFallback;
   } else {
     const uint32_t cc_in = __float_as_uint(rsn[2]);
@@ -931,6 +953,24 @@ __global__ __launch_bounds__(kNT) void k_select(RowParams P, RowPtrs Q) {
   }
 
   // ---- full-row fallback: every probability, stable radix sort, filters
+  select_full_row(P, Q, sh, bank, m, S, path);
+}
+
+// The full-row fallback of k_select: every probability, stable radix sort of
+// the whole row in the workspace, the filters and the draw over it.
+__device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q, SampleShared& sh, int bank,
+                                             float m, float S, uint32_t path) {
+  const int row = blockIdx.x;
+  const int t = (int)threadIdx.x;
+  const int n = P.n;
+  const bool t1 = (P.flags & kFlagTIsOne) != 0;
+  const bool vec = (P.flags & kFlagVecSrc) != 0;
+  const float* xr = Q.src + (int64_t)row * P.src_stride;
+  const bool typical = P.typical_p > 0.0f && P.typical_p < 1.0f;
+  const float u = Q.uniforms[row];
+  int K = 0;
+  float H = 0.0f, total = 0.0f;
+  uint32_t token = 0, consumed = 0;
   path |= kPathFallback;
   if (!(P.flags & kFlagFallback)) {
     if (t == 0) {

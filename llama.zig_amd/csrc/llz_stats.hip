@@ -20,25 +20,6 @@ using namespace fastp;
 constexpr float kInfS = __builtin_inff();
 
 
-// d[k] for a wave-uniform runtime k: every case reads a fixed register.
-__device__ __forceinline__ float4 pick(const float4 (&d)[KV], int k) {
-  float4 r = d[0];
-  switch (k) {
-#define LLZ_PICK(i) \
-  case i:           \
-    r = d[i];       \
-    break;
-    LLZ_PICK(0) LLZ_PICK(1) LLZ_PICK(2) LLZ_PICK(3) LLZ_PICK(4) LLZ_PICK(5) LLZ_PICK(6) LLZ_PICK(7)
-    LLZ_PICK(8) LLZ_PICK(9) LLZ_PICK(10) LLZ_PICK(11) LLZ_PICK(12) LLZ_PICK(13) LLZ_PICK(14) LLZ_PICK(15)
-    LLZ_PICK(16) LLZ_PICK(17) LLZ_PICK(18) LLZ_PICK(19) LLZ_PICK(20) LLZ_PICK(21) LLZ_PICK(22) LLZ_PICK(23)
-    LLZ_PICK(24) LLZ_PICK(25) LLZ_PICK(26) LLZ_PICK(27) LLZ_PICK(28) LLZ_PICK(29) LLZ_PICK(30) LLZ_PICK(31)
-    LLZ_PICK(32) LLZ_PICK(33) LLZ_PICK(34) LLZ_PICK(35) LLZ_PICK(36) LLZ_PICK(37) LLZ_PICK(38) LLZ_PICK(39)
-    LLZ_PICK(40) LLZ_PICK(41) LLZ_PICK(42) LLZ_PICK(43) LLZ_PICK(44)
-#undef LLZ_PICK
-  }
-  return r;
-}
-static_assert(KV == 45, "pick() covers 45 register segments");
 
 __device__ __forceinline__ float wave_incl_scan_f32(float v) {
   return __uint_as_float(wave_incl_scan_op(__float_as_uint(v), 0u, [](uint32_t a, uint32_t b) {
@@ -102,35 +83,29 @@ __device__ __forceinline__ float4 q_of(float4 v, float l2e_t, float cw) {
 }
 
 __device__ __forceinline__ float max4(float4 v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
-__device__ __forceinline__ uint32_t nan4(float4 v) {
-  return (uint32_t)((v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w));
-}
 
 __device__ __forceinline__ void push_cand(FastShared& F, const RowPtrs& Q, int row, float e, uint32_t id) {
   const uint32_t slot = atomicAdd(&F.ncand, 1u);
   if (slot < (uint32_t)kCandCap) Q.cand[(int64_t)row * kCandCap + slot] = ((uint64_t)__float_as_uint(e) << 32) | id;
 }
 
-// Owner wave: its EXACT segments that hold a dump slot, at or after g_from,
-// as a bit mask over the wave's segments (bit k: segment seg0 + k).
-__device__ __forceinline__ uint64_t exact_mask(const FastShared& F, int seg0, int nseg_w, int g_from) {
-  const int lane = lane_id();
-  const int seg = seg0 + lane;
-  const bool ex = lane < nseg_w && seg >= g_from && F.sflag[seg] != PLAIN && F.sdump[seg] >= 0;
-  return __ballot(ex);
+// EXACT slots are spread over the waves: wave w owns slots w, w + W, ...
+
+// Issue the re-reads of this wave's EXACT slots into their dump areas (the
+// caller waits for them).
+template <bool FASTLD>
+__device__ __forceinline__ void exact_loads(FastShared& F, const float* xr, int w, int nslot, int n) {
+  for (int slot = w; slot < nslot; slot += W) seg_to_lds(xr, F.slotseg[slot], n, FASTLD, &F.u.x.dump[slot][0]);
 }
 
-// Owner wave: exact terms of the EXACT segments in `mask` (their loads were
-// issued and waited for by the caller), their candidates, and the per-lane
-// prefix tables of the roundings on grids sj and sj+1.
-__device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int seg0,
-                                               uint64_t mask, int n, float m, float theta, bool t1) {
+// Exact terms of this wave's EXACT slots (loaded and waited for), their
+// candidates (once per segment), and the per-lane inclusive prefix tables of
+// the roundings on grids sj and sj+1 with the lanes holding a tie.
+__device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
+                                               int nslot, int n, float m, float theta, bool t1) {
   const int lane = lane_id();
-  while (mask != 0ull) {
-    const int k = __ffsll((long long)mask) - 1;
-    mask &= mask - 1ull;
-    const int seg = seg0 + k;
-    const int slot = F.sdump[seg];
+  for (int slot = w; slot < nslot; slot += W) {
+    const int seg = F.slotseg[slot];
     const bool pred = F.sflag[seg] == EXACT_PRED;
     float4* p = reinterpret_cast<float4*>(&F.u.x.dump[slot][lane * 4]);
     const float4 v = *p;
@@ -162,41 +137,47 @@ __device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, 
   }
 }
 
-// Owner wave: issue the re-reads of the EXACT segments in `mask` into their slots.
-template <bool FASTLD>
-__device__ __forceinline__ void exact_loads(FastShared& F, const float* xr, int seg0, uint64_t mask, int n) {
-  while (mask != 0ull) {
-    const int k = __ffsll((long long)mask) - 1;
-    mask &= mask - 1ull;
-    const int seg = seg0 + k;
-    seg_to_lds(xr, seg, n, FASTLD, &F.u.x.dump[F.sdump[seg]][0]);
-  }
-}
-
 // Combine wave: the exact sequential sum across EXACT segment `slot` from
 // the running value s, using the prefix tables (grids J0, J0+1) between
 // events and replaying the lane that holds an event term by term.
 __device__ __forceinline__ float resolve_exact(float s, int slot, int J0, const FastShared& F) {
   const int lane = lane_id();
   const float4 e4 = *reinterpret_cast<const float4*>(&F.u.x.dump[slot][lane * 4]);
+  const uint32_t pv0 = F.u.x.pref[slot][0][lane];
+  const uint32_t pv1 = F.u.x.pref[slot][1][lane];
+  const uint64_t tm0 = F.u.x.tmask[slot][0];
+  const uint64_t tm1 = F.u.x.tmask[slot][1];
   int p = 0;  // first lane not consumed
   for (int guard = 0; guard <= kWave && p < kWave; ++guard) {
     const Grid gr = grid_of(s);
     const int k = gr.j - J0;
-    if (k < 0 || k > 1) {
-      // outside the tabulated grids: the generic exact accumulation
+    if (k < 0) {
+      // below the tabulated grids (the row's first segment starts at 0, so
+      // its running sum climbs through many binades): term by term until the
+      // running sum reaches grid J0
+      do {
+        s = s + readlane_f32(e4.x, p);
+        s = s + readlane_f32(e4.y, p);
+        s = s + readlane_f32(e4.z, p);
+        s = s + readlane_f32(e4.w, p);
+        ++p;
+      } while (p < kWave && grid_of(s).j < J0);
+      continue;
+    }
+    if (k > 1) {
+      // above them: the generic exact accumulation
       const float x[4] = {lane >= p ? e4.x : -0.0f, lane >= p ? e4.y : -0.0f, lane >= p ? e4.z : -0.0f,
                           lane >= p ? e4.w : -0.0f};
       return wave_accumulate<4>(s, x);
     }
-    const uint32_t pv = F.u.x.pref[slot][k][lane];
-    const uint32_t base = p > 0 ? F.u.x.pref[slot][k][p - 1] : 0u;
+    const uint32_t pv = k == 0 ? pv0 : pv1;
+    const uint32_t base = p > 0 ? readlane_u32(pv, p - 1) : 0u;
     const uint64_t live = p == 0 ? ~0ull : (~0ull << p);
     const bool cr = lane >= p && (pv >= kSat || gr.N + (pv - base) >= kGridTop);
-    const uint64_t ev = (__ballot(cr) | F.u.x.tmask[slot][k]) & live;
-    if (ev == 0ull) return grid_value(gr.N + (F.u.x.pref[slot][k][kWave - 1] - base), gr.j);
+    const uint64_t ev = (__ballot(cr) | (k == 0 ? tm0 : tm1)) & live;
+    if (ev == 0ull) return grid_value(gr.N + (readlane_u32(pv, kWave - 1) - base), gr.j);
     const int E = __ffsll((long long)ev) - 1;
-    if (E > p) s = grid_value(gr.N + (F.u.x.pref[slot][k][E - 1] - base), gr.j);
+    if (E > p) s = grid_value(gr.N + (readlane_u32(pv, E - 1) - base), gr.j);
     // the lane holding the event, term by term (sampler.zig:87)
     s = s + readlane_f32(e4.x, E);
     s = s + readlane_f32(e4.y, E);
@@ -205,6 +186,92 @@ __device__ __forceinline__ float resolve_exact(float s, int slot, int J0, const 
     p = E + 1;
   }
   return s;
+}
+
+// Combine wave: the units that the ties of PLAIN_TIE segment g add to its
+// integer sum when the segment starts at N on its grid.  Each tie rounds to
+// even: up when the running integer before it plus its rounding down is odd.
+// Returns false when the records cannot be read (more than one wave's worth).
+__device__ __forceinline__ bool tie_bump(const FastShared& F, int g, uint32_t N, uint32_t& bump) {
+  const int lane = lane_id();
+  const int nt = (int)F.ntie;
+  if (nt > kWave) return false;
+  bool mine = false;
+  TieRec tr{0u, 0u, 0u};
+  if (lane < nt) {
+    tr = F.v.tie[lane];
+    mine = (int)(tr.pos >> 8) == g;
+  }
+  bump = 0;
+  while (__ballot(mine) != 0ull) {  // in position order
+    const uint32_t pmin = wave_min_u32(mine ? tr.pos : 0xffffffffu);
+    const bool me = mine && tr.pos == pmin;
+    const int L = __ffsll((long long)__ballot(me)) - 1;
+    const uint32_t pre = readlane_u32(tr.pre, L), k = readlane_u32(tr.k, L);
+    if (((N + pre + bump + k) & 1u) != 0u) ++bump;
+    mine = mine && !me;
+  }
+  return true;
+}
+
+// Owner wave: settle its queued specials (v2: their re-read logits, entry
+// h * 64 + lane): exact terms, corrections of the segment sums, candidates,
+// and a record per tie.  A segment's specials are always queued and settled
+// together, so the integer sum before a tie is its lower-bracket prefix plus
+// the corrections of the specials before it in the same segment.
+__device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
+                                                int qn, const float (&v2)[2], float Rw, float cw, float m,
+                                                float theta, bool t1) {
+  const int lane = lane_id();
+  uint32_t pos2[2], pre2[2], d2[2], r2[2];
+  bool act2[2], tie2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = h * kWave + lane;
+    act2[h] = i < qn;
+    pos2[h] = act2[h] ? F.qpos[w][i] : 0u;
+    pre2[h] = act2[h] ? F.qpre[w][i] : 0u;
+    d2[h] = 0u;
+    r2[h] = 0u;
+    tie2[h] = false;
+    if (act2[h]) {
+      const int seg = (int)(pos2[h] >> 8);
+      const int j = F.sj[seg];
+      const GridConst gc = grid_const(j, Rw, theta);
+      const float q = __builtin_amdgcn_exp2f(fmaf(v2[h], P.l2e_t, -cw));  // phase L's estimate, bit for bit
+      const uint32_t rl = __float_as_uint(fmaf(q, gc.sc_lo, MAGIC)) - MAGIC_BITS;
+      const float e = exact_term(v2[h], m, P.temperature, t1);
+      bool tie;
+      r2[h] = grid_round(e, j, tie);
+      tie2[h] = tie;
+      d2[h] = r2[h] - rl;
+      atomicAdd(&F.ssum[seg], d2[h]);
+      if (e >= theta) push_cand(F, Q, row, e, pos2[h]);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint64_t tb = __ballot(tie2[h]);
+    while (tb != 0ull) {  // ties are rare
+      const int L = __ffsll((long long)tb) - 1;
+      tb &= tb - 1ull;
+      const uint32_t pt = readlane_u32(pos2[h], L);
+      uint32_t c = 0;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+        if (act2[h2] && (pos2[h2] >> 8) == (pt >> 8) && pos2[h2] < pt) c += d2[h2];
+      const uint32_t pre_t = readlane_u32(pre2[h], L) + wave_sum_u32(c);
+      const uint32_t k_t = readlane_u32(r2[h], L);
+      if (lane == 0) {
+        const uint32_t slot = atomicAdd(&F.ntie, 1u);
+        if (slot < (uint32_t)TCAP)
+          F.v.tie[slot] = TieRec{pt, pre_t, k_t};
+        else
+          atomicOr(&F.fail, 1u);
+        F.sflag[pt >> 8] = PLAIN_TIE;
+      }
+    }
+  }
 }
 
 // FASTLD: 16-byte aligned rows with n % 4 == 0 (one float4 per lane per
@@ -222,9 +289,10 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   const int G = (n + SEG - 1) / SEG;
   const int SPW = (G + W - 1) / W;
   const bool fits = SPW <= SPWMAX && P.cand_theta > 0.0f && fabsf(l2e_t) <= 0x1p40f;
-  const int seg0 = w * SPW;
-  const int nseg_w = fits ? max(0, min(SPW, G - seg0)) : 0;
-  const int base_w = seg0 * SEG + lane * 4;
+  // wave w owns segments w, w + W, w + 2W, ...: its k-th is segment w + W k
+  // (interleaved, so the costly start of the row is shared by every wave)
+  const int nseg_w = fits ? max(0, (G - w + W - 1) / W) : 0;
+  const int base_w = w * SEG + lane * 4;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
   float* rs_out = Q.row_state + (int64_t)row * 4;
 
@@ -241,23 +309,23 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     for (int k = KV; k < SPWMAX; ++k) {
       int kk = k;
       asm volatile("" : "+s"(kk));
-      const bool full = kk < nseg_w && (seg0 + kk + 1) * SEG <= n;
-      dma16(xr + (full ? base_w + kk * SEG : lane * 4),
+      const bool full = kk < nseg_w && (w + W * kk + 1) * SEG <= n;
+      dma16(xr + (full ? base_w + kk * (W * SEG) : lane * 4),
             (uint32_t)__builtin_amdgcn_readfirstlane((int)(uintptr_t)&F.u.data[w][k - KV][0]));
     }
     // register segments: one shared lane offset, the segment offset in an
     // SGPR; reads past the row return 0
     const llz_i4v rs = row_rsrc(xr, (uint32_t)n * 4u);
-    const int soff = __builtin_amdgcn_readfirstlane(seg0 * SEG * 4);
+    const int soff = __builtin_amdgcn_readfirstlane(w * SEG * 4);
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
-      d[k] = buf_ld4(rs, lane * 16, soff + k * SEG * 4);
+      d[k] = buf_ld4(rs, lane * 16, soff + k * (W * SEG * 4));
       __builtin_amdgcn_sched_barrier(0);  // keep the issue order: segment k lands k-th
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < KV; ++k) d[k] = ld1x4(xr, base_w + k * SEG, k < nseg_w ? n : 0);
-    for (int k = KV; k < nseg_w; ++k) seg_to_lds(xr, seg0 + k, n, false, &F.u.data[w][k - KV][0]);
+    for (int k = 0; k < KV; ++k) d[k] = ld1x4(xr, base_w + k * (W * SEG), k < nseg_w ? n : 0);
+    for (int k = KV; k < nseg_w; ++k) seg_to_lds(xr, w + W * k, n, false, &F.u.data[w][k - KV][0]);
   }
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before any use
 
@@ -267,9 +335,9 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   // limits are recomputed in place (an empty asm keeps the compiler from
   // hoisting 45 of them into live registers)
   const int lane4 = lane * 4;
-  const int lim_w = min(n - seg0 * SEG, nseg_w * SEG);  // this wave's positions < lim_w
+  const int lim_w = nseg_w > 0 ? n - w * SEG : 0;  // segment k holds positions lane4 < lim_w - k W SEG
   auto seg_lim = [&](int k) {
-    int l = lim_w - k * SEG;
+    int l = k < nseg_w ? lim_w - k * (W * SEG) : 0;
     asm volatile("" : "+s"(l));
     return l;
   };
@@ -299,13 +367,13 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     my_a = lane == k ? a : my_a;
     __builtin_amdgcn_sched_barrier(0);  // one segment at a time: bounded live ranges
   }
-  if (lane < min(nseg_w, KV)) F.aseg[seg0 + lane] = my_a;
+  if (lane < min(nseg_w, KV)) F.v.aseg[w + W * lane] = my_a;
   nanf = (lane < min(nseg_w, KV) && my_a != my_a) ? 1u : 0u;
   if (nseg_w > KV) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (FASTLD && (seg0 + nseg_w) * SEG > n) {  // the row's partial last segment
+    if (FASTLD && (w + W * (nseg_w - 1) + 1) * SEG > n) {  // the row's partial last segment
       const int k = nseg_w - 1;
-      *reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]) = ld4(xr, base_w + k * SEG, n);
+      *reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]) = ld4(xr, base_w + k * (W * SEG), n);
     }
   }
   for (int k = KV; k < nseg_w; ++k) {
@@ -315,7 +383,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     const float4 q = q_of(v, l2e_t, cw);
     *p = q;
     const float a = wave_sum_f32((q.x + q.y) + (q.z + q.w));
-    if (lane == 0) F.aseg[seg0 + k] = a;
+    if (lane == 0) F.v.aseg[w + W * k] = a;
     nanf |= a != a ? 1u : 0u;
   }
   if (!fits) {  // rows the fast path does not take: maximum and NaN scan only
@@ -336,6 +404,8 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     F.fail = fits ? 0u : 1u;
     F.flood = 0;
     F.ncand = 0;
+    F.ntie = 0;
+    F.nslot = 0;
     F.next_g = 0;
     F.s_run = 0.0f;
     F.done = 0;
@@ -362,28 +432,32 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   }
   const float aw = fmaf(m, -l2e_t, cw);
   const float Rw = __builtin_amdgcn_exp2f(aw);  // q * Rw ~ e = exp((v - m) / T)
-  // each wave predicts its own segments (one per lane); wave totals give the carries
+  // Prediction in index order: lane k takes round k (segments W k .. W k +
+  // W - 1, one per wave, each scaled by its wave's R); a scan over the rounds
+  // gives every segment's running sum.  Every wave computes it for its own
+  // segments (the lane's segment of this wave is W k + w).
   const bool have = lane < nseg_w;
   {
-    const float a_l = have ? F.aseg[seg0 + lane] * Rw : 0.0f;
-    const float sc = wave_incl_scan_f32(a_l);
-    const float tot = __uint_as_float(lane_readlast(__float_as_uint(sc)));
-    const bool badw = (nseg_w > 0 && !(fabsf(aw) <= 32.0f)) || !(tot <= 3.0e38f);
-    if (lane == 0) {
-      F.wtot[w] = tot;
-      F.wflag[w] = badw ? 1u : 0u;
-    }
-    __syncthreads();
-    float carry = 0.0f;
+    float rtot = 0.0f, before_w = 0.0f, b_w = 0.0f;
     bool bad = false;
+#pragma unroll
     for (int i = 0; i < W; ++i) {
-      if (i < w) carry += F.wtot[i];
-      bad = bad || (F.wflag[i] & 1u) != 0u;
+      const float awi = fmaf(m, -l2e_t, F.cw[i]);
+      bad = bad || ((G > i) && !(fabsf(awi) <= 32.0f));
+      const int g = W * lane + i;
+      const float b = g < G ? F.v.aseg[g] * __builtin_amdgcn_exp2f(awi) : 0.0f;
+      rtot += b;
+      before_w += i < w ? b : 0.0f;
+      b_w = i == w ? b : b_w;
     }
+    const float rin = wave_incl_scan_f32(rtot);
+    const float rex = __uint_as_float(wave_shift_up1(__float_as_uint(rin)));
+    const float total = __uint_as_float(lane_readlast(__float_as_uint(rin)));
+    bad = bad || !(total <= 3.0e38f);
     bool ex = false, fl = false;
     if (!bad && have) {
-      const float incl = carry + sc;
-      const float excl = carry + __uint_as_float(wave_shift_up1(__float_as_uint(sc)));
+      const float excl = rex + before_w;
+      const float incl = excl + b_w;
       const float lo = excl * (1.0f - DELTA), hi = incl * (1.0f + DELTA);
       const int elo = (int)(__float_as_uint(lo) >> 23) - 127;
       const int ehi = (int)(__float_as_uint(hi) >> 23) - 127;
@@ -392,31 +466,25 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       // EXACT: tabulate the binade the segment starts in and the next one
       int j0 = lo >= 0x1p-126f ? elo : ehi - 1;
       j0 = max(-126, min(j0, 126));
-      F.sflag[seg0 + lane] = plain ? PLAIN : EXACT_PRED;
-      F.sj[seg0 + lane] = (int8_t)(plain ? elo : j0);
+      const int g = w + W * lane;
+      F.sflag[g] = plain ? PLAIN : EXACT_PRED;
+      F.sj[g] = (int8_t)(plain ? elo : j0);
       ex = !plain;
     }
+    // EXACT slots (any order; a row with more than DCAP takes further rounds in index order)
     const uint64_t exm = __ballot(ex);
-    const bool flw = __ballot(fl) != 0ull;
-    __syncthreads();  // every wave has read wtot/wflag
+    int base = 0;
     if (lane == 0) {
-      F.wnex[w] = __popcll(exm);
-      F.wflag[w] = (bad ? 1u : 0u) | (flw ? 2u : 0u);
+      if (exm != 0ull) base = (int)atomicAdd((uint32_t*)&F.nslot, (uint32_t)__popcll(exm));
+      if (bad) atomicOr(&F.fail, 1u);
+      if (__ballot(fl) != 0ull) atomicOr(&F.flood, 1u);
     }
-    __syncthreads();
-    int before = 0;
-    bool flood_any = false;
-    for (int i = 0; i < W; ++i) {
-      if (i < w) before += F.wnex[i];
-      flood_any = flood_any || (F.wflag[i] & 2u) != 0u;
-    }
+    base = __builtin_amdgcn_readfirstlane(base);
     if (have) {
-      const int slot = before + __popcll(exm & lt_mask);
-      F.sdump[seg0 + lane] = (int8_t)(ex && slot < DCAP ? slot : -1);
-    }
-    if (t == 0) {
-      if (bad) F.fail = 1u;
-      F.flood = flood_any ? 1u : 0u;
+      const int slot = base + __popcll(exm & lt_mask);
+      const bool got = ex && slot < DCAP;
+      F.sdump[w + W * lane] = (int8_t)(got ? slot : -1);
+      if (got) F.slotseg[slot] = (int16_t)(w + W * lane);
     }
   }
   __syncthreads();
@@ -424,47 +492,30 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   const float theta = flood ? kInfS : P.cand_theta;
 
   // ---- phase S: integer sums of PLAIN segments, four segments per step;
-  // specials queued (and flushed when the queue is full)
+  // specials queued with the segment's integer sum before them (lower
+  // bracket), and settled when the queue is full
   int qn = 0;
-  // re-read the queued logits, evaluate them exactly, correct the sums
-  auto flush = [&]() {
-    uint32_t pos2[2];
-    float v2[2], q2[2];
-    bool act2[2];
+  float v2[2];
+  auto reread = [&]() {  // the queued logits (wave-uniform count qn)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int i = h * kWave + lane;
-      act2[h] = i < qn;
-      pos2[h] = act2[h] ? F.qpos[w][i] : 0u;
-      q2[h] = act2[h] ? F.qq[w][i] : 0.0f;
-      v2[h] = xr[pos2[h]];
+      v2[h] = xr[i < qn ? F.qpos[w][i] : 0u];
     }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (act2[h]) {
-        const int seg = (int)(pos2[h] >> 8);
-        const int j = F.sj[seg];
-        const GridConst gc = grid_const(j, Rw, theta);
-        const uint32_t rl = __float_as_uint(fmaf(q2[h], gc.sc_lo, MAGIC)) - MAGIC_BITS;
-        const float e = exact_term(v2[h], m, P.temperature, t1);
-        bool tie;
-        const uint32_t r = grid_round(e, j, tie);
-        atomicAdd(&F.ssum[seg], r - rl);
-        if (tie) F.sflag[seg] = EXACT_TIE;
-        if (e >= theta) push_cand(F, Q, row, e, pos2[h]);
-      }
-    }
+  };
+  auto settle = [&]() {
+    settle_specials(F, Q, P, row, w, qn, v2, Rw, cw, m, theta, t1);
     qn = 0;
   };
   bool qovf = false;
   if (!F.fail) {
-    const uint32_t flag_l = have ? (uint32_t)F.sflag[seg0 + lane] : (uint32_t)EXACT_PRED;
-    const int j_l = have ? (int)F.sj[seg0 + lane] : 0;
+    const uint32_t flag_l = have ? (uint32_t)F.sflag[w + W * lane] : (uint32_t)EXACT_PRED;
+    const int j_l = have ? (int)F.sj[w + W * lane] : 0;
     const GridConst gc_l = grid_const(j_l, Rw, theta);
-    int seg0_s = seg0, n_s = n;
-    asm volatile("" : "+s"(seg0_s), "+s"(n_s));  // recompute phase-L expressions instead of keeping them
     auto lds_q = [&](int k) {
-      return *reinterpret_cast<const float4*>(&F.u.data[w][min(max(k - KV, 0), KL - 1)][lane * 4]);
+      int l4 = lane_id() * 4;
+      asm volatile("" : "+v"(l4));  // recomputed here rather than kept live through the loop
+      return *reinterpret_cast<const float4*>(&F.u.data[w][min(max(k - KV, 0), KL - 1)][l4]);
     };
     for (int k0 = 0; k0 < nseg_w; k0 += 4) {
       llz_f4v qa, qb, qc, qd;  // native vectors: an array or HIP's float4 struct here ends up in scratch
@@ -487,7 +538,9 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           qc = to_v4(lds_q(k0 + 2));
           qd = to_v4(lds_q(k0 + 3));
       }
-      uint32_t r4[4], spm = 0;
+      // per segment s: w1..w3 = the lane's integer sums before its elements
+      // 1..3, acc = the lane's sum, incl = the inclusive scan over lanes
+      uint32_t acc4[4], incl4[4], wa[4], wb[4], wc[4], spm = 0;
       bool pl4[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -497,48 +550,59 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         const float sc_lo = readlane_f32(gc_l.sc_lo, kl);
         const float sc_hi = readlane_f32(gc_l.sc_hi, kl);
         const float tspec = readlane_f32(gc_l.tspec, kl);
-        const int lim = n_s - (seg0_s + k) * SEG;  // positions lane4 + c < lim are present
         const llz_f4v qv4 = s == 0 ? qa : s == 1 ? qb : s == 2 ? qc : qd;  // s is a constant here
         const float qs[4] = {qv4.x, qv4.y, qv4.z, qv4.w};
-        uint32_t acc = 0, sp = 0;
+        uint32_t b[4], sp = 0;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const float rlo = fmaf(qs[c], sc_lo, MAGIC);
           const float rhi = fmaf(qs[c], sc_hi, MAGIC);
-          acc += __float_as_uint(rlo);
+          b[c] = __float_as_uint(rlo);
           sp |= (rlo != rhi || rhi >= tspec) ? (1u << c) : 0u;
         }
-        if (lim < SEG) sp &= (1u << max(0, min(4, lim - lane4))) - 1u;  // absent positions
+        // absent positions hold q = 0, so rlo = rhi = MAGIC: never special
+        // (tspec > MAGIC for PLAIN segments outside flood mode, and theta is
+        // +inf in flood mode)
+        wa[s] = b[0] - MAGIC_BITS;
+        wb[s] = wa[s] + b[1] - MAGIC_BITS;
+        wc[s] = wb[s] + b[2] - MAGIC_BITS;
+        acc4[s] = wc[s] + b[3] - MAGIC_BITS;
         if (!pl4[s]) sp = 0;
         spm |= sp << (4 * s);
-        r4[s] = acc - 4u * MAGIC_BITS;
       }
 #pragma unroll
-      for (int s = 0; s < 4; ++s) r4[s] = wave_sum_u32(r4[s]);
-      if (lane == 0) {
+      for (int s = 0; s < 4; ++s)
+        incl4[s] = wave_incl_scan_op(acc4[s], 0u, [](uint32_t a, uint32_t b) { return a + b; });
+      if (lane == kWave - 1) {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          if (pl4[s]) F.ssum[seg0 + k0 + s] = r4[s];
+          if (pl4[s]) F.ssum[w + W * (k0 + s)] = incl4[s];
       }
       if (__ballot(spm != 0u) != 0ull) {
         // every lane appends its own specials after those of the lanes below it
         const uint32_t my = (uint32_t)__popc(spm);
         const uint32_t incl = wave_incl_scan_op(my, 0u, [](uint32_t a, uint32_t b) { return a + b; });
         const int total = (int)lane_readlast(incl);
-        if (qn + total > QCAP) flush();
+        if (qn + total > QCAP) {
+          reread();
+          settle();
+        }
         if (total > QCAP) {
           qovf = true;  // more specials in four segments than the queue holds
         } else {
           int slot = qn + (int)(incl - my);
           uint32_t rem = spm;
           while (rem != 0u) {
-            const int b = __ffs(rem) - 1;
+            const int bt = __ffs(rem) - 1;
             rem &= rem - 1u;
-            const int s = b >> 2, c = b & 3;
-            const llz_f4v qs4 = s == 0 ? qa : s == 1 ? qb : s == 2 ? qc : qd;
-            const float qv = c == 0 ? qs4.x : c == 1 ? qs4.y : c == 2 ? qs4.z : qs4.w;
-            F.qpos[w][slot] = (uint32_t)((seg0 + k0 + s) * SEG + lane4 + c);
-            F.qq[w][slot] = qv;
+            const int s = bt >> 2, c = bt & 3;
+            const uint32_t ex_s = s == 0 ? incl4[0] - acc4[0] : s == 1 ? incl4[1] - acc4[1]
+                                : s == 2 ? incl4[2] - acc4[2] : incl4[3] - acc4[3];
+            const uint32_t wa_s = s == 0 ? wa[0] : s == 1 ? wa[1] : s == 2 ? wa[2] : wa[3];
+            const uint32_t wb_s = s == 0 ? wb[0] : s == 1 ? wb[1] : s == 2 ? wb[2] : wb[3];
+            const uint32_t wc_s = s == 0 ? wc[0] : s == 1 ? wc[1] : s == 2 ? wc[2] : wc[3];
+            F.qpos[w][slot] = (uint32_t)((w + W * (k0 + s)) * SEG + lane4 + c);
+            F.qpre[w][slot] = ex_s + (c == 0 ? 0u : c == 1 ? wa_s : c == 2 ? wb_s : wc_s);
             ++slot;
           }
           qn += total;
@@ -548,45 +612,22 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     if (qovf && lane == 0) atomicOr(&F.fail, 1u);
   }
 
-  // ---- phase F+X: the remaining specials and the first EXACT slots in one
-  // round trip (the slots overlay the LDS-resident segments: every wave is
-  // past phase S)
+  // ---- phase F+X: the remaining specials and this round's EXACT slots in
+  // one round trip (the slots overlay the LDS-resident segments: every wave
+  // is past phase S)
   __syncthreads();
   if (!F.fail) {
-    uint32_t pos2[2];
-    float v2[2], q2[2];
-    bool act2[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = h * kWave + lane;
-      act2[h] = i < qn;
-      pos2[h] = act2[h] ? F.qpos[w][i] : 0u;
-      q2[h] = act2[h] ? F.qq[w][i] : 0.0f;
-      v2[h] = xr[pos2[h]];
-    }
-    const uint64_t emask = exact_mask(F, seg0, nseg_w, 0);
-    exact_loads<FASTLD>(F, xr, seg0, emask, n);
+    reread();
+    const int nslot = min(F.nslot, DCAP);
+    exact_loads<FASTLD>(F, xr, w, nslot, n);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (act2[h]) {
-        const int seg = (int)(pos2[h] >> 8);
-        const int j = F.sj[seg];
-        const GridConst gc = grid_const(j, Rw, theta);
-        const uint32_t rl = __float_as_uint(fmaf(q2[h], gc.sc_lo, MAGIC)) - MAGIC_BITS;
-        const float e = exact_term(v2[h], m, P.temperature, t1);
-        bool tie;
-        const uint32_t r = grid_round(e, j, tie);
-        atomicAdd(&F.ssum[seg], r - rl);
-        if (tie) F.sflag[seg] = EXACT_TIE;
-        if (e >= theta) push_cand(F, Q, row, e, pos2[h]);
-      }
-    }
-    exact_segments(F, Q, P, row, seg0, emask, n, m, theta, t1);
+    settle();
+    exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
   }
   __syncthreads();
 
-  // ---- phase C: the walk in index order; later EXACT segments in rounds
+  // ---- phase C: the walk in index order; EXACT segments beyond the slots
+  // in further rounds
   for (int round = 0; !F.fail; ++round) {
     const int g_from = F.next_g;
     if (round > 0) {
@@ -594,57 +635,90 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         int cnt = 0;
         for (int b = g_from; b < G; b += kWave) {
           const int g = b + lane;
-          const bool ex = g < G && F.sflag[g] != PLAIN;
+          const bool ex = g < G && (F.sflag[g] == EXACT_PRED || F.sflag[g] == EXACT_DONE);
           const uint64_t mk = __ballot(ex);
           const int slot = cnt + __popcll(mk & lt_mask);
           if (ex) {
             F.sdump[g] = (int8_t)(slot < DCAP ? slot : -1);
+            if (slot < DCAP) F.slotseg[slot] = (int16_t)g;
           }
           cnt += __popcll(mk);
         }
+        if (lane == 0) F.nslot = min(cnt, DCAP);
       }
       __syncthreads();
-      const uint64_t emask = exact_mask(F, seg0, nseg_w, g_from);
-      exact_loads<FASTLD>(F, xr, seg0, emask, n);
+      const int nslot = F.nslot;
+      exact_loads<FASTLD>(F, xr, w, nslot, n);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      exact_segments(F, Q, P, row, seg0, emask, n, m, theta, t1);
+      exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
       __syncthreads();
     }
     if (w == 0) {
       float s = F.s_run;
       int g = g_from;
       bool fail = false, more = false;
-      while (g < G) {
-        const Grid gr = grid_of(s);
-        const int gg = g + lane;
-        bool okp = false;
-        uint32_t sm = 0;
-        if (gg < G) {
-          okp = F.sflag[gg] == PLAIN && (int)F.sj[gg] == gr.j;
-          sm = F.ssum[gg];
+      while (g < G && !fail && !more) {
+        // this group of 64 segments, one per lane
+        const int gb = g & ~(kWave - 1);
+        const int gend = min(gb + kWave, G);
+        const int gg = gb + lane;
+        uint32_t fl = PLAIN, sm = 0;
+        int jj = 0, sd = -1;
+        if (gg < gend) {
+          fl = F.sflag[gg];
+          jj = F.sj[gg];
+          sm = min(F.ssum[gg], kSat);
+          sd = F.sdump[gg];
         }
-        const uint64_t bad = __ballot(!okp);
-        const int fb = bad ? __ffsll((long long)bad) - 1 : kWave;
-        const uint32_t incl = wave_incl_scan_sat(lane < fb ? sm : 0u, kSat);
-        if (__ballot(lane < fb && gr.N + incl >= kGridTop) != 0ull) {
-          fail = true;  // a crossing the prediction did not see
-          break;
-        }
-        if (fb > 0) {
-          s = grid_value(gr.N + readlane_u32(incl, fb - 1), gr.j);
-          g += fb;
-        }
-        if (fb < kWave && g < G) {
-          if (F.sflag[g] == PLAIN) {
+        // inclusive prefix of the group's sums (each <= 2^25: no wrap)
+        const uint32_t pincl = wave_incl_scan_op(sm, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+        while (g < gend) {
+          const Grid gr = grid_of(s);
+          const int p = g - gb;
+          const bool okp = fl == PLAIN && jj == gr.j;
+          const uint64_t bad = __ballot(lane >= p && gg < gend && !okp);
+          const int fb = bad ? __ffsll((long long)bad) - 1 : gend - gb;
+          if (fb > p) {
+            // PLAIN run [p, fb): terms are >= 0, so it stays in the binade
+            // exactly when its total does
+            const uint32_t tot = readlane_u32(pincl, fb - 1) - (p > 0 ? readlane_u32(pincl, p - 1) : 0u);
+            if (gr.N + tot >= kGridTop) {
+              fail = true;  // a crossing the prediction did not see
+              break;
+            }
+            s = grid_value(gr.N + tot, gr.j);
+            g = gb + fb;
+          }
+          if (g >= gend) break;
+          // segment g is an event
+          const uint32_t flg = readlane_u32(fl, fb);
+          const int jg = (int)readlane_u32((uint32_t)jj, fb);
+          if (flg == PLAIN_TIE) {
+            const Grid g2 = grid_of(s);
+            uint32_t bump = 0;
+            if (jg != g2.j || !tie_bump(F, g, g2.N, bump)) {
+              fail = true;
+              break;
+            }
+            const uint32_t tot = g2.N + readlane_u32(sm, fb) + bump;
+            if (tot >= kGridTop) {
+              fail = true;
+              break;
+            }
+            s = grid_value(tot, g2.j);
+            ++g;
+            continue;
+          }
+          if (flg == PLAIN) {
             fail = true;  // the running sum is not in the predicted binade
             break;
           }
-          const int slot = F.sdump[g];
+          const int slot = (int)readlane_u32((uint32_t)sd, fb);
           if (slot < 0 || g < g_from) {
             more = true;
             break;
           }
-          s = resolve_exact(s, slot, F.sj[g], F);
+          s = resolve_exact(s, slot, jg, F);
           ++g;
         }
       }
