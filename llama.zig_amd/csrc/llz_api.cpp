@@ -16,7 +16,7 @@ namespace {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 
-// measurement hook: events recorded around k_sample (see llz_debug_kernel_events)
+// measurement hook: events recorded around the fused sampling kernel (see llz_debug_kernel_events)
 hipEvent_t g_ev_begin = nullptr;
 hipEvent_t g_ev_end = nullptr;
 
@@ -26,7 +26,7 @@ bool penalty_active(const llz_sampler_config* cfg, int32_t n_prev) {
 
 // Workspace layout of one llz_sample_rows call.
 struct Layout {
-  size_t maxpart, status, rstate, cand, penal, fb, fb_mask, total;
+  size_t status, cand, penal, fb, fb_mask, total;
   bool has_penal;
 };
 
@@ -34,9 +34,7 @@ Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int
   Layout L{};
   const size_t r = (size_t)rows, n = (size_t)vocab;
   size_t off = 0;
-  L.maxpart = off; off = align_up(off + r * (size_t)max_parts(vocab) * sizeof(float));
   L.status = off;  off = align_up(off + r * sizeof(uint32_t));
-  L.rstate = off;  off = align_up(off + r * 4 * sizeof(float));
   L.cand = off;    off = align_up(off + r * (size_t)kCandCap * sizeof(uint64_t));
   L.has_penal = penalty_active(cfg, n_prev);
   L.penal = off;   if (L.has_penal) off = align_up(off + r * n * sizeof(float));
@@ -150,7 +148,6 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
     src_stride = vocab;
   }
   const bool vec = ((uintptr_t)src % 16 == 0) && (src_stride % 4 == 0);
-  float* maxpart = (float*)(ws + L.maxpart);
   hipError_t e = hipSuccess;
 
   RowParams P{};
@@ -163,7 +160,6 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   P.l2e_t = (float)(1.4426950408889634 / (double)cfg->temperature);
   P.n = vocab;
   P.rows = rows;
-  P.nparts = max_parts(vocab);
   P.kept_cap = extras ? extras->kept_cap : 0;
   P.src_stride = src_stride;
   P.orig_stride = row_stride;
@@ -172,7 +168,6 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   RowPtrs Q{};
   Q.src = src;
   Q.orig = d_logits;
-  Q.maxpart = maxpart;
   Q.uniforms = d_uniforms;
   Q.tokens = d_tokens;
   Q.consumed = d_consumed;
@@ -184,7 +179,6 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   }
   Q.status = (uint32_t*)(ws + L.status);
   Q.cand = (uint64_t*)(ws + L.cand);
-  Q.row_state = (float*)(ws + L.rstate);
   Q.fb = (uint32_t*)(ws + L.fb);
   Q.fb_mask = (uint8_t*)(ws + L.fb_mask);
   e = launch_sample(P, Q, g_ev_begin, g_ev_end, st);

@@ -16,8 +16,8 @@ constexpr uint32_t kFlagFallback = 4u;  // the full-row fallback buffers are pre
 // per-row status bits (diagnostics)
 constexpr uint32_t kPathSumLe0 = 1u;
 constexpr uint32_t kPathEntropy = 2u;
-constexpr uint32_t kPathFallback = 4u;      // full-row radix sort in k_select
-constexpr uint32_t kPathNormFallback = 8u;  // streaming normaliser in k_select
+constexpr uint32_t kPathFallback = 4u;      // full-row radix sort
+constexpr uint32_t kPathNormFallback = 8u;  // streaming normaliser (row not certified by the fast path)
 constexpr uint32_t kPathError = 0x80000000u;
 
 struct RowParams {
@@ -30,7 +30,6 @@ struct RowParams {
   float l2e_t;        // RN(log2(e) / temperature)
   int32_t n;          // vocab
   int32_t rows;
-  int32_t nparts;     // partial maxima per row
   int32_t kept_cap;
   int64_t src_stride;
   int64_t orig_stride;
@@ -41,7 +40,6 @@ struct RowParams {
 struct RowPtrs {
   const float* src;       // rows the chain reads (penalised copy or the caller's)
   const float* orig;      // the caller's rows (sampleArgmax exits)
-  const float* maxpart;   // [rows][nparts]
   const float* uniforms;  // [rows]
   uint32_t* tokens;
   uint8_t* consumed;
@@ -50,21 +48,16 @@ struct RowPtrs {
   float* kept_probs;
   float* row_stats;
   uint32_t* status;
-  uint64_t* cand;         // [rows][kCandCap] candidate list (k_norm -> k_select)
-  float* row_state;       // [rows][4]: max, normaliser, candidate count (bits)
+  uint64_t* cand;         // [rows][kCandCap] candidate list
   uint32_t* fb;           // 6 x [rows][n] u32 (fallback sort buffers)
   uint8_t* fb_mask;       // [rows][n]
 };
 
-int max_parts(int n);
 hipError_t launch_penalty(const float* logits, int64_t stride, int rows, int n, const uint32_t* prev,
                           int n_prev, int64_t prev_stride, int window, float penalty, float* out,
                           hipStream_t st);
-hipError_t launch_rowmax(const float* logits, int64_t stride, int rows, int n, bool vec, float* part,
-                         hipStream_t st);
 hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t* tokens,
                          uint8_t* consumed, uint32_t* kept_count, hipStream_t st);
-hipError_t launch_stats(const RowParams& P, const RowPtrs& Q, hipStream_t st);
 hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_begin, hipEvent_t ev_end,
                          hipStream_t st);
 hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, int64_t n, hipStream_t st);

@@ -1,0 +1,844 @@
+// llz_select.h -- the selection stage of the sampling chain (sampler.zig:89-168):
+// candidate sort by (p desc, id asc), top-k / top-p / min-p, typical-p,
+// total and the draw, with the streaming normaliser and a full-row radix
+// sort as the fallbacks.  Included by the fused per-row kernel only.
+#pragma once
+
+#include "llz_accum.h"
+#include "llz_rowops.h"
+
+namespace llz {
+
+// Shared memory of the selection stage.
+struct PostShared {
+  uint64_t aux[kCap];       // (dev bits, id) for typical-p
+  uint32_t aux_pos[kCap];   // p-order position carried through the dev sort
+  uint8_t keep[kCap];       // final keep flag per p-order position
+  RadixScratch radix;
+};
+
+struct SampleShared {
+  WgScratch<kNT> wg;
+  uint32_t cand_count;
+  uint32_t misc[4];
+  uint64_t cand[kCap];      // (e bits, id) while collecting, then (~p bits, id) sorted
+  union {
+    NormShared<kNT> norm;   // streaming normaliser (rows k_stats could not certify)
+    PostShared post;        // sort, filters and draw
+  } u;
+};
+
+// Candidate list push (e >= theta): (e bits, id), capacity kCap.
+__device__ __forceinline__ void push_candidate(SampleShared& sh, float e, uint32_t id) {
+  const uint32_t slot = atomicAdd(&sh.cand_count, 1u);
+  if (slot < (uint32_t)kCap) sh.cand[slot] = ((uint64_t)__float_as_uint(e) << 32) | id;
+}
+
+// Per-element state of a wave's slice for one base grid jb: wv holds the
+// estimate q = e / 2^(jb-23), or, for special elements (bit set in spec),
+// the exact term e.  Specials are the elements whose rounding is ambiguous
+// in grid jb or jb+1, the large terms, and the candidates, so any rounding in
+// those two grids follows from the state without a new exp.
+struct SliceState {
+  float wv[kSub][kV];
+  uint32_t spec;   // bit c*kV + k
+};
+
+// RN(element / 2^(jj-23)) for jj in {jb, jb+1}; jj = jb + sh (sh = 0 or 1).
+__device__ __forceinline__ uint32_t state_round(float w, bool spec, int jj, int sh, bool& tie) {
+  tie = false;
+  if (spec) return grid_round(w, jj, tie);
+  return (uint32_t)rintf(fminf(sh ? w * 0.5f : w, 32768.0f));
+}
+
+// Sub-chunk sums (c >= c_from) in grid jb + sh from the slice state.
+__device__ __forceinline__ void slice_sums(const SliceState& S, int sb, int n, int jb, int sh, int c_from,
+                                           uint32_t* part) {
+  const int lane = lane_id();
+  uint32_t acc[kSub], tie_c = 0;
+#pragma unroll
+  for (int c = 0; c < kSub; ++c) {
+    acc[c] = 0;
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const int p = sb + c * (kWave * kV) + lane * kV + k;
+      if (c >= c_from && p < n) {
+        bool tie;
+        acc[c] = sat_add(acc[c], state_round(S.wv[c][k], (S.spec >> (c * kV + k)) & 1u, jb + sh, sh, tie), kSat);
+        if (tie) tie_c |= 1u << c;
+      }
+    }
+  }
+  uint32_t sums[kSub];
+#pragma unroll
+  for (int c = 0; c < kSub; ++c) sums[c] = c < c_from ? 0u : wave_sum_sat(acc[c], kSat);
+  uint32_t tie_w = 0;
+#pragma unroll
+  for (int c = 0; c < kSub; ++c) tie_w |= (__ballot((tie_c >> c) & 1u) != 0ull) ? (1u << c) : 0u;
+  if (lane == 0) {
+#pragma unroll
+    for (int c = 0; c < kSub; ++c)
+      if (c >= c_from) part[c] = sums[c] | (((tie_w >> c) & 1u) ? 0x80000000u : 0u);
+  }
+}
+
+// Slice state for base grid jb (sub-chunks c >= c_from), candidates on the
+// first pass.  Exact terms of specials come from a per-wave queue so one
+// rolled loop evaluates them densely.
+__device__ __forceinline__ void slice_state(const float (&v)[kSub][kV], int sb, int n, float m, const RowParams& P,
+                                            bool t1, int jb, bool first_pass, int c_from, SampleShared& sh,
+                                            SliceState& S) {
+  NormShared<kNT>& ns = sh.u.norm;
+  const int lane = lane_id(), w = wave_id();
+  const bool exact_mode = jb < -40;
+  const float cj = (float)(23 - jb);
+  const float qc = (exact_mode || !first_pass) ? (first_pass ? 0.0f : kInf)
+                                               : ldexpf(P.cand_theta, 23 - jb) * (1.0f - 0x1p-14f);
+  S.spec = 0;
+#pragma unroll
+  for (int c = 0; c < kSub; ++c) {
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const int p = sb + c * (kWave * kV) + lane * kV + k;
+      const float q = __builtin_amdgcn_exp2f(fmaf(v[c][k] - m, P.l2e_t, cj));
+      S.wv[c][k] = q;
+      // ambiguous in grid jb or jb+1 (NaN-safe), large, or a candidate
+      const float r0 = rintf(fminf(q, 32768.0f));
+      const float h = q * 0.5f;
+      const float r1 = rintf(fminf(h, 32768.0f));
+      const bool amb = !(fmaf(q, kEps, fabsf(q - r0)) < 0.5f) || !(fmaf(h, kEps, fabsf(h - r1)) < 0.5f);
+      const bool spec = c >= c_from && p < n && (exact_mode || amb || q >= qc);
+      if (spec) S.spec |= 1u << (c * kV + k);
+    }
+  }
+  if (__ballot(S.spec != 0) == 0ull) return;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+  int qn = 0;
+#pragma unroll
+  for (int e = 0; e < kSub * kV; ++e) {
+    const bool sp = (S.spec >> e) & 1u;
+    const uint64_t mk = __ballot(sp);
+    if (sp) {
+      ns.ev[w][e][lane] = v[e / kV][e % kV];
+      const int slot = qn + (int)__popcll(mk & lt);
+      if (slot < kQCap) ns.q[w][slot] = (uint16_t)(e * kWave + lane);
+    }
+    qn += (int)__popcll(mk);
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (qn <= kQCap) {
+    for (int i = lane; i < qn; i += kWave) {
+      const uint32_t slot = ns.q[w][i];
+      const uint32_t el = slot / kWave, ln = slot % kWave;
+      const float x = exact_term(ns.ev[w][el][ln], m, P.temperature, t1);
+      ns.ev[w][el][ln] = x;
+      if (first_pass && x >= P.cand_theta)
+        push_candidate(sh, x, (uint32_t)(sb + (int)(el / kV) * (kWave * kV) + (int)ln * kV + (int)(el % kV)));
+    }
+  } else {
+    // more specials than the queue holds: each lane walks its own slots
+    for (int el = 0; el < kSub * kV; ++el) {
+      if ((S.spec >> el) & 1u) {
+        const float x = exact_term(ns.ev[w][el][lane], m, P.temperature, t1);
+        ns.ev[w][el][lane] = x;
+        if (first_pass && x >= P.cand_theta)
+          push_candidate(sh, x, (uint32_t)(sb + (el / kV) * (kWave * kV) + lane * kV + (el % kV)));
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int e = 0; e < kSub * kV; ++e)
+    if ((S.spec >> e) & 1u) S.wv[e / kV][e % kV] = ns.ev[w][e][lane];
+  __builtin_amdgcn_wave_barrier();
+}
+
+// The exact running sum across sub-chunk oc of this wave's slice, by the
+// owner wave, from the slice state.  Returns false (and leaves s at the
+// last exact value, `done` at the last position consumed) when the sum
+// leaves grids {jb, jb+1}: the caller then rebuilds the state.
+__device__ __forceinline__ bool wave_resolve(float& s, int& done, const SliceState& S, const float (&v)[kSub][kV],
+                                             int oc, int sb, int n, float m, const RowParams& P, bool t1, int jb) {
+  const int lane = lane_id();
+  const int base = sb + oc * (kWave * kV);
+  float w4[kV], v4[kV];
+  uint32_t sp4 = 0;
+#pragma unroll
+  for (int k = 0; k < kV; ++k) {
+    w4[k] = 0.0f;
+    v4[k] = 0.0f;
+  }
+#pragma unroll
+  for (int c = 0; c < kSub; ++c)
+    if (c == oc) {
+#pragma unroll
+      for (int k = 0; k < kV; ++k) {
+        w4[k] = S.wv[c][k];
+        v4[k] = v[c][k];
+      }
+      sp4 = (S.spec >> (c * kV)) & 0xfu;
+    }
+  for (;;) {
+    const Grid g = grid_of(s);
+    if (g.j != jb && g.j != jb + 1) return false;
+    const int sh = g.j - jb;
+    uint32_t r[kV];
+    bool tie[kV];
+    uint32_t tsum = 0;
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const int p = lane * kV + k;
+      r[k] = 0;
+      tie[k] = false;
+      if (p > done && base + p < n) r[k] = state_round(w4[k], (sp4 >> k) & 1u, g.j, sh, tie[k]);
+      tsum = sat_add(tsum, r[k], kSat);
+    }
+    const uint32_t incl = wave_incl_scan_sat(tsum, kSat);
+    uint32_t run = g.N + wave_shift_up1(incl);
+    int my_evt = -1, my_k = 0;
+    uint32_t my_before = 0;
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const int p = lane * kV + k;
+      if (my_evt < 0 && p > done && base + p < n) {
+        const uint32_t before = run;
+        run += r[k];
+        if (tie[k] || run >= kGridTop) {
+          my_evt = p;
+          my_before = before;
+          my_k = k;
+        }
+      }
+    }
+    const uint64_t mask = __ballot(my_evt >= 0);
+    if (mask == 0ull) {
+      s = grid_value(g.N + lane_readlast(incl), g.j);
+      done = kWave * kV - 1;
+      return true;
+    }
+    const int L = __ffsll((long long)mask) - 1;
+    const int kk = (int)readlane_u32((uint32_t)my_k, L);
+    float wsel = 0.0f, vsel = 0.0f;
+    bool ssel = false;
+#pragma unroll
+    for (int k = 0; k < kV; ++k)
+      if (k == kk) {
+        wsel = w4[k];
+        vsel = v4[k];
+        ssel = (sp4 >> k) & 1u;
+      }
+    const float ws = readlane_f32(wsel, L);
+    const bool ss = readlane_u32(ssel ? 1u : 0u, L) != 0u;
+    const float e = ss ? ws : exact_term(readlane_f32(vsel, L), m, P.temperature, t1);
+    s = grid_value(readlane_u32(my_before, L), g.j) + e;
+    done = (int)readlane_u32((uint32_t)my_evt, L);
+    if (done >= kWave * kV - 1) return true;
+  }
+}
+
+// sampler.zig:83-88: the exact sequential f32 normaliser of one row, plus the
+// candidate list (every element with e >= cand_theta).
+__device__ float row_normaliser(const float* xr, int n, const RowParams& P, SampleShared& sh, int& bank,
+                                float& m_out, float m_known) {
+  constexpr int W = kNT / kWave;
+  constexpr int GE = W * kSlice;    // elements per group
+  constexpr int NC = W * kSub;      // sub-chunks per group
+  static_assert(NC <= kWave, "one wave scans a group's sub-chunk sums");
+  NormShared<kNT>& ns = sh.u.norm;
+  const int t = (int)threadIdx.x, lane = lane_id(), w = wave_id();
+  const bool t1 = (P.flags & kFlagTIsOne) != 0;
+  const bool vec = (P.flags & kFlagVecSrc) != 0;
+  const int p0 = min(n, kPrologue);
+
+  // independent loads first: the max partials, the prologue's logits and the
+  // first group
+  const float mp = m_known;
+  const float vp = (w == 0 && lane < p0) ? xr[lane] : 0.0f;
+  float vcur[kSub][kV], vnext[kSub][kV];
+#pragma unroll
+  for (int c = 0; c < kSub; ++c) load4(xr, p0 + w * kSlice + c * (kWave * kV) + lane * kV, n, vec, vcur[c]);
+  const float m = wg_fmax<kNT>(mp, sh.wg, bank);
+  m_out = m;
+
+  // ---- prologue: the event-dense start of the row, the reference's loop
+  if (w == 0) {
+    float e = -0.0f;
+    if (lane < p0) {
+      e = exact_term(vp, m, P.temperature, t1);
+      if (e >= P.cand_theta) push_candidate(sh, e, (uint32_t)lane);
+    }
+    float s0 = 0.0f;
+    for (int l = 0; l < p0; ++l) s0 = s0 + readlane_f32(e, l);
+    if (lane == 0) ns.s_bcast[0] = s0;
+  }
+  lds_barrier();
+  float s = ns.s_bcast[0];
+  int sbi = 1;
+  int pb = 0;
+  SliceState S;
+
+  for (int gb = p0; gb < n; gb += GE) {
+    if (gb + GE < n) {
+#pragma unroll
+      for (int c = 0; c < kSub; ++c)
+        load4(xr, gb + GE + w * kSlice + c * (kWave * kV) + lane * kV, n, vec, vnext[c]);
+    }
+    uint32_t* part = ns.part[pb];
+    const int sb = gb + w * kSlice;
+    int c0 = 0;        // first sub-chunk not yet added
+    int dn = -1;       // positions of sub-chunk c0 already added (resolution in progress)
+    bool first = true;
+    for (;;) {  // (re)build the state for the grid of s
+      const int jb = grid_of(s).j;
+      slice_state(vcur, sb, n, m, P, t1, jb, first, max(0, c0 - w * kSub), sh, S);
+      first = false;
+      slice_sums(S, sb, n, jb, 0, max(0, c0 - w * kSub), &part[w * kSub]);
+      lds_barrier();
+      int j = jb;
+      bool rebuilt = false;
+      for (;;) {
+        uint32_t N = grid_of(s).N;
+        int cs;
+        uint32_t before;
+        if (dn >= 0) {
+          // a resolution stopped inside sub-chunk c0: continue it there
+          cs = c0;
+          before = N;
+        } else {
+          const bool act = lane >= c0 && lane < NC;
+          const uint32_t pv = act ? part[lane] : 0u;
+          const uint32_t psum = pv & 0x7fffffffu;
+          const uint32_t incl = wave_incl_scan_sat(psum, kSat);
+          const uint32_t excl = wave_shift_up1(incl);
+          const bool evt = act && ((pv >> 31) || g_top_reached(N, incl));
+          const uint64_t mask = __ballot(evt);
+          if (mask == 0ull) {
+            s = grid_value(N + lane_readlast(incl), j);
+            c0 = NC;
+            break;
+          }
+          cs = __ffsll((long long)mask) - 1;
+          before = N + readlane_u32(excl, cs);
+        }
+        // resolve sub-chunk cs in its owner wave
+        const int ow = cs / kSub, oc = cs % kSub;
+        if (w == ow) {
+          float so = grid_value(before, j);
+          int d = dn;
+          const bool ok = wave_resolve(so, d, S, vcur, oc, sb, n, m, P, t1, jb);
+          if (lane == 0) {
+            ns.s_bcast[sbi] = so;
+            ns.part[pb ^ 1][NC] = ok ? 0xffffffffu : (uint32_t)d;  // resolution status
+          }
+        }
+        lds_barrier();
+        s = ns.s_bcast[sbi];
+        sbi ^= 1;
+        const uint32_t st = ns.part[pb ^ 1][NC];
+        lds_barrier();
+        if (st != 0xffffffffu) {
+          // the sum left grids {jb, jb+1} inside sub-chunk cs: rebuild
+          c0 = cs;
+          dn = (int)st;
+          rebuilt = true;
+          break;
+        }
+        dn = -1;
+        c0 = cs + 1;
+        if (c0 >= NC) break;
+        const int jn = grid_of(s).j;
+        if (jn == j) continue;
+        if (jn == jb + 1) {
+          j = jn;
+          if (w * kSub + kSub > c0) slice_sums(S, sb, n, jb, 1, max(0, c0 - w * kSub), &part[w * kSub]);
+          lds_barrier();
+          continue;
+        }
+        rebuilt = true;  // beyond jb+1: rebuild the state for the new grid
+        break;
+      }
+      if (!rebuilt || c0 >= NC) break;
+    }
+    pb ^= 1;
+#pragma unroll
+    for (int c = 0; c < kSub; ++c)
+#pragma unroll
+      for (int k = 0; k < kV; ++k) vcur[c][k] = vnext[c][k];
+  }
+  return s;
+}
+
+// Sequential accumulation dispatcher: short lists run the reference's loop
+// on one wave; long ones use the workgroup's exact parallel scan.
+constexpr int kSeqMax = 128;
+
+template <bool SUB, typename TermFn>
+__device__ float seq_accumulate(float s, int len, float thr, int& stop, TermFn term, SampleShared& sh,
+                                int& bank) {
+  if (len <= kSeqMax) {
+    float res = 0.0f;
+    int st = -1;
+    if (wave_id() == 0) res = wave_seq_list<SUB>(s, len, thr, st, term);
+    uint32_t stu = (uint32_t)st;
+    wg_bcast<kNT>(threadIdx.x == 0, res, stu, sh.wg, bank);
+    stop = (int)stu;
+    return res;
+  }
+  return list_accumulate<kNT, 2, SUB>(s, len, thr, stop, term, sh.wg, bank);
+}
+
+// Bitonic sort of u64 keys with a u32 payload, ascending.
+template <int NT>
+__device__ void lds_bitonic_sort_kv(uint64_t* a, uint32_t* pl, int n) {
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = (int)threadIdx.x; i < n; i += NT) {
+        const int p = i ^ j;
+        if (p > i) {
+          const uint64_t x = a[i], y = a[p];
+          const bool up = (i & k) == 0;
+          if ((x > y) == up) {
+            a[i] = y; a[p] = x;
+            const uint32_t t = pl[i]; pl[i] = pl[p]; pl[p] = t;
+          }
+        }
+      }
+      lds_barrier();
+    }
+  }
+}
+
+__device__ __forceinline__ int next_pow2(int v) {
+  int p = 2;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+// Sorted-list views used by the filter stage: position q in (p desc, id asc).
+struct LdsList {
+  const uint64_t* a;
+  __device__ float p(int q) const { return __uint_as_float(~(uint32_t)(a[q] >> 32)); }
+  __device__ uint32_t id(int q) const { return (uint32_t)a[q]; }
+};
+struct GlobalList {
+  const uint32_t* key;  // ~p bits
+  const uint32_t* val;  // id
+  __device__ float p(int q) const { return __uint_as_float(~key[q]); }
+  __device__ uint32_t id(int q) const { return val[q]; }
+};
+
+// top-k / top-p / min-p over a sorted list whose first M positions are
+// exactly the first M positions of the full order (sampler.zig:106-126).
+// p_nc bounds the probability of every element beyond M (+inf when no bound
+// is known).  Returns K (the kept prefix length) or -1 when positions beyond
+// M decide.
+// All three filters keep a prefix of the order, so the kept prefix length is
+// min(Kk, Kp, Km); top-p's cut only matters when it falls before the other
+// two, which is why min-p is resolved first.
+template <typename List>
+__device__ int prefix_filters(const List& L, int M, float p_nc, int n, const RowParams& P, float S,
+                              SampleShared& sh, int& bank) {
+  const int Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
+  int Km = n;  // n also stands for "at least M" when km_known is false
+  bool km_known = true;
+  if (P.min_p > 0.0f) {
+    // probs[indices[0]] is the row maximum, e = exp(0) = 1, so p0 = 1/S
+    const float p0 = 1.0f / S;
+    const float thr = p0 * P.min_p;
+    uint32_t cnt = 0;
+    for (int q = (int)threadIdx.x; q < M; q += kNT) cnt += L.p(q) >= thr ? 1u : 0u;
+    cnt = wg_sum_sat<kNT>(cnt, 0x7fffffffu, sh.wg, bank);
+    if ((int)cnt < M) Km = (int)cnt;
+    else if (M < n) {
+      if (thr > p_nc) Km = M;
+      else km_known = false;
+    }
+  }
+  int Kp = n;
+  if (P.top_p > 0.0f && P.top_p < 1.0f) {
+    const int bound = min(Kk, Km);
+    const int lim = min(bound, M);
+    int st;
+    seq_accumulate<false>(0.0f, lim, P.top_p, st, [&](int q) { return L.p(q); }, sh, bank);
+    if (st >= 0) Kp = st;
+    else if (bound > M) return -1;  // the cut may lie beyond the certified prefix
+  }
+  (void)km_known;  // an unknown Km >= M only matters if the result exceeds M
+  const int K = min(Kk, min(Kp, Km));
+  return K > M ? -1 : K;
+}
+
+// Entropy sum over the whole row in index order (sampler.zig:129-132).
+__device__ float entropy_pass(const float* xr, int n, float m, float S, const RowParams& P,
+                              SampleShared& sh, int& bank) {
+  const bool t1 = (P.flags & kFlagTIsOne) != 0;
+  const bool vec = (P.flags & kFlagVecSrc) != 0;
+  float H = 0.0f;
+  const int t = (int)threadIdx.x;
+  for (int base = 0; base < n; base += kTile) {
+    float v[kV], term[kV];
+    load4(xr, base + t * kV, n, vec, v);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const float p = row_exp(v[k], m, P.temperature, t1) / S;
+      // entropy -= p * log(p) for p > 0; the term enters negated (exact)
+      term[k] = p > 0.0f ? -(p * log_f32(p)) : -0.0f;
+    }
+    int st;
+    H = tile_accumulate<kNT, kV, false>(H, term, min(kTile, n - base), -1.0f, st, sh.wg, bank);
+  }
+  return H;
+}
+
+// Total and draw over p-order positions [0, K) whose keep flag is set
+// (sampler.zig:156-168).  keep(q) -> bool.
+template <typename List, typename Keep>
+__device__ void total_and_draw(const List& L, int K, Keep keep, float u, float& total,
+                               uint32_t& token, uint32_t& consumed, SampleShared& sh, int& bank) {
+  int st;
+  total = seq_accumulate<false>(0.0f, K, -1.0f, st, [&](int q) { return keep(q) ? L.p(q) : -0.0f; }, sh,
+                                bank);
+  const uint32_t tok0 = L.id(0);
+  if (total <= 0.0f) {
+    token = tok0;
+    consumed = 0;
+    return;
+  }
+  consumed = 1;
+  const float r0 = u * total;
+  seq_accumulate<true>(r0, K, -1.0f, st, [&](int q) { return keep(q) ? L.p(q) : -0.0f; }, sh, bank);
+  token = st >= 0 ? L.id(st) : tok0;
+}
+
+// Rare paths of k_select, out of line so that the common path's register
+// allocation stays small.
+
+struct NormResult {
+  float S, m;
+  int bank;
+};
+
+// The streaming normaliser (sampler.zig:83-88) for a row k_stats could not
+// certify; fills the candidate list in LDS.
+__device__ __noinline__ NormResult select_norm_fallback(const RowParams P, const float* xr, SampleShared& sh,
+                                                        int bank, float m_known) {
+  if (threadIdx.x == 0) sh.cand_count = 0;
+  NormResult r;
+  r.S = row_normaliser(xr, P.n, P, sh, bank, r.m, m_known);
+  r.bank = bank;
+  return r;
+}
+
+__device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q, SampleShared& sh, int bank,
+                                             float m, float S, uint32_t path);
+
+// The rest of sampleWithRandom (sampler.zig:89-168) for row blockIdx.x,
+// after k_stats' phases: from the row maximum m, the normaliser S and the
+// candidate list in Q.cand (cc entries), or, for a row k_stats could not
+// certify, from the streaming normaliser.  Every thread of the workgroup
+// calls it; `sh` may alias the caller's shared memory once all of it is read.
+__device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q, SampleShared& sh, float m,
+                                           float S, uint32_t cc_in, bool uncertified) {
+  int bank = 0;
+  const int row = blockIdx.x;
+  const int t = (int)threadIdx.x;
+  const int n = P.n;
+  const float* xr = Q.src + (int64_t)row * P.src_stride;
+  uint32_t path = 0;
+  if (uncertified) {
+    // the streaming normaliser (sampler.zig:83-88) fills the candidate list in LDS
+    const NormResult r = select_norm_fallback(P, xr, sh, bank, m);
+    S = r.S;
+    m = r.m;
+    bank = r.bank;
+    path |= kPathNormFallback;
+  } else {
+    const int c = cc_in > (uint32_t)kCap ? kCap : (int)cc_in;
+    const uint64_t* gc = Q.cand + (int64_t)row * kCap;
+    for (int i = t; i < c; i += kNT) sh.cand[i] = gc[i];
+    if (t == 0) sh.cand_count = cc_in;
+  }
+  uint32_t token = 0, consumed = 0;
+  float H = 0.0f, total = 0.0f;
+  int K = 0;
+
+  // ---- 3. sum <= 0 exit: sampleArgmax of the caller's logits (:89)
+  if (S <= 0.0f) {
+    token = wg_argmax_row<kNT>(Q.orig + (int64_t)row * P.orig_stride, n, sh.wg, bank);
+    path = kPathSumLe0;
+    if (t == 0) {
+      Q.tokens[row] = token;
+      if (Q.consumed) Q.consumed[row] = 0;
+      if (Q.kept_count) Q.kept_count[row] = 0;
+      if (Q.row_stats) {
+        float* rs = Q.row_stats + (int64_t)row * 4;
+        rs[0] = m; rs[1] = S; rs[2] = 0.0f; rs[3] = 0.0f;
+      }
+      if (Q.status) Q.status[row] = path;
+    }
+    return;
+  }
+
+  // ---- a NaN normaliser (a NaN logit or an infinite maximum): every
+  // probability is NaN, so every comparison of the chain is false.  The
+  // stable sort keeps index order, top-k keeps the first k indices, top-p,
+  // min-p and typical-p keep everything, the total is NaN and the walk never
+  // stops: indices[0] = 0 after one draw (sampler.zig:96-168).
+  if (S != S) {
+    const int kept = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
+    if (Q.kept_ids || Q.kept_probs) {
+      for (int q = t; q < kept && q < P.kept_cap; q += kNT) {
+        if (Q.kept_ids) Q.kept_ids[(int64_t)row * P.kept_cap + q] = (uint32_t)q;
+        if (Q.kept_probs) Q.kept_probs[(int64_t)row * P.kept_cap + q] = __builtin_nanf("");
+      }
+    }
+    if (t == 0) {
+      Q.tokens[row] = 0;
+      if (Q.consumed) Q.consumed[row] = 1;
+      if (Q.kept_count) Q.kept_count[row] = (uint32_t)kept;
+      if (Q.row_stats) {
+        float* rs = Q.row_stats + (int64_t)row * 4;
+        rs[0] = m; rs[1] = S; rs[2] = 0.0f; rs[3] = __builtin_nanf("");
+      }
+      if (Q.status) Q.status[row] = 0;
+    }
+    return;
+  }
+
+  // ---- 4. candidates -> probabilities -> (p desc, id asc) (:90-100)
+  lds_barrier();
+  const uint32_t cc = sh.cand_count;
+  const bool ovf = cc > (uint32_t)kCap;
+  const int c = ovf ? kCap : (int)cc;
+  const int csort = next_pow2(c);
+  for (int i = t; i < csort; i += kNT) {
+    if (i < c) {
+      const uint64_t a = sh.cand[i];
+      const float p = __uint_as_float((uint32_t)(a >> 32)) / S;
+      sh.cand[i] = ((uint64_t)(~__float_as_uint(p)) << 32) | (uint32_t)a;
+    } else {
+      sh.cand[i] = ~0ull;
+    }
+  }
+  lds_barrier();
+  lds_bitonic_sort_u64<kNT>(sh.cand, csort);
+
+  // certified prefix: every element outside the list has p <= theta / S
+  int M = 0;
+  if (!ovf) {
+    if (P.cand_theta <= 0.0f) {
+      M = c;  // every element was collected
+    } else {
+      const float p_nc = P.cand_theta / S;
+      uint32_t cnt = 0;
+      for (int q = t; q < c; q += kNT) cnt += __uint_as_float(~(uint32_t)(sh.cand[q] >> 32)) > p_nc ? 1u : 0u;
+      M = (int)wg_sum_sat<kNT>(cnt, 0x7fffffffu, sh.wg, bank);
+    }
+  }
+
+  const LdsList LL{sh.cand};
+  // a complete list bounds everything outside it: e < theta, p <= theta / S
+  const float p_nc = ovf ? kInf : P.cand_theta / S;
+  K = prefix_filters(LL, M, p_nc, n, P, S, sh, bank);
+  const bool typical = P.typical_p > 0.0f && P.typical_p < 1.0f;
+  const float u = Q.uniforms[row];
+  bool fallback = K < 0;
+
+  if (!fallback) {
+    // ---- 5. typical-p on the kept prefix (:128-154)
+    for (int q = t; q < kCap; q += kNT) sh.u.post.keep[q] = q < K ? 1 : 0;
+    lds_barrier();
+    if (typical && K == 1) {
+      if (t == 0 && LL.p(0) > P.typical_p) sh.u.post.keep[0] = 0;
+      lds_barrier();
+    } else if (typical && K >= 2) {
+      path |= kPathEntropy;
+      H = entropy_pass(xr, n, m, S, P, sh, bank);
+      const int ksort = next_pow2(K);
+      for (int q = t; q < ksort; q += kNT) {
+        if (q < K) {
+          const float p = LL.p(q);
+          const float surprise = p > 0.0f ? -log_f32(p) : kInf;
+          const float dev = fabsf(surprise - H);
+          sh.u.post.aux[q] = ((uint64_t)__float_as_uint(dev) << 32) | LL.id(q);
+          sh.u.post.aux_pos[q] = (uint32_t)q;
+        } else {
+          sh.u.post.aux[q] = ~0ull;
+          sh.u.post.aux_pos[q] = 0;
+        }
+      }
+      lds_barrier();
+      lds_bitonic_sort_kv<kNT>(sh.u.post.aux, sh.u.post.aux_pos, ksort);
+      int st;
+      seq_accumulate<false>(0.0f, K, P.typical_p, st, [&](int d) { return LL.p((int)sh.u.post.aux_pos[d]); },
+                            sh, bank);
+      if (st >= 0) {
+        for (int d = st + t; d < K; d += kNT) sh.u.post.keep[sh.u.post.aux_pos[d]] = 0;
+      }
+      lds_barrier();
+    }
+    // ---- 6. total and draw (:156-168)
+    total_and_draw(LL, K, [&](int q) { return sh.u.post.keep[q] != 0; }, u, total, token, consumed, sh, bank);
+
+    // ---- outputs
+    uint32_t kept = 0;
+    for (int q = t; q < K; q += kNT) kept += sh.u.post.keep[q];
+    kept = wg_sum_sat<kNT>(kept, 0x7fffffffu, sh.wg, bank);
+    if (Q.kept_ids || Q.kept_probs) {
+      // compact the kept positions in p order (thread-serial over K <= kCap)
+      if (t == 0) {
+        int o = 0;
+        for (int q = 0; q < K && o < P.kept_cap; ++q) {
+          if (sh.u.post.keep[q]) {
+            if (Q.kept_ids) Q.kept_ids[(int64_t)row * P.kept_cap + o] = LL.id(q);
+            if (Q.kept_probs) Q.kept_probs[(int64_t)row * P.kept_cap + o] = LL.p(q);
+            ++o;
+          }
+        }
+      }
+    }
+    if (t == 0) {
+      Q.tokens[row] = token;
+      if (Q.consumed) Q.consumed[row] = (uint8_t)consumed;
+      if (Q.kept_count) Q.kept_count[row] = kept;
+      if (Q.row_stats) {
+        float* rs = Q.row_stats + (int64_t)row * 4;
+        rs[0] = m; rs[1] = S; rs[2] = H; rs[3] = total;
+      }
+      if (Q.status) Q.status[row] = path;
+    }
+    return;
+  }
+
+  // ---- full-row fallback: every probability, stable radix sort, filters
+  select_full_row(P, Q, sh, bank, m, S, path);
+}
+
+// The full-row fallback of k_select: every probability, stable radix sort of
+// the whole row in the workspace, the filters and the draw over it.
+__device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q, SampleShared& sh, int bank,
+                                             float m, float S, uint32_t path) {
+  const int row = blockIdx.x;
+  const int t = (int)threadIdx.x;
+  const int n = P.n;
+  const bool t1 = (P.flags & kFlagTIsOne) != 0;
+  const bool vec = (P.flags & kFlagVecSrc) != 0;
+  const float* xr = Q.src + (int64_t)row * P.src_stride;
+  const bool typical = P.typical_p > 0.0f && P.typical_p < 1.0f;
+  const float u = Q.uniforms[row];
+  int K = 0;
+  float H = 0.0f, total = 0.0f;
+  uint32_t token = 0, consumed = 0;
+  path |= kPathFallback;
+  if (!(P.flags & kFlagFallback)) {
+    if (t == 0) {
+      Q.tokens[row] = 0xffffffffu;
+      if (Q.consumed) Q.consumed[row] = 0;
+      if (Q.status) Q.status[row] = path | kPathError;
+    }
+    return;
+  }
+  const int64_t fo = (int64_t)row * n;
+  uint32_t* Ak = Q.fb + 0 * (int64_t)P.rows * n + fo;
+  uint32_t* Av = Q.fb + 1 * (int64_t)P.rows * n + fo;
+  uint32_t* Bk = Q.fb + 2 * (int64_t)P.rows * n + fo;
+  uint32_t* Bv = Q.fb + 3 * (int64_t)P.rows * n + fo;
+  uint32_t* Ck = Q.fb + 4 * (int64_t)P.rows * n + fo;
+  uint32_t* Cv = Q.fb + 5 * (int64_t)P.rows * n + fo;
+  uint8_t* mask = Q.fb_mask + fo;
+  for (int base = 0; base < n; base += kTile) {
+    float v[kV];
+    const int pos = base + t * kV;
+    load4(xr, pos, n, vec, v);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      if (pos + k < n) {
+        const float p = row_exp(v[k], m, P.temperature, t1) / S;
+        Ak[pos + k] = ~__float_as_uint(p);
+        Av[pos + k] = (uint32_t)(pos + k);
+      }
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  wg_radix_sort_pairs<kNT>(Ak, Av, Bk, Bv, n, sh.u.post.radix);
+  __threadfence();
+  __syncthreads();
+  const GlobalList GL{Ak, Av};
+  K = prefix_filters(GL, n, kInf, n, P, S, sh, bank);  // M = n: never -1
+  if (K < 0) K = 0;
+  if (typical && K >= 2) {
+    path |= kPathEntropy;
+    H = entropy_pass(xr, n, m, S, P, sh, bank);
+    for (int i = t; i < n; i += kNT) mask[i] = 0;
+    __threadfence();
+    __syncthreads();
+    for (int q = t; q < K; q += kNT) mask[Av[q]] = 1;
+    __threadfence();
+    __syncthreads();
+    // selected ids in index order with their dev keys (stream compaction)
+    int written = 0;
+    for (int base = 0; base < n; base += kNT) {
+      const int i = base + t;
+      const bool sel = i < n && mask[i] == 1;
+      const uint32_t before = wg_excl_scan_sat<kNT>(sel ? 1u : 0u, 0x7fffffffu, sh.wg, bank);
+      if (sel) {
+        const float p = row_exp(xr[i], m, P.temperature, t1) / S;
+        const float surprise = p > 0.0f ? -log_f32(p) : kInf;
+        Bk[written + before] = __float_as_uint(fabsf(surprise - H));
+        Bv[written + before] = (uint32_t)i;
+      }
+      written += (int)wg_sum_sat<kNT>(sel ? 1u : 0u, 0x7fffffffu, sh.wg, bank);
+    }
+    __threadfence();
+    __syncthreads();
+    wg_radix_sort_pairs<kNT>(Bk, Bv, Ck, Cv, written, sh.u.post.radix);
+    __threadfence();
+    __syncthreads();
+    int st;
+    list_accumulate<kNT, 2, false>(
+        0.0f, written, P.typical_p, st,
+        [&](int d) { return row_exp(xr[Bv[d]], m, P.temperature, t1) / S; }, sh.wg, bank);
+    const int keep_n = st >= 0 ? st : written;
+    for (int d = t; d < keep_n; d += kNT) mask[Bv[d]] = 2;
+    __threadfence();
+    __syncthreads();
+    total_and_draw(GL, K, [&](int q) { return mask[Av[q]] == 2; }, u, total, token, consumed, sh, bank);
+  } else if (typical && K == 1) {
+    const bool k0 = !(GL.p(0) > P.typical_p);
+    total_and_draw(GL, K, [&](int q) { return k0; }, u, total, token, consumed, sh, bank);
+  } else {
+    total_and_draw(GL, K, [&](int q) { return true; }, u, total, token, consumed, sh, bank);
+  }
+  // outputs (kept list compaction is thread-serial: diagnostic use only)
+  const bool use_mask = typical && K >= 2;
+  uint32_t kept = 0;
+  for (int q = t; q < K; q += kNT) {
+    bool kq = use_mask ? mask[Av[q]] == 2 : (typical && K == 1 ? !(GL.p(0) > P.typical_p) : true);
+    kept += kq ? 1u : 0u;
+  }
+  kept = wg_sum_sat<kNT>(kept, 0x7fffffffu, sh.wg, bank);
+  if (t == 0) {
+    if (Q.kept_ids || Q.kept_probs) {
+      int o = 0;
+      for (int q = 0; q < K && o < P.kept_cap; ++q) {
+        bool kq = use_mask ? mask[Av[q]] == 2 : (typical && K == 1 ? !(GL.p(0) > P.typical_p) : true);
+        if (kq) {
+          if (Q.kept_ids) Q.kept_ids[(int64_t)row * P.kept_cap + o] = GL.id(q);
+          if (Q.kept_probs) Q.kept_probs[(int64_t)row * P.kept_cap + o] = GL.p(q);
+          ++o;
+        }
+      }
+    }
+    Q.tokens[row] = token;
+    if (Q.consumed) Q.consumed[row] = (uint8_t)consumed;
+    if (Q.kept_count) Q.kept_count[row] = kept;
+    if (Q.row_stats) {
+      float* rs = Q.row_stats + (int64_t)row * 4;
+      rs[0] = m; rs[1] = S; rs[2] = H; rs[3] = total;
+    }
+    if (Q.status) Q.status[row] = path;
+  }
+}
+
+}  // namespace llz

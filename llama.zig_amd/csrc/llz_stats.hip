@@ -1,9 +1,9 @@
-// llz_stats.hip -- k_stats: single-pass row statistics for the sampling chain
-// (sampler.zig:80-88): the row maximum, the exact sequential f32 normaliser
-// and the candidate list, with one HBM read per logit.  The method and its
-// error bound are described in llz_fast.h.  Rows it cannot certify are
-// flagged in row_state[3]; k_select then runs the streaming normaliser on
-// them.
+// llz_stats.hip -- k_stats: the fused per-row sampling kernel.  Phases L .. C
+// compute the row statistics (sampler.zig:80-88): the row maximum, the exact
+// sequential f32 normaliser and the candidate list, with one HBM read per
+// logit (method and error bound in llz_fast.h).  The same workgroup then runs
+// the selection stage (llz_select.h, sampler.zig:89-168); a row the fast path
+// cannot certify takes the streaming normaliser there instead.
 #include <hip/hip_runtime.h>
 
 #include "llz_exact.h"
@@ -11,6 +11,7 @@
 #include "llz_internal.h"
 #include "llz_math.h"
 #include "llz_norm.h"
+#include "llz_select.h"
 #include "llz_wg.h"
 
 namespace llz {
@@ -278,7 +279,11 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
 // segment through buffer loads); otherwise element loads.
 template <bool FASTLD>
 __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
-  __shared__ FastShared F;
+  __shared__ union {
+    FastShared fast;      // phases L .. C
+    SampleShared select;  // then the selection stage
+  } U;
+  FastShared& F = U.fast;
   const int row = blockIdx.x;
   const int t = (int)threadIdx.x, lane = lane_id();
   const int w = __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform: scalar registers
@@ -294,7 +299,6 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   const int nseg_w = fits ? max(0, (G - w + W - 1) / W) : 0;
   const int base_w = w * SEG + lane * 4;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
-  float* rs_out = Q.row_state + (int64_t)row * 4;
 
   // ---- phase L: every load in flight, then per segment as it lands: running
   // maximum, the estimate q (stored over v) and the segment sum of q
@@ -420,343 +424,341 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     m = fmaxf(m, F.mw[i]);
     nanrow = nanrow || F.nanw[i] != 0u;
   }
-  if (nanrow || !(fabsf(m) <= 3.0e38f)) {
-    // a NaN logit or an infinite maximum makes the reference's sum NaN
-    if (t == 0) {
-      rs_out[0] = m;
-      rs_out[1] = __builtin_nanf("");
-      rs_out[2] = __uint_as_float(0u);
-      rs_out[3] = 0.0f;
-    }
-    return;
-  }
-  const float aw = fmaf(m, -l2e_t, cw);
-  const float Rw = __builtin_amdgcn_exp2f(aw);  // q * Rw ~ e = exp((v - m) / T)
-  // Prediction in index order: lane k takes round k (segments W k .. W k +
-  // W - 1, one per wave, each scaled by its wave's R); a scan over the rounds
-  // gives every segment's running sum.  Every wave computes it for its own
-  // segments (the lane's segment of this wave is W k + w).
-  const bool have = lane < nseg_w;
-  {
-    float rtot = 0.0f, before_w = 0.0f, b_w = 0.0f;
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < W; ++i) {
-      const float awi = fmaf(m, -l2e_t, F.cw[i]);
-      bad = bad || ((G > i) && !(fabsf(awi) <= 32.0f));
-      const int g = W * lane + i;
-      const float b = g < G ? F.v.aseg[g] * __builtin_amdgcn_exp2f(awi) : 0.0f;
-      rtot += b;
-      before_w += i < w ? b : 0.0f;
-      b_w = i == w ? b : b_w;
-    }
-    const float rin = wave_incl_scan_f32(rtot);
-    const float rex = __uint_as_float(wave_shift_up1(__float_as_uint(rin)));
-    const float total = __uint_as_float(lane_readlast(__float_as_uint(rin)));
-    bad = bad || !(total <= 3.0e38f);
-    bool ex = false, fl = false;
-    if (!bad && have) {
-      const float excl = rex + before_w;
-      const float incl = excl + b_w;
-      const float lo = excl * (1.0f - DELTA), hi = incl * (1.0f + DELTA);
-      const int elo = (int)(__float_as_uint(lo) >> 23) - 127;
-      const int ehi = (int)(__float_as_uint(hi) >> 23) - 127;
-      const bool plain = lo >= 0x1p-64f && hi <= 3.0e38f && elo == ehi;
-      fl = plain && ldexpf(P.cand_theta, 23 - elo) < 2.0f;
-      // EXACT: tabulate the binade the segment starts in and the next one
-      int j0 = lo >= 0x1p-126f ? elo : ehi - 1;
-      j0 = max(-126, min(j0, 126));
-      const int g = w + W * lane;
-      F.sflag[g] = plain ? PLAIN : EXACT_PRED;
-      F.sj[g] = (int8_t)(plain ? elo : j0);
-      ex = !plain;
-    }
-    // EXACT slots (any order; a row with more than DCAP takes further rounds in index order)
-    const uint64_t exm = __ballot(ex);
-    int base = 0;
-    if (lane == 0) {
-      if (exm != 0ull) base = (int)atomicAdd((uint32_t*)&F.nslot, (uint32_t)__popcll(exm));
-      if (bad) atomicOr(&F.fail, 1u);
-      if (__ballot(fl) != 0ull) atomicOr(&F.flood, 1u);
-    }
-    base = __builtin_amdgcn_readfirstlane(base);
-    if (have) {
-      const int slot = base + __popcll(exm & lt_mask);
-      const bool got = ex && slot < DCAP;
-      F.sdump[w + W * lane] = (int8_t)(got ? slot : -1);
-      if (got) F.slotseg[slot] = (int16_t)(w + W * lane);
-    }
-  }
-  __syncthreads();
-  const bool flood = F.flood != 0u;
-  const float theta = flood ? kInfS : P.cand_theta;
-
-  // ---- phase S: integer sums of PLAIN segments, four segments per step;
-  // specials queued with the segment's integer sum before them (lower
-  // bracket), and settled when the queue is full
-  int qn = 0;
-  float v2[2];
-  auto reread = [&]() {  // the queued logits (wave-uniform count qn)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = h * kWave + lane;
-      v2[h] = xr[i < qn ? F.qpos[w][i] : 0u];
-    }
-  };
-  auto settle = [&]() {
-    settle_specials(F, Q, P, row, w, qn, v2, Rw, cw, m, theta, t1);
-    qn = 0;
-  };
-  bool qovf = false;
-  if (!F.fail) {
-    const uint32_t flag_l = have ? (uint32_t)F.sflag[w + W * lane] : (uint32_t)EXACT_PRED;
-    const int j_l = have ? (int)F.sj[w + W * lane] : 0;
-    const GridConst gc_l = grid_const(j_l, Rw, theta);
-    auto lds_q = [&](int k) {
-      int l4 = lane_id() * 4;
-      asm volatile("" : "+v"(l4));  // recomputed here rather than kept live through the loop
-      return *reinterpret_cast<const float4*>(&F.u.data[w][min(max(k - KV, 0), KL - 1)][l4]);
-    };
-    for (int k0 = 0; k0 < nseg_w; k0 += 4) {
-      llz_f4v qa, qb, qc, qd;  // native vectors: an array or HIP's float4 struct here ends up in scratch
-      switch (k0 >> 2) {
-#define LLZ_GET(i) to_v4((i) < KV ? d[(i) < KV ? (i) : 0] : lds_q(i))
-#define LLZ_CASE(b)                 \
-  case b:                           \
-    qa = LLZ_GET(4 * (b) + 0);      \
-    qb = LLZ_GET(4 * (b) + 1);      \
-    qc = LLZ_GET(4 * (b) + 2);      \
-    qd = LLZ_GET(4 * (b) + 3);      \
-    break;
-        LLZ_CASE(0) LLZ_CASE(1) LLZ_CASE(2) LLZ_CASE(3) LLZ_CASE(4) LLZ_CASE(5)
-        LLZ_CASE(6) LLZ_CASE(7) LLZ_CASE(8) LLZ_CASE(9) LLZ_CASE(10) LLZ_CASE(11)
-#undef LLZ_CASE
-#undef LLZ_GET
-        default:
-          qa = to_v4(lds_q(k0 + 0));
-          qb = to_v4(lds_q(k0 + 1));
-          qc = to_v4(lds_q(k0 + 2));
-          qd = to_v4(lds_q(k0 + 3));
+  // a NaN logit or an infinite maximum makes the reference's sum NaN: the
+  // selection handles that row without the phases below
+  const bool nan_sum = nanrow || !(fabsf(m) <= 3.0e38f);
+  bool certified = true;
+  float S = __builtin_nanf("");
+  uint32_t cc = 0;
+  if (!nan_sum) {
+    const float aw = fmaf(m, -l2e_t, cw);
+    const float Rw = __builtin_amdgcn_exp2f(aw);  // q * Rw ~ e = exp((v - m) / T)
+    // Prediction in index order: lane k takes round k (segments W k .. W k +
+    // W - 1, one per wave, each scaled by its wave's R); a scan over the rounds
+    // gives every segment's running sum.  Every wave computes it for its own
+    // segments (the lane's segment of this wave is W k + w).
+    const bool have = lane < nseg_w;
+    {
+      float rtot = 0.0f, before_w = 0.0f, b_w = 0.0f;
+      bool bad = false;
+  #pragma unroll
+      for (int i = 0; i < W; ++i) {
+        const float awi = fmaf(m, -l2e_t, F.cw[i]);
+        bad = bad || ((G > i) && !(fabsf(awi) <= 32.0f));
+        const int g = W * lane + i;
+        const float b = g < G ? F.v.aseg[g] * __builtin_amdgcn_exp2f(awi) : 0.0f;
+        rtot += b;
+        before_w += i < w ? b : 0.0f;
+        b_w = i == w ? b : b_w;
       }
-      // per segment s: w1..w3 = the lane's integer sums before its elements
-      // 1..3, acc = the lane's sum, incl = the inclusive scan over lanes
-      uint32_t acc4[4], incl4[4], wa[4], wb[4], wc[4], spm = 0;
-      bool pl4[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int k = k0 + s;
-        const int kl = min(k, kWave - 1);
-        pl4[s] = k < nseg_w && readlane_u32(flag_l, kl) == (uint32_t)PLAIN;
-        const float sc_lo = readlane_f32(gc_l.sc_lo, kl);
-        const float sc_hi = readlane_f32(gc_l.sc_hi, kl);
-        const float tspec = readlane_f32(gc_l.tspec, kl);
-        const llz_f4v qv4 = s == 0 ? qa : s == 1 ? qb : s == 2 ? qc : qd;  // s is a constant here
-        const float qs[4] = {qv4.x, qv4.y, qv4.z, qv4.w};
-        uint32_t b[4], sp = 0;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float rlo = fmaf(qs[c], sc_lo, MAGIC);
-          const float rhi = fmaf(qs[c], sc_hi, MAGIC);
-          b[c] = __float_as_uint(rlo);
-          sp |= (rlo != rhi || rhi >= tspec) ? (1u << c) : 0u;
-        }
-        // absent positions hold q = 0, so rlo = rhi = MAGIC: never special
-        // (tspec > MAGIC for PLAIN segments outside flood mode, and theta is
-        // +inf in flood mode)
-        wa[s] = b[0] - MAGIC_BITS;
-        wb[s] = wa[s] + b[1] - MAGIC_BITS;
-        wc[s] = wb[s] + b[2] - MAGIC_BITS;
-        acc4[s] = wc[s] + b[3] - MAGIC_BITS;
-        if (!pl4[s]) sp = 0;
-        spm |= sp << (4 * s);
+      const float rin = wave_incl_scan_f32(rtot);
+      const float rex = __uint_as_float(wave_shift_up1(__float_as_uint(rin)));
+      const float total = __uint_as_float(lane_readlast(__float_as_uint(rin)));
+      bad = bad || !(total <= 3.0e38f);
+      bool ex = false, fl = false;
+      if (!bad && have) {
+        const float excl = rex + before_w;
+        const float incl = excl + b_w;
+        const float lo = excl * (1.0f - DELTA), hi = incl * (1.0f + DELTA);
+        const int elo = (int)(__float_as_uint(lo) >> 23) - 127;
+        const int ehi = (int)(__float_as_uint(hi) >> 23) - 127;
+        const bool plain = lo >= 0x1p-64f && hi <= 3.0e38f && elo == ehi;
+        fl = plain && ldexpf(P.cand_theta, 23 - elo) < 2.0f;
+        // EXACT: tabulate the binade the segment starts in and the next one
+        int j0 = lo >= 0x1p-126f ? elo : ehi - 1;
+        j0 = max(-126, min(j0, 126));
+        const int g = w + W * lane;
+        F.sflag[g] = plain ? PLAIN : EXACT_PRED;
+        F.sj[g] = (int8_t)(plain ? elo : j0);
+        ex = !plain;
       }
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        incl4[s] = wave_incl_scan_op(acc4[s], 0u, [](uint32_t a, uint32_t b) { return a + b; });
-      if (lane == kWave - 1) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          if (pl4[s]) F.ssum[w + W * (k0 + s)] = incl4[s];
-      }
-      if (__ballot(spm != 0u) != 0ull) {
-        // every lane appends its own specials after those of the lanes below it
-        const uint32_t my = (uint32_t)__popc(spm);
-        const uint32_t incl = wave_incl_scan_op(my, 0u, [](uint32_t a, uint32_t b) { return a + b; });
-        const int total = (int)lane_readlast(incl);
-        if (qn + total > QCAP) {
-          reread();
-          settle();
-        }
-        if (total > QCAP) {
-          qovf = true;  // more specials in four segments than the queue holds
-        } else {
-          int slot = qn + (int)(incl - my);
-          uint32_t rem = spm;
-          while (rem != 0u) {
-            const int bt = __ffs(rem) - 1;
-            rem &= rem - 1u;
-            const int s = bt >> 2, c = bt & 3;
-            const uint32_t ex_s = s == 0 ? incl4[0] - acc4[0] : s == 1 ? incl4[1] - acc4[1]
-                                : s == 2 ? incl4[2] - acc4[2] : incl4[3] - acc4[3];
-            const uint32_t wa_s = s == 0 ? wa[0] : s == 1 ? wa[1] : s == 2 ? wa[2] : wa[3];
-            const uint32_t wb_s = s == 0 ? wb[0] : s == 1 ? wb[1] : s == 2 ? wb[2] : wb[3];
-            const uint32_t wc_s = s == 0 ? wc[0] : s == 1 ? wc[1] : s == 2 ? wc[2] : wc[3];
-            F.qpos[w][slot] = (uint32_t)((w + W * (k0 + s)) * SEG + lane4 + c);
-            F.qpre[w][slot] = ex_s + (c == 0 ? 0u : c == 1 ? wa_s : c == 2 ? wb_s : wc_s);
-            ++slot;
-          }
-          qn += total;
-        }
-      }
-    }
-    if (qovf && lane == 0) atomicOr(&F.fail, 1u);
-  }
-
-  // ---- phase F+X: the remaining specials and this round's EXACT slots in
-  // one round trip (the slots overlay the LDS-resident segments: every wave
-  // is past phase S)
-  __syncthreads();
-  if (!F.fail) {
-    reread();
-    const int nslot = min(F.nslot, DCAP);
-    exact_loads<FASTLD>(F, xr, w, nslot, n);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    settle();
-    exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
-  }
-  __syncthreads();
-
-  // ---- phase C: the walk in index order; EXACT segments beyond the slots
-  // in further rounds
-  for (int round = 0; !F.fail; ++round) {
-    const int g_from = F.next_g;
-    if (round > 0) {
-      if (w == 0) {  // slots for the EXACT segments from g_from on, in order
-        int cnt = 0;
-        for (int b = g_from; b < G; b += kWave) {
-          const int g = b + lane;
-          const bool ex = g < G && (F.sflag[g] == EXACT_PRED || F.sflag[g] == EXACT_DONE);
-          const uint64_t mk = __ballot(ex);
-          const int slot = cnt + __popcll(mk & lt_mask);
-          if (ex) {
-            F.sdump[g] = (int8_t)(slot < DCAP ? slot : -1);
-            if (slot < DCAP) F.slotseg[slot] = (int16_t)g;
-          }
-          cnt += __popcll(mk);
-        }
-        if (lane == 0) F.nslot = min(cnt, DCAP);
-      }
-      __syncthreads();
-      const int nslot = F.nslot;
-      exact_loads<FASTLD>(F, xr, w, nslot, n);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
-      __syncthreads();
-    }
-    if (w == 0) {
-      float s = F.s_run;
-      int g = g_from;
-      bool fail = false, more = false;
-      while (g < G && !fail && !more) {
-        // this group of 64 segments, one per lane
-        const int gb = g & ~(kWave - 1);
-        const int gend = min(gb + kWave, G);
-        const int gg = gb + lane;
-        uint32_t fl = PLAIN, sm = 0;
-        int jj = 0, sd = -1;
-        if (gg < gend) {
-          fl = F.sflag[gg];
-          jj = F.sj[gg];
-          sm = min(F.ssum[gg], kSat);
-          sd = F.sdump[gg];
-        }
-        // inclusive prefix of the group's sums (each <= 2^25: no wrap)
-        const uint32_t pincl = wave_incl_scan_op(sm, 0u, [](uint32_t a, uint32_t b) { return a + b; });
-        while (g < gend) {
-          const Grid gr = grid_of(s);
-          const int p = g - gb;
-          const bool okp = fl == PLAIN && jj == gr.j;
-          const uint64_t bad = __ballot(lane >= p && gg < gend && !okp);
-          const int fb = bad ? __ffsll((long long)bad) - 1 : gend - gb;
-          if (fb > p) {
-            // PLAIN run [p, fb): terms are >= 0, so it stays in the binade
-            // exactly when its total does
-            const uint32_t tot = readlane_u32(pincl, fb - 1) - (p > 0 ? readlane_u32(pincl, p - 1) : 0u);
-            if (gr.N + tot >= kGridTop) {
-              fail = true;  // a crossing the prediction did not see
-              break;
-            }
-            s = grid_value(gr.N + tot, gr.j);
-            g = gb + fb;
-          }
-          if (g >= gend) break;
-          // segment g is an event
-          const uint32_t flg = readlane_u32(fl, fb);
-          const int jg = (int)readlane_u32((uint32_t)jj, fb);
-          if (flg == PLAIN_TIE) {
-            const Grid g2 = grid_of(s);
-            uint32_t bump = 0;
-            if (jg != g2.j || !tie_bump(F, g, g2.N, bump)) {
-              fail = true;
-              break;
-            }
-            const uint32_t tot = g2.N + readlane_u32(sm, fb) + bump;
-            if (tot >= kGridTop) {
-              fail = true;
-              break;
-            }
-            s = grid_value(tot, g2.j);
-            ++g;
-            continue;
-          }
-          if (flg == PLAIN) {
-            fail = true;  // the running sum is not in the predicted binade
-            break;
-          }
-          const int slot = (int)readlane_u32((uint32_t)sd, fb);
-          if (slot < 0 || g < g_from) {
-            more = true;
-            break;
-          }
-          s = resolve_exact(s, slot, jg, F);
-          ++g;
-        }
-      }
+      // EXACT slots (any order; a row with more than DCAP takes further rounds in index order)
+      const uint64_t exm = __ballot(ex);
+      int base = 0;
       if (lane == 0) {
-        F.s_run = s;
-        F.next_g = g;
-        if (fail) F.fail = 1u;
-        F.done = (!fail && !more) ? 1 : 0;
+        if (exm != 0ull) base = (int)atomicAdd((uint32_t*)&F.nslot, (uint32_t)__popcll(exm));
+        if (bad) atomicOr(&F.fail, 1u);
+        if (__ballot(fl) != 0ull) atomicOr(&F.flood, 1u);
+      }
+      base = __builtin_amdgcn_readfirstlane(base);
+      if (have) {
+        const int slot = base + __popcll(exm & lt_mask);
+        const bool got = ex && slot < DCAP;
+        F.sdump[w + W * lane] = (int8_t)(got ? slot : -1);
+        if (got) F.slotseg[slot] = (int16_t)(w + W * lane);
       }
     }
     __syncthreads();
-    if (F.done) break;
+    const bool flood = F.flood != 0u;
+    const float theta = flood ? kInfS : P.cand_theta;
+
+    // ---- phase S: integer sums of PLAIN segments, four segments per step;
+    // specials queued with the segment's integer sum before them (lower
+    // bracket), and settled when the queue is full
+    int qn = 0;
+    float v2[2];
+    auto reread = [&]() {  // the queued logits (wave-uniform count qn)
+  #pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int i = h * kWave + lane;
+        v2[h] = xr[i < qn ? F.qpos[w][i] : 0u];
+      }
+    };
+    auto settle = [&]() {
+      settle_specials(F, Q, P, row, w, qn, v2, Rw, cw, m, theta, t1);
+      qn = 0;
+    };
+    bool qovf = false;
+    if (!F.fail) {
+      const uint32_t flag_l = have ? (uint32_t)F.sflag[w + W * lane] : (uint32_t)EXACT_PRED;
+      const int j_l = have ? (int)F.sj[w + W * lane] : 0;
+      const GridConst gc_l = grid_const(j_l, Rw, theta);
+      auto lds_q = [&](int k) {
+        int l4 = lane_id() * 4;
+        asm volatile("" : "+v"(l4));  // recomputed here rather than kept live through the loop
+        return *reinterpret_cast<const float4*>(&F.u.data[w][min(max(k - KV, 0), KL - 1)][l4]);
+      };
+      for (int k0 = 0; k0 < nseg_w; k0 += 4) {
+        llz_f4v qa, qb, qc, qd;  // native vectors: an array or HIP's float4 struct here ends up in scratch
+        switch (k0 >> 2) {
+  #define LLZ_GET(i) to_v4((i) < KV ? d[(i) < KV ? (i) : 0] : lds_q(i))
+  #define LLZ_CASE(b)                 \
+    case b:                           \
+      qa = LLZ_GET(4 * (b) + 0);      \
+      qb = LLZ_GET(4 * (b) + 1);      \
+      qc = LLZ_GET(4 * (b) + 2);      \
+      qd = LLZ_GET(4 * (b) + 3);      \
+      break;
+          LLZ_CASE(0) LLZ_CASE(1) LLZ_CASE(2) LLZ_CASE(3) LLZ_CASE(4) LLZ_CASE(5)
+          LLZ_CASE(6) LLZ_CASE(7) LLZ_CASE(8) LLZ_CASE(9) LLZ_CASE(10) LLZ_CASE(11)
+  #undef LLZ_CASE
+  #undef LLZ_GET
+          default:
+            qa = to_v4(lds_q(k0 + 0));
+            qb = to_v4(lds_q(k0 + 1));
+            qc = to_v4(lds_q(k0 + 2));
+            qd = to_v4(lds_q(k0 + 3));
+        }
+        // per segment s: w1..w3 = the lane's integer sums before its elements
+        // 1..3, acc = the lane's sum, incl = the inclusive scan over lanes
+        uint32_t acc4[4], incl4[4], wa[4], wb[4], wc[4], spm = 0;
+        bool pl4[4];
+  #pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int k = k0 + s;
+          const int kl = min(k, kWave - 1);
+          pl4[s] = k < nseg_w && readlane_u32(flag_l, kl) == (uint32_t)PLAIN;
+          const float sc_lo = readlane_f32(gc_l.sc_lo, kl);
+          const float sc_hi = readlane_f32(gc_l.sc_hi, kl);
+          const float tspec = readlane_f32(gc_l.tspec, kl);
+          const llz_f4v qv4 = s == 0 ? qa : s == 1 ? qb : s == 2 ? qc : qd;  // s is a constant here
+          const float qs[4] = {qv4.x, qv4.y, qv4.z, qv4.w};
+          uint32_t b[4], sp = 0;
+  #pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const float rlo = fmaf(qs[c], sc_lo, MAGIC);
+            const float rhi = fmaf(qs[c], sc_hi, MAGIC);
+            b[c] = __float_as_uint(rlo);
+            sp |= (rlo != rhi || rhi >= tspec) ? (1u << c) : 0u;
+          }
+          // absent positions hold q = 0, so rlo = rhi = MAGIC: never special
+          // (tspec > MAGIC for PLAIN segments outside flood mode, and theta is
+          // +inf in flood mode)
+          wa[s] = b[0] - MAGIC_BITS;
+          wb[s] = wa[s] + b[1] - MAGIC_BITS;
+          wc[s] = wb[s] + b[2] - MAGIC_BITS;
+          acc4[s] = wc[s] + b[3] - MAGIC_BITS;
+          if (!pl4[s]) sp = 0;
+          spm |= sp << (4 * s);
+        }
+  #pragma unroll
+        for (int s = 0; s < 4; ++s)
+          incl4[s] = wave_incl_scan_op(acc4[s], 0u, [](uint32_t a, uint32_t b) { return a + b; });
+        if (lane == kWave - 1) {
+  #pragma unroll
+          for (int s = 0; s < 4; ++s)
+            if (pl4[s]) F.ssum[w + W * (k0 + s)] = incl4[s];
+        }
+        if (__ballot(spm != 0u) != 0ull) {
+          // every lane appends its own specials after those of the lanes below it
+          const uint32_t my = (uint32_t)__popc(spm);
+          const uint32_t incl = wave_incl_scan_op(my, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+          const int total = (int)lane_readlast(incl);
+          if (qn + total > QCAP) {
+            reread();
+            settle();
+          }
+          if (total > QCAP) {
+            qovf = true;  // more specials in four segments than the queue holds
+          } else {
+            int slot = qn + (int)(incl - my);
+            uint32_t rem = spm;
+            while (rem != 0u) {
+              const int bt = __ffs(rem) - 1;
+              rem &= rem - 1u;
+              const int s = bt >> 2, c = bt & 3;
+              const uint32_t ex_s = s == 0 ? incl4[0] - acc4[0] : s == 1 ? incl4[1] - acc4[1]
+                                  : s == 2 ? incl4[2] - acc4[2] : incl4[3] - acc4[3];
+              const uint32_t wa_s = s == 0 ? wa[0] : s == 1 ? wa[1] : s == 2 ? wa[2] : wa[3];
+              const uint32_t wb_s = s == 0 ? wb[0] : s == 1 ? wb[1] : s == 2 ? wb[2] : wb[3];
+              const uint32_t wc_s = s == 0 ? wc[0] : s == 1 ? wc[1] : s == 2 ? wc[2] : wc[3];
+              F.qpos[w][slot] = (uint32_t)((w + W * (k0 + s)) * SEG + lane4 + c);
+              F.qpre[w][slot] = ex_s + (c == 0 ? 0u : c == 1 ? wa_s : c == 2 ? wb_s : wc_s);
+              ++slot;
+            }
+            qn += total;
+          }
+        }
+      }
+      if (qovf && lane == 0) atomicOr(&F.fail, 1u);
+    }
+
+    // ---- phase F+X: the remaining specials and this round's EXACT slots in
+    // one round trip (the slots overlay the LDS-resident segments: every wave
+    // is past phase S)
+    __syncthreads();
+    if (!F.fail) {
+      reread();
+      const int nslot = min(F.nslot, DCAP);
+      exact_loads<FASTLD>(F, xr, w, nslot, n);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      settle();
+      exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
+    }
+    __syncthreads();
+
+    // ---- phase C: the walk in index order; EXACT segments beyond the slots
+    // in further rounds
+    for (int round = 0; !F.fail; ++round) {
+      const int g_from = F.next_g;
+      if (round > 0) {
+        if (w == 0) {  // slots for the EXACT segments from g_from on, in order
+          int cnt = 0;
+          for (int b = g_from; b < G; b += kWave) {
+            const int g = b + lane;
+            const bool ex = g < G && (F.sflag[g] == EXACT_PRED || F.sflag[g] == EXACT_DONE);
+            const uint64_t mk = __ballot(ex);
+            const int slot = cnt + __popcll(mk & lt_mask);
+            if (ex) {
+              F.sdump[g] = (int8_t)(slot < DCAP ? slot : -1);
+              if (slot < DCAP) F.slotseg[slot] = (int16_t)g;
+            }
+            cnt += __popcll(mk);
+          }
+          if (lane == 0) F.nslot = min(cnt, DCAP);
+        }
+        __syncthreads();
+        const int nslot = F.nslot;
+        exact_loads<FASTLD>(F, xr, w, nslot, n);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
+        __syncthreads();
+      }
+      if (w == 0) {
+        float s = F.s_run;
+        int g = g_from;
+        bool fail = false, more = false;
+        while (g < G && !fail && !more) {
+          // this group of 64 segments, one per lane
+          const int gb = g & ~(kWave - 1);
+          const int gend = min(gb + kWave, G);
+          const int gg = gb + lane;
+          uint32_t fl = PLAIN, sm = 0;
+          int jj = 0, sd = -1;
+          if (gg < gend) {
+            fl = F.sflag[gg];
+            jj = F.sj[gg];
+            sm = min(F.ssum[gg], kSat);
+            sd = F.sdump[gg];
+          }
+          // inclusive prefix of the group's sums (each <= 2^25: no wrap)
+          const uint32_t pincl = wave_incl_scan_op(sm, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+          while (g < gend) {
+            const Grid gr = grid_of(s);
+            const int p = g - gb;
+            const bool okp = fl == PLAIN && jj == gr.j;
+            const uint64_t bad = __ballot(lane >= p && gg < gend && !okp);
+            const int fb = bad ? __ffsll((long long)bad) - 1 : gend - gb;
+            if (fb > p) {
+              // PLAIN run [p, fb): terms are >= 0, so it stays in the binade
+              // exactly when its total does
+              const uint32_t tot = readlane_u32(pincl, fb - 1) - (p > 0 ? readlane_u32(pincl, p - 1) : 0u);
+              if (gr.N + tot >= kGridTop) {
+                fail = true;  // a crossing the prediction did not see
+                break;
+              }
+              s = grid_value(gr.N + tot, gr.j);
+              g = gb + fb;
+            }
+            if (g >= gend) break;
+            // segment g is an event
+            const uint32_t flg = readlane_u32(fl, fb);
+            const int jg = (int)readlane_u32((uint32_t)jj, fb);
+            if (flg == PLAIN_TIE) {
+              const Grid g2 = grid_of(s);
+              uint32_t bump = 0;
+              if (jg != g2.j || !tie_bump(F, g, g2.N, bump)) {
+                fail = true;
+                break;
+              }
+              const uint32_t tot = g2.N + readlane_u32(sm, fb) + bump;
+              if (tot >= kGridTop) {
+                fail = true;
+                break;
+              }
+              s = grid_value(tot, g2.j);
+              ++g;
+              continue;
+            }
+            if (flg == PLAIN) {
+              fail = true;  // the running sum is not in the predicted binade
+              break;
+            }
+            const int slot = (int)readlane_u32((uint32_t)sd, fb);
+            if (slot < 0 || g < g_from) {
+              more = true;
+              break;
+            }
+            s = resolve_exact(s, slot, jg, F);
+            ++g;
+          }
+        }
+        if (lane == 0) {
+          F.s_run = s;
+          F.next_g = g;
+          if (fail) F.fail = 1u;
+          F.done = (!fail && !more) ? 1 : 0;
+        }
+      }
+      __syncthreads();
+      if (F.done) break;
+    }
+
+    // ---- hand-over to the selection stage
+    certified = F.fail == 0u;
+    S = F.s_run;
+    cc = flood ? (uint32_t)kCandCap + 1u : F.ncand;
   }
 
-  if (t == 0) {
-    if (!F.fail) {
-      rs_out[0] = m;
-      rs_out[1] = F.s_run;
-      rs_out[2] = __uint_as_float(flood ? (uint32_t)kCandCap + 1u : F.ncand);
-      rs_out[3] = 0.0f;
-    } else {
-      // not certified: k_select runs the streaming normaliser on this row
-      rs_out[0] = m;
-      rs_out[1] = 0.0f;
-      rs_out[2] = __uint_as_float(0u);
-      rs_out[3] = 1.0f;
-    }
-  }
+  // ---- the selection stage, on the same workgroup and shared memory
+  __syncthreads();  // F is read: the selection reuses the memory
+  select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified);
 }
 
 }  // namespace
 
-hipError_t launch_stats(const RowParams& P, const RowPtrs& Q, hipStream_t st) {
+// One launch per call: every row's statistics, then its selection.
+hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_begin, hipEvent_t ev_end,
+                         hipStream_t st) {
+  if (ev_begin && hipEventRecord(ev_begin, st) != hipSuccess) return hipErrorUnknown;
   if ((P.flags & kFlagVecSrc) != 0 && (P.n % 4) == 0)
     hipLaunchKernelGGL(k_stats<true>, dim3(P.rows), dim3(NT), 0, st, P, Q);
   else
     hipLaunchKernelGGL(k_stats<false>, dim3(P.rows), dim3(NT), 0, st, P, Q);
-  return hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (ev_end && hipEventRecord(ev_end, st) != hipSuccess) return hipErrorUnknown;
+  return hipSuccess;
 }
 
 }  // namespace llz
