@@ -532,6 +532,107 @@ __device__ __noinline__ NormResult select_norm_fallback(const RowParams P, const
 __device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q, SampleShared& sh, int bank,
                                              float m, float S, uint32_t path);
 
+constexpr int kShortMax = 256;  // longest candidate list of the short path
+
+// The selection for a short candidate list without typical-p (the common
+// case): a rank sort by every wave, then filters, total and draw by wave 0
+// alone (sampler.zig:92-126, 156-168), with the same certified-prefix rules
+// as prefix_filters.  Returns false, on every thread, when elements outside
+// the list decide the cut: the caller then takes the full-row fallback.
+__device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& Q, SampleShared& sh, int c,
+                                             float m, float S, uint32_t path) {
+  const int row = blockIdx.x;
+  const int t = (int)threadIdx.x, lane = lane_id(), w = wave_id();
+  const int n = P.n;
+  uint64_t* key = sh.cand;               // (~p bits, id): ascending = (p desc, id asc)
+  uint32_t* rank = sh.u.post.aux_pos;
+  uint64_t* srt = sh.u.post.aux;
+  // probabilities as sampler.zig:90 computes them
+  for (int i = t; i < c; i += kNT) {
+    const uint64_t a = key[i];
+    const float p = __uint_as_float((uint32_t)(a >> 32)) / S;
+    key[i] = ((uint64_t)(~__float_as_uint(p)) << 32) | (uint32_t)a;
+    rank[i] = 0;
+  }
+  lds_barrier();
+  // rank = number of smaller keys (keys are distinct: the ids are); wave w
+  // counts against its eighth of the list
+  {
+    constexpr int NW = kNT / kWave;
+    const int j0 = (w * c) / NW, j1 = ((w + 1) * c) / NW;
+    for (int i = lane; i < c; i += kWave) {
+      const uint64_t ki = key[i];
+      uint32_t r = 0;
+      for (int j = j0; j < j1; ++j) r += key[j] < ki ? 1u : 0u;
+      if (r != 0u) atomicAdd(&rank[i], r);
+    }
+  }
+  lds_barrier();
+  for (int i = t; i < c; i += kNT) srt[rank[i]] = key[i];
+  lds_barrier();
+  if (w == 0) {
+    auto pq = [&](int q) { return __uint_as_float(~(uint32_t)(srt[q] >> 32)); };
+    // certified prefix M: every element outside the list has p <= theta / S
+    const float p_nc = P.cand_theta / S;
+    int M = c;
+    if (P.cand_theta > 0.0f) {
+      M = 0;
+      for (int b = 0; b < c; b += kWave) M += __popcll(__ballot(b + lane < c && pq(b + lane) > p_nc));
+    }
+    // top-k, min-p, top-p (sampler.zig:106-126): each keeps a prefix
+    const int Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
+    int Km = n;
+    if (P.min_p > 0.0f) {
+      const float thr = (1.0f / S) * P.min_p;  // probs[indices[0]] = 1 / S: the row maximum has e = 1
+      int cnt = 0;
+      for (int b = 0; b < M; b += kWave) cnt += __popcll(__ballot(b + lane < M && pq(b + lane) >= thr));
+      if (cnt < M) Km = cnt;
+      else if (M < n && thr > p_nc) Km = M;
+    }
+    int K = min(Kk, Km);
+    bool undecided = false;
+    if (P.top_p > 0.0f && P.top_p < 1.0f) {
+      const int lim = min(K, M);
+      int st;
+      wave_seq_list<false>(0.0f, lim, P.top_p, st, pq);
+      if (st >= 0) K = min(K, st);
+      else if (K > M) undecided = true;
+    }
+    if (K > M) undecided = true;
+    if (!undecided) {
+      // total and draw (sampler.zig:156-168)
+      int st;
+      const float total = wave_seq_list<false>(0.0f, K, -1.0f, st, pq);
+      const uint32_t tok0 = (uint32_t)srt[0];
+      uint32_t token = tok0, consumed = 0;
+      if (total > 0.0f) {
+        consumed = 1;
+        wave_seq_list<true>(Q.uniforms[row] * total, K, -1.0f, st, pq);
+        if (st >= 0) token = (uint32_t)srt[st];
+      }
+      if (Q.kept_ids || Q.kept_probs) {
+        for (int q = lane; q < K && q < P.kept_cap; q += kWave) {
+          if (Q.kept_ids) Q.kept_ids[(int64_t)row * P.kept_cap + q] = (uint32_t)srt[q];
+          if (Q.kept_probs) Q.kept_probs[(int64_t)row * P.kept_cap + q] = pq(q);
+        }
+      }
+      if (lane == 0) {
+        Q.tokens[row] = token;
+        if (Q.consumed) Q.consumed[row] = (uint8_t)consumed;
+        if (Q.kept_count) Q.kept_count[row] = (uint32_t)K;
+        if (Q.row_stats) {
+          float* rs = Q.row_stats + (int64_t)row * 4;
+          rs[0] = m; rs[1] = S; rs[2] = 0.0f; rs[3] = total;
+        }
+        if (Q.status) Q.status[row] = path;
+      }
+    }
+    if (lane == 0) sh.misc[0] = undecided ? 1u : 0u;
+  }
+  lds_barrier();
+  return sh.misc[0] == 0u;
+}
+
 // The rest of sampleWithRandom (sampler.zig:89-168) for row blockIdx.x,
 // after k_stats' phases: from the row maximum m, the normaliser S and the
 // candidate list in Q.cand (cc entries), or, for a row k_stats could not
@@ -610,6 +711,10 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   const uint32_t cc = sh.cand_count;
   const bool ovf = cc > (uint32_t)kCap;
   const int c = ovf ? kCap : (int)cc;
+  if (!ovf && c <= kShortMax && !(P.typical_p > 0.0f && P.typical_p < 1.0f)) {
+    if (!select_short(P, Q, sh, c, m, S, path)) select_full_row(P, Q, sh, bank, m, S, path);
+    return;
+  }
   const int csort = next_pow2(c);
   for (int i = t; i < csort; i += kNT) {
     if (i < c) {
