@@ -63,11 +63,12 @@ constexpr int SPWMAX = KV + KL;     // segments per wave at most (<= 64: one lan
 constexpr int GMAX = W * SPWMAX;    // 504 segments = 129024 logits
 constexpr int QCAP = 128;           // special queue capacity per wave (flushed when full)
 constexpr int DCAP = 48;            // EXACT segments evaluated per round
+constexpr int NG = 6;               // grids tabulated per EXACT segment at most
 constexpr float DELTA = 0x1p-10f;   // relative margin of the binade prediction
 constexpr float MAGIC = 12582912.0f;            // 1.5 * 2^23
 constexpr uint32_t MAGIC_BITS = 0x4b400000u;    // its bit pattern
-constexpr int TCAP = 160;          // tie records per row
-// PLAIN: integer sum on one grid; PLAIN_TIE: the same with tie records;
+// PLAIN: integer sum on one grid; PLAIN_TIE: the same, plus the units its
+// ties add (sbump);
 // EXACT_PRED: predicted binade change, its candidates not collected yet;
 // EXACT_DONE: the same, collected.
 enum : uint8_t { PLAIN = 0, EXACT_PRED = 1, PLAIN_TIE = 2, EXACT_DONE = 3 };
@@ -77,19 +78,11 @@ static_assert(GMAX <= 8 * 64, "the combine holds eight segments per lane");
 }  // namespace fastp
 
 // EXACT segments: exact terms, per-lane inclusive prefixes of their
-// roundings on grids sj and sj+1, and the lanes holding a tie.
+// roundings on grids sj .. sj + sng - 1, and the lanes holding a tie.
 struct ExactSlots {
   float dump[fastp::DCAP][fastp::SEG];
-  uint32_t pref[fastp::DCAP][2][kWave];
-  uint64_t tmask[fastp::DCAP][2];
-};
-
-// A special term whose exact value is an exact half-integer of its grid:
-// its rounding follows the parity of the running integer just before it.
-struct TieRec {
-  uint32_t pos;  // position in the row
-  uint32_t pre;  // integer sum of the segment's terms before it (exact roundings, ties down)
-  uint32_t k;    // its rounding, down
+  uint32_t pref[fastp::DCAP][fastp::NG][kWave];
+  uint64_t tmask[fastp::DCAP][fastp::NG];
 };
 
 struct FastShared {
@@ -99,12 +92,14 @@ struct FastShared {
   } u;
   union {
     float aseg[fastp::GMAX];                    // segment sums of q (phases L, M)
-    TieRec tie[fastp::TCAP];                    // after phase M
   } v;
   uint32_t ssum[fastp::GMAX];                   // PLAIN: integer sum on grid sj
   int8_t sj[fastp::GMAX];                       // PLAIN: its binade; EXACT: first binade tabulated
+  uint8_t sng[fastp::GMAX];                     // EXACT: number of binades tabulated
   uint8_t sflag[fastp::GMAX];
   int8_t sdump[fastp::GMAX];                    // EXACT: slot in `dump`, or -1
+  uint8_t sbump[fastp::GMAX];                   // PLAIN_TIE: units its ties add when the segment
+                                                //   starts at an even (bits 0-3) or odd (4-7) integer
   uint32_t qpos[fastp::W][fastp::QCAP];         // special queue: position
   uint32_t qpre[fastp::W][fastp::QCAP];         //   and its segment's integer sum before it (lower bracket)
   int16_t slotseg[fastp::DCAP];                 // segment held by each EXACT slot
@@ -115,7 +110,6 @@ struct FastShared {
   uint32_t wflag[fastp::W]; //   bit 0: not certifiable, bit 1: candidate flood
   int wnex[fastp::W];       //   number of its EXACT segments
   uint32_t ncand;
-  uint32_t ntie;
   int nslot;      // EXACT slots in use this round
   uint32_t fail;
   uint32_t flood;

@@ -101,7 +101,7 @@ __device__ __forceinline__ void exact_loads(FastShared& F, const float* xr, int 
 
 // Exact terms of this wave's EXACT slots (loaded and waited for), their
 // candidates (once per segment), and the per-lane inclusive prefix tables of
-// the roundings on grids sj and sj+1 with the lanes holding a tie.
+// the roundings on grids sj .. sj + sng - 1 with the lanes holding a tie.
 __device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
                                                int nslot, int n, float m, float theta, bool t1) {
   const int lane = lane_id();
@@ -121,8 +121,8 @@ __device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, 
     *p = make_float4(es[0], es[1], es[2], es[3]);
     if (pred && lane == 0) F.sflag[seg] = EXACT_DONE;  // a later round must not collect them again
     const int J0 = F.sj[seg];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    const int ng = F.sng[seg];
+    for (int kk = 0; kk < ng; ++kk) {
       uint32_t sum = 0;
       bool tie_any = false;
 #pragma unroll
@@ -138,81 +138,80 @@ __device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, 
   }
 }
 
+// Combine wave: the exact accumulation of lanes p.. of a segment's exact
+// terms (x) from s by the generic exact method (llz_norm.h), for a running
+// sum outside the tabulated grids: a segment holding a term far above the
+// running sum, or a prediction miss.  Out of line: it is rare.
+__device__ __noinline__ float resolve_generic(float s, float x0, float x1, float x2, float x3, int p) {
+  const int lane = lane_id();
+  const bool live = lane >= p;
+  const float x[4] = {live ? x0 : -0.0f, live ? x1 : -0.0f, live ? x2 : -0.0f, live ? x3 : -0.0f};
+  return wave_accumulate<4>(s, x);
+}
+
+// Wave-uniform copies (scalar registers): values every lane read from the
+// same LDS address, or computed from such values, are uniform, but the
+// compiler cannot prove it and would otherwise branch on them lane by lane.
+__device__ __forceinline__ float uni_f(float x) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x))); }
+__device__ __forceinline__ uint32_t uni_u(uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); }
+__device__ __forceinline__ uint64_t uni_u64(uint64_t x) {
+  return ((uint64_t)uni_u((uint32_t)(x >> 32)) << 32) | uni_u((uint32_t)x);
+}
+
 // Combine wave: the exact sequential sum across EXACT segment `slot` from
-// the running value s, using the prefix tables (grids J0, J0+1) between
-// events and replaying the lane that holds an event term by term.
-__device__ __forceinline__ float resolve_exact(float s, int slot, int J0, const FastShared& F) {
+// the running value s, using the prefix tables (grids J0 .. J0 + ng - 1)
+// between events and replaying the lane that holds an event term by term.
+__device__ __forceinline__ void resolve_exact(float& s_io, int slot, int J0, int ng, const FastShared& F) {
   const int lane = lane_id();
   const float4 e4 = *reinterpret_cast<const float4*>(&F.u.x.dump[slot][lane * 4]);
-  const uint32_t pv0 = F.u.x.pref[slot][0][lane];
-  const uint32_t pv1 = F.u.x.pref[slot][1][lane];
-  const uint64_t tm0 = F.u.x.tmask[slot][0];
-  const uint64_t tm1 = F.u.x.tmask[slot][1];
+  float s = uni_f(s_io);
   int p = 0;  // first lane not consumed
+  if (grid_of(s).j < J0) {
+    if (s != 0.0f || J0 <= -126) {
+      s_io = uni_f(resolve_generic(s, e4.x, e4.y, e4.z, e4.w, 0));
+      return;
+    }
+    // the row's first segment starts at 0, below its tabulated grids: term
+    // by term until the running sum reaches 2^J0
+    const float lim = __uint_as_float((uint32_t)(J0 + 127) << 23);
+    do {
+      float t = s + readlane_f32(e4.x, p);
+      t = t + readlane_f32(e4.y, p);
+      t = t + readlane_f32(e4.z, p);
+      t = t + readlane_f32(e4.w, p);
+      s = uni_f(t);
+      ++p;
+    } while (p < kWave && s < lim);
+  }
   for (int guard = 0; guard <= kWave && p < kWave; ++guard) {
     const Grid gr = grid_of(s);
     const int k = gr.j - J0;
-    if (k < 0) {
-      // below the tabulated grids (the row's first segment starts at 0, so
-      // its running sum climbs through many binades): term by term until the
-      // running sum reaches grid J0
-      do {
-        s = s + readlane_f32(e4.x, p);
-        s = s + readlane_f32(e4.y, p);
-        s = s + readlane_f32(e4.z, p);
-        s = s + readlane_f32(e4.w, p);
-        ++p;
-      } while (p < kWave && grid_of(s).j < J0);
-      continue;
+    if (k < 0 || k >= ng) {
+      s = uni_f(resolve_generic(s, e4.x, e4.y, e4.z, e4.w, p));
+      break;
     }
-    if (k > 1) {
-      // above them: the generic exact accumulation
-      const float x[4] = {lane >= p ? e4.x : -0.0f, lane >= p ? e4.y : -0.0f, lane >= p ? e4.z : -0.0f,
-                          lane >= p ? e4.w : -0.0f};
-      return wave_accumulate<4>(s, x);
-    }
-    const uint32_t pv = k == 0 ? pv0 : pv1;
+    const uint32_t pv = F.u.x.pref[slot][k][lane];
+    const uint64_t tm = uni_u64(F.u.x.tmask[slot][k]);
     const uint32_t base = p > 0 ? readlane_u32(pv, p - 1) : 0u;
     const uint64_t live = p == 0 ? ~0ull : (~0ull << p);
     const bool cr = lane >= p && (pv >= kSat || gr.N + (pv - base) >= kGridTop);
-    const uint64_t ev = (__ballot(cr) | (k == 0 ? tm0 : tm1)) & live;
-    if (ev == 0ull) return grid_value(gr.N + (readlane_u32(pv, kWave - 1) - base), gr.j);
+    const uint64_t ev = (__ballot(cr) | tm) & live;
+    if (ev == 0ull) {
+      s = uni_f(grid_value(gr.N + (readlane_u32(pv, kWave - 1) - base), gr.j));
+      break;
+    }
     const int E = __ffsll((long long)ev) - 1;
-    if (E > p) s = grid_value(gr.N + (readlane_u32(pv, E - 1) - base), gr.j);
+    float t = s;
+    if (E > p) t = grid_value(gr.N + (readlane_u32(pv, E - 1) - base), gr.j);
     // the lane holding the event, term by term (sampler.zig:87)
-    s = s + readlane_f32(e4.x, E);
-    s = s + readlane_f32(e4.y, E);
-    s = s + readlane_f32(e4.z, E);
-    s = s + readlane_f32(e4.w, E);
+    t = t + readlane_f32(e4.x, E);
+    t = t + readlane_f32(e4.y, E);
+    t = t + readlane_f32(e4.z, E);
+    t = t + readlane_f32(e4.w, E);
+    s = uni_f(t);
     p = E + 1;
   }
-  return s;
-}
-
-// Combine wave: the units that the ties of PLAIN_TIE segment g add to its
-// integer sum when the segment starts at N on its grid.  Each tie rounds to
-// even: up when the running integer before it plus its rounding down is odd.
-// Returns false when the records cannot be read (more than one wave's worth).
-__device__ __forceinline__ bool tie_bump(const FastShared& F, int g, uint32_t N, uint32_t& bump) {
-  const int lane = lane_id();
-  const int nt = (int)F.ntie;
-  if (nt > kWave) return false;
-  bool mine = false;
-  TieRec tr{0u, 0u, 0u};
-  if (lane < nt) {
-    tr = F.v.tie[lane];
-    mine = (int)(tr.pos >> 8) == g;
-  }
-  bump = 0;
-  while (__ballot(mine) != 0ull) {  // in position order
-    const uint32_t pmin = wave_min_u32(mine ? tr.pos : 0xffffffffu);
-    const bool me = mine && tr.pos == pmin;
-    const int L = __ffsll((long long)__ballot(me)) - 1;
-    const uint32_t pre = readlane_u32(tr.pre, L), k = readlane_u32(tr.k, L);
-    if (((N + pre + bump + k) & 1u) != 0u) ++bump;
-    mine = mine && !me;
-  }
-  return true;
+  s_io = s;
 }
 
 // Owner wave: settle its queued specials (v2: their re-read logits, entry
@@ -250,10 +249,18 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
       if (e >= theta) push_cand(F, Q, row, e, pos2[h]);
     }
   }
+  // ties (rare): the integer sum before each (its lower-bracket prefix plus
+  // the corrections of the specials before it in the segment), then per
+  // segment the units its ties add for an even and an odd starting integer:
+  // a tie rounds up when the running integer before it plus its rounding
+  // down is odd (round half to even), and the running integer's parity
+  // depends on the segment's start only through the start's parity.
+  uint32_t tpos = 0xffffffffu, tpre = 0, tk = 0;  // this wave's ties, one per lane
+  int nt = 0;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     uint64_t tb = __ballot(tie2[h]);
-    while (tb != 0ull) {  // ties are rare
+    while (tb != 0ull) {
       const int L = __ffsll((long long)tb) - 1;
       tb &= tb - 1ull;
       const uint32_t pt = readlane_u32(pos2[h], L);
@@ -263,15 +270,39 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
         if (act2[h2] && (pos2[h2] >> 8) == (pt >> 8) && pos2[h2] < pt) c += d2[h2];
       const uint32_t pre_t = readlane_u32(pre2[h], L) + wave_sum_u32(c);
       const uint32_t k_t = readlane_u32(r2[h], L);
-      if (lane == 0) {
-        const uint32_t slot = atomicAdd(&F.ntie, 1u);
-        if (slot < (uint32_t)TCAP)
-          F.v.tie[slot] = TieRec{pt, pre_t, k_t};
-        else
-          atomicOr(&F.fail, 1u);
-        F.sflag[pt >> 8] = PLAIN_TIE;
+      if (lane == nt) {
+        tpos = pt;
+        tpre = pre_t;
+        tk = k_t;
       }
+      ++nt;
+      if (nt > kWave) break;
     }
+  }
+  if (nt > kWave) {
+    if (lane == 0) atomicOr(&F.fail, 1u);
+    return;
+  }
+  bool open_t = lane < nt;
+  while (__ballot(open_t) != 0ull) {
+    // the segment of the first remaining tie, its ties in position order
+    const uint32_t g = wave_min_u32(open_t ? tpos : 0xffffffffu) >> 8;
+    bool mine = open_t && (tpos >> 8) == g;
+    uint32_t b0 = 0, b1 = 0;
+    while (__ballot(mine) != 0ull) {
+      const uint32_t pmin = wave_min_u32(mine ? tpos : 0xffffffffu);
+      const int L = __ffsll((long long)__ballot(mine && tpos == pmin)) - 1;
+      const uint32_t pr = readlane_u32(tpre, L), kk = readlane_u32(tk, L);
+      b0 += ((0u + pr + b0 + kk) & 1u);
+      b1 += ((1u + pr + b1 + kk) & 1u);
+      mine = mine && tpos != pmin;
+    }
+    if (lane == 0) {
+      if (b0 > 15u || b1 > 15u) atomicOr(&F.fail, 1u);
+      F.sbump[g] = (uint8_t)(min(b0, 15u) | (min(b1, 15u) << 4));
+      F.sflag[g] = PLAIN_TIE;
+    }
+    open_t = open_t && (tpos >> 8) != g;
   }
 }
 
@@ -408,7 +439,6 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     F.fail = fits ? 0u : 1u;
     F.flood = 0;
     F.ncand = 0;
-    F.ntie = 0;
     F.nslot = 0;
     F.next_g = 0;
     F.s_run = 0.0f;
@@ -464,12 +494,15 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         const int ehi = (int)(__float_as_uint(hi) >> 23) - 127;
         const bool plain = lo >= 0x1p-64f && hi <= 3.0e38f && elo == ehi;
         fl = plain && ldexpf(P.cand_theta, 23 - elo) < 2.0f;
-        // EXACT: tabulate the binade the segment starts in and the next one
-        int j0 = lo >= 0x1p-126f ? elo : ehi - 1;
+        // EXACT: tabulate the binades from the one the segment starts in to
+        // the one it ends in (the row's first segment starts at 0: its NG
+        // highest, below them it is summed term by term)
+        int j0 = lo >= 0x1p-126f ? elo : ehi - (NG - 1);
         j0 = max(-126, min(j0, 126));
         const int g = w + W * lane;
         F.sflag[g] = plain ? PLAIN : EXACT_PRED;
         F.sj[g] = (int8_t)(plain ? elo : j0);
+        F.sng[g] = (uint8_t)max(1, min(ehi - j0 + 1, NG));
         ex = !plain;
       }
       // EXACT slots (any order; a row with more than DCAP takes further rounds in index order)
@@ -655,7 +688,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         __syncthreads();
       }
       if (w == 0) {
-        float s = F.s_run;
+        float s = uni_f(F.s_run);
         int g = g_from;
         bool fail = false, more = false;
         while (g < G && !fail && !more) {
@@ -663,54 +696,51 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           const int gb = g & ~(kWave - 1);
           const int gend = min(gb + kWave, G);
           const int gg = gb + lane;
-          uint32_t fl = PLAIN, sm = 0;
+          uint32_t fl = PLAIN, sm = 0, sb = 0;
           int jj = 0, sd = -1;
           if (gg < gend) {
             fl = F.sflag[gg];
             jj = F.sj[gg];
             sm = min(F.ssum[gg], kSat);
             sd = F.sdump[gg];
+            sb = F.sbump[gg];
           }
           // inclusive prefix of the group's sums (each <= 2^25: no wrap)
           const uint32_t pincl = wave_incl_scan_op(sm, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+          const uint64_t tie_lanes = __ballot(fl == PLAIN_TIE);
           while (g < gend) {
             const Grid gr = grid_of(s);
             const int p = g - gb;
-            const bool okp = fl == PLAIN && jj == gr.j;
+            const bool okp = (fl == PLAIN || fl == PLAIN_TIE) && jj == gr.j;
             const uint64_t bad = __ballot(lane >= p && gg < gend && !okp);
             const int fb = bad ? __ffsll((long long)bad) - 1 : gend - gb;
             if (fb > p) {
-              // PLAIN run [p, fb): terms are >= 0, so it stays in the binade
-              // exactly when its total does
-              const uint32_t tot = readlane_u32(pincl, fb - 1) - (p > 0 ? readlane_u32(pincl, p - 1) : 0u);
+              // run [p, fb) on grid gr.j: terms are >= 0, so it stays in the binade
+              // exactly when its total does.  A PLAIN_TIE segment adds the units its
+              // ties take for the parity of the integer it starts at.
+              const uint32_t before = p > 0 ? readlane_u32(pincl, p - 1) : 0u;
+              uint32_t bump = 0;
+              uint64_t tl = tie_lanes & (~0ull << p) & (fb >= kWave ? ~0ull : ((1ull << fb) - 1ull));
+              while (tl != 0ull) {
+                const int L = __ffsll((long long)tl) - 1;
+                tl &= tl - 1ull;
+                const uint32_t at = gr.N + ((L > 0 ? readlane_u32(pincl, L - 1) : 0u) - before) + bump;
+                const uint32_t bb = readlane_u32(sb, L);
+                bump += (at & 1u) ? (bb >> 4) : (bb & 15u);
+              }
+              const uint32_t tot = readlane_u32(pincl, fb - 1) - before + bump;
               if (gr.N + tot >= kGridTop) {
                 fail = true;  // a crossing the prediction did not see
                 break;
               }
-              s = grid_value(gr.N + tot, gr.j);
+              s = uni_f(grid_value(gr.N + tot, gr.j));
               g = gb + fb;
             }
             if (g >= gend) break;
-            // segment g is an event
+            // segment g is an event: an EXACT segment, or a PLAIN one whose binade
+            // the running sum is not in
             const uint32_t flg = readlane_u32(fl, fb);
-            const int jg = (int)readlane_u32((uint32_t)jj, fb);
-            if (flg == PLAIN_TIE) {
-              const Grid g2 = grid_of(s);
-              uint32_t bump = 0;
-              if (jg != g2.j || !tie_bump(F, g, g2.N, bump)) {
-                fail = true;
-                break;
-              }
-              const uint32_t tot = g2.N + readlane_u32(sm, fb) + bump;
-              if (tot >= kGridTop) {
-                fail = true;
-                break;
-              }
-              s = grid_value(tot, g2.j);
-              ++g;
-              continue;
-            }
-            if (flg == PLAIN) {
+            if (flg == PLAIN || flg == PLAIN_TIE) {
               fail = true;  // the running sum is not in the predicted binade
               break;
             }
@@ -719,7 +749,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
               more = true;
               break;
             }
-            s = resolve_exact(s, slot, jg, F);
+            resolve_exact(s, slot, (int)readlane_u32((uint32_t)jj, fb), F.sng[g], F);
             ++g;
           }
         }
