@@ -214,72 +214,110 @@ __device__ __forceinline__ void resolve_exact(float& s_io, int slot, int J0, int
   s_io = s;
 }
 
-// Owner wave: settle its queued specials (v2: their re-read logits, entry
-// h * 64 + lane): exact terms, corrections of the segment sums, candidates,
-// and a record per tie.  A segment's specials are always queued and settled
-// together, so the integer sum before a tie is its lower-bracket prefix plus
-// the corrections of the specials before it in the same segment.
+// Owner wave: settle its queued lanes (v4q[h]: the re-read logits of entry
+// h * 64 + lane, four consecutive positions from the entry's position).
+// Each term's lower-bracket rounding is recomputed exactly as phase S summed
+// it; the terms it could not certify are evaluated with the exact exp and
+// the difference corrects the segment sum.  Candidates are collected, and
+// per segment with ties the units they add (PLAIN_TIE, sbump).  A
+// segment's lanes are always queued and settled together, so the integer
+// sum before a tie is the lane's queued prefix, plus the corrections of the
+// segment's lanes below it, plus the lane's exact roundings before it.
 __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
-                                                int qn, const float (&v2)[2], float Rw, float cw, float m,
+                                                int qn, const float4 (&v4q)[2], float Rw, float cw, float m,
                                                 float theta, bool t1) {
   const int lane = lane_id();
-  uint32_t pos2[2], pre2[2], d2[2], r2[2];
-  bool act2[2], tie2[2];
+  const int n = P.n;
+  uint32_t pos2[2], pre2[2], rl[2][4], rx[2][4];
+  int j2[2];
+  bool act2[2];
+  uint32_t spm = 0;
+  // brackets as phase S computed them
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int i = h * kWave + lane;
     act2[h] = i < qn;
     pos2[h] = act2[h] ? F.qpos[w][i] : 0u;
     pre2[h] = act2[h] ? F.qpre[w][i] : 0u;
-    d2[h] = 0u;
-    r2[h] = 0u;
-    tie2[h] = false;
-    if (act2[h]) {
-      const int seg = (int)(pos2[h] >> 8);
-      const int j = F.sj[seg];
-      const GridConst gc = grid_const(j, Rw, theta);
-      const float q = __builtin_amdgcn_exp2f(fmaf(v2[h], P.l2e_t, -cw));  // phase L's estimate, bit for bit
-      const uint32_t rl = __float_as_uint(fmaf(q, gc.sc_lo, MAGIC)) - MAGIC_BITS;
-      const float e = exact_term(v2[h], m, P.temperature, t1);
-      bool tie;
-      r2[h] = grid_round(e, j, tie);
-      tie2[h] = tie;
-      d2[h] = r2[h] - rl;
-      atomicAdd(&F.ssum[seg], d2[h]);
-      if (e >= theta) push_cand(F, Q, row, e, pos2[h]);
+    j2[h] = F.sj[pos2[h] >> 8];
+    const GridConst gc = grid_const(j2[h], Rw, theta);
+    const uint32_t tspec = __float_as_uint(gc.tspec);
+    const float vv[4] = {v4q[h].x, v4q[h].y, v4q[h].z, v4q[h].w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool present = act2[h] && (int)pos2[h] + c < n;
+      const float q = present ? __builtin_amdgcn_exp2f(fmaf(vv[c], P.l2e_t, -cw)) : 0.0f;  // phase L's q, bit for bit
+      const uint32_t lo = __float_as_uint(fmaf(q, gc.sc_lo, MAGIC));
+      const uint32_t hi = __float_as_uint(fmaf(q, gc.sc_hi, MAGIC));
+      rl[h][c] = lo - MAGIC_BITS;
+      rx[h][c] = rl[h][c];
+      if (present && (lo != hi || hi >= tspec)) spm |= 1u << (4 * h + c);
     }
   }
-  // ties (rare): the integer sum before each (its lower-bracket prefix plus
-  // the corrections of the specials before it in the segment), then per
-  // segment the units its ties add for an even and an odd starting integer:
-  // a tie rounds up when the running integer before it plus its rounding
-  // down is odd (round half to even), and the running integer's parity
-  // depends on the segment's start only through the start's parity.
+  // exact roundings of the special terms (about one per lane)
+  uint32_t tiem = 0, rem = spm;
+  while (rem != 0u) {
+    const int bt = __ffs(rem) - 1;
+    rem &= rem - 1u;
+    const int h = bt >> 2, c = bt & 3;
+    const float4 vh = h == 0 ? v4q[0] : v4q[1];
+    const float v = c == 0 ? vh.x : c == 1 ? vh.y : c == 2 ? vh.z : vh.w;
+    const float e = exact_term(v, m, P.temperature, t1);
+    bool tie;
+    const uint32_t r = grid_round(e, h == 0 ? j2[0] : j2[1], tie);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) rx[hh][cc] = bt == 4 * hh + cc ? r : rx[hh][cc];
+    if (tie) tiem |= 1u << bt;
+    if (e >= theta) push_cand(F, Q, row, e, (h == 0 ? pos2[0] : pos2[1]) + (uint32_t)c);
+  }
+  uint32_t corr2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    corr2[h] = (rx[h][0] - rl[h][0]) + (rx[h][1] - rl[h][1]) + (rx[h][2] - rl[h][2]) + (rx[h][3] - rl[h][3]);
+    if (act2[h] && corr2[h] != 0u) atomicAdd(&F.ssum[pos2[h] >> 8], corr2[h]);
+  }
+  if (__ballot(tiem != 0u) == 0ull) return;
+
+  // ties (rare): the integer sum before each, then per segment the units
+  // its ties add for an even and an odd starting integer (a tie rounds up
+  // when the running integer before it plus its rounding down is odd; the
+  // running integer's parity depends on the start only through its parity)
   uint32_t tpos = 0xffffffffu, tpre = 0, tk = 0;  // this wave's ties, one per lane
   int nt = 0;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    uint64_t tb = __ballot(tie2[h]);
-    while (tb != 0ull) {
-      const int L = __ffsll((long long)tb) - 1;
-      tb &= tb - 1ull;
-      const uint32_t pt = readlane_u32(pos2[h], L);
+    uint64_t lanes = __ballot((tiem >> (4 * h)) & 15u);
+    while (lanes != 0ull) {
+      const int L = __ffsll((long long)lanes) - 1;
+      lanes &= lanes - 1ull;
+      const uint32_t p4 = readlane_u32(pos2[h], L);
+      // corrections of the segment's lanes below this one
       uint32_t c = 0;
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2)
-        if (act2[h2] && (pos2[h2] >> 8) == (pt >> 8) && pos2[h2] < pt) c += d2[h2];
-      const uint32_t pre_t = readlane_u32(pre2[h], L) + wave_sum_u32(c);
-      const uint32_t k_t = readlane_u32(r2[h], L);
-      if (lane == nt) {
-        tpos = pt;
-        tpre = pre_t;
-        tk = k_t;
+        if (act2[h2] && (pos2[h2] >> 8) == (p4 >> 8) && pos2[h2] < p4) c += corr2[h2];
+      const uint32_t below = readlane_u32(pre2[h], L) + wave_sum_u32(c);
+      const uint32_t tb = readlane_u32((tiem >> (4 * h)) & 15u, L);
+      uint32_t within = 0;
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const uint32_t r = readlane_u32(rx[h][cc], L);
+        if ((tb >> cc) & 1u) {
+          if (lane == nt) {
+            tpos = p4 + (uint32_t)cc;
+            tpre = below + within;
+            tk = r;
+          }
+          ++nt;
+        }
+        within += r;
       }
-      ++nt;
-      if (nt > kWave) break;
+      if (nt > kWave - 4) break;
     }
   }
-  if (nt > kWave) {
+  if (nt > kWave - 4) {
     if (lane == 0) atomicOr(&F.fail, 1u);
     return;
   }
@@ -525,20 +563,23 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     const bool flood = F.flood != 0u;
     const float theta = flood ? kInfS : P.cand_theta;
 
-    // ---- phase S: integer sums of PLAIN segments, four segments per step;
-    // specials queued with the segment's integer sum before them (lower
-    // bracket), and settled when the queue is full
+    // ---- phase S: integer sums of PLAIN segments, four segments per step.
+    // A lane whose roundings a segment cannot certify (its lower and upper
+    // bracket sums differ, or a term reaches tspec: large terms and
+    // candidates) is queued as (position of its first term, the segment's
+    // integer sum before it), and the queue is settled when full.
     int qn = 0;
-    float v2[2];
-    auto reread = [&]() {  // the queued logits (wave-uniform count qn)
-  #pragma unroll
+    float4 v4q[2];
+    auto reread = [&]() {  // the queued lanes' logits (wave-uniform count qn)
+#pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int i = h * kWave + lane;
-        v2[h] = xr[i < qn ? F.qpos[w][i] : 0u];
+        const int pos = i < qn ? (int)F.qpos[w][i] : 0;
+        v4q[h] = FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n);
       }
     };
     auto settle = [&]() {
-      settle_specials(F, Q, P, row, w, qn, v2, Rw, cw, m, theta, t1);
+      settle_specials(F, Q, P, row, w, qn, v4q, Rw, cw, m, theta, t1);
       qn = 0;
     };
     bool qovf = false;
@@ -554,67 +595,68 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       for (int k0 = 0; k0 < nseg_w; k0 += 4) {
         llz_f4v qa, qb, qc, qd;  // native vectors: an array or HIP's float4 struct here ends up in scratch
         switch (k0 >> 2) {
-  #define LLZ_GET(i) to_v4((i) < KV ? d[(i) < KV ? (i) : 0] : lds_q(i))
-  #define LLZ_CASE(b)                 \
-    case b:                           \
-      qa = LLZ_GET(4 * (b) + 0);      \
-      qb = LLZ_GET(4 * (b) + 1);      \
-      qc = LLZ_GET(4 * (b) + 2);      \
-      qd = LLZ_GET(4 * (b) + 3);      \
-      break;
+#define LLZ_GET(i) to_v4((i) < KV ? d[(i) < KV ? (i) : 0] : lds_q(i))
+#define LLZ_CASE(b)                 \
+      case b:                           \
+        qa = LLZ_GET(4 * (b) + 0);      \
+        qb = LLZ_GET(4 * (b) + 1);      \
+        qc = LLZ_GET(4 * (b) + 2);      \
+        qd = LLZ_GET(4 * (b) + 3);      \
+        break;
           LLZ_CASE(0) LLZ_CASE(1) LLZ_CASE(2) LLZ_CASE(3) LLZ_CASE(4) LLZ_CASE(5)
           LLZ_CASE(6) LLZ_CASE(7) LLZ_CASE(8) LLZ_CASE(9) LLZ_CASE(10) LLZ_CASE(11)
-  #undef LLZ_CASE
-  #undef LLZ_GET
+#undef LLZ_CASE
+#undef LLZ_GET
           default:
             qa = to_v4(lds_q(k0 + 0));
             qb = to_v4(lds_q(k0 + 1));
             qc = to_v4(lds_q(k0 + 2));
             qd = to_v4(lds_q(k0 + 3));
         }
-        // per segment s: w1..w3 = the lane's integer sums before its elements
-        // 1..3, acc = the lane's sum, incl = the inclusive scan over lanes
-        uint32_t acc4[4], incl4[4], wa[4], wb[4], wc[4], spm = 0;
+        // per segment s: acc = the lane's integer sum (lower bracket), incl =
+        // its inclusive scan over lanes; bit s of sl: the lane is not certified
+        uint32_t acc4[4], incl4[4], sl = 0;
         bool pl4[4];
-  #pragma unroll
+#pragma unroll
         for (int s = 0; s < 4; ++s) {
           const int k = k0 + s;
           const int kl = min(k, kWave - 1);
           pl4[s] = k < nseg_w && readlane_u32(flag_l, kl) == (uint32_t)PLAIN;
           const float sc_lo = readlane_f32(gc_l.sc_lo, kl);
           const float sc_hi = readlane_f32(gc_l.sc_hi, kl);
-          const float tspec = readlane_f32(gc_l.tspec, kl);
+          const uint32_t tspec = __float_as_uint(readlane_f32(gc_l.tspec, kl));
           const llz_f4v qv4 = s == 0 ? qa : s == 1 ? qb : s == 2 ? qc : qd;  // s is a constant here
-          const float qs[4] = {qv4.x, qv4.y, qv4.z, qv4.w};
-          uint32_t b[4], sp = 0;
-  #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const float rlo = fmaf(qs[c], sc_lo, MAGIC);
-            const float rhi = fmaf(qs[c], sc_hi, MAGIC);
-            b[c] = __float_as_uint(rlo);
-            sp |= (rlo != rhi || rhi >= tspec) ? (1u << c) : 0u;
-          }
-          // absent positions hold q = 0, so rlo = rhi = MAGIC: never special
-          // (tspec > MAGIC for PLAIN segments outside flood mode, and theta is
-          // +inf in flood mode)
-          wa[s] = b[0] - MAGIC_BITS;
-          wb[s] = wa[s] + b[1] - MAGIC_BITS;
-          wc[s] = wb[s] + b[2] - MAGIC_BITS;
-          acc4[s] = wc[s] + b[3] - MAGIC_BITS;
-          if (!pl4[s]) sp = 0;
-          spm |= sp << (4 * s);
+          const uint32_t l0 = __float_as_uint(fmaf(qv4.x, sc_lo, MAGIC));
+          const uint32_t l1 = __float_as_uint(fmaf(qv4.y, sc_lo, MAGIC));
+          const uint32_t l2 = __float_as_uint(fmaf(qv4.z, sc_lo, MAGIC));
+          const uint32_t l3 = __float_as_uint(fmaf(qv4.w, sc_lo, MAGIC));
+          const uint32_t h0 = __float_as_uint(fmaf(qv4.x, sc_hi, MAGIC));
+          const uint32_t h1 = __float_as_uint(fmaf(qv4.y, sc_hi, MAGIC));
+          const uint32_t h2 = __float_as_uint(fmaf(qv4.z, sc_hi, MAGIC));
+          const uint32_t h3 = __float_as_uint(fmaf(qv4.w, sc_hi, MAGIC));
+          // bit patterns of non-negative floats order like their values: each
+          // upper bracket is >= its lower one, so the sums agree exactly when
+          // every pair does (no wrap below tspec <= MAGIC + 2^15)
+          const uint32_t lsum = (l0 + l1) + (l2 + l3);
+          const uint32_t hsum = (h0 + h1) + (h2 + h3);
+          const uint32_t hmax = max(max(h0, h1), max(h2, h3));
+          acc4[s] = lsum - 4u * MAGIC_BITS;
+          // absent positions hold q = 0, so their brackets are MAGIC: never
+          // special (tspec > MAGIC for PLAIN segments outside flood mode, and
+          // theta is +inf in flood mode)
+          sl |= (pl4[s] && (hsum != lsum || hmax >= tspec)) ? (1u << s) : 0u;
         }
-  #pragma unroll
+#pragma unroll
         for (int s = 0; s < 4; ++s)
           incl4[s] = wave_incl_scan_op(acc4[s], 0u, [](uint32_t a, uint32_t b) { return a + b; });
         if (lane == kWave - 1) {
-  #pragma unroll
+#pragma unroll
           for (int s = 0; s < 4; ++s)
             if (pl4[s]) F.ssum[w + W * (k0 + s)] = incl4[s];
         }
-        if (__ballot(spm != 0u) != 0ull) {
-          // every lane appends its own specials after those of the lanes below it
-          const uint32_t my = (uint32_t)__popc(spm);
+        if (__ballot(sl != 0u) != 0ull) {
+          // every lane appends its entries after those of the lanes below it
+          const uint32_t my = (uint32_t)__popc(sl);
           const uint32_t incl = wave_incl_scan_op(my, 0u, [](uint32_t a, uint32_t b) { return a + b; });
           const int total = (int)lane_readlast(incl);
           if (qn + total > QCAP) {
@@ -622,22 +664,16 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
             settle();
           }
           if (total > QCAP) {
-            qovf = true;  // more specials in four segments than the queue holds
+            qovf = true;  // more uncertified lanes in four segments than the queue holds
           } else {
             int slot = qn + (int)(incl - my);
-            uint32_t rem = spm;
-            while (rem != 0u) {
-              const int bt = __ffs(rem) - 1;
-              rem &= rem - 1u;
-              const int s = bt >> 2, c = bt & 3;
-              const uint32_t ex_s = s == 0 ? incl4[0] - acc4[0] : s == 1 ? incl4[1] - acc4[1]
-                                  : s == 2 ? incl4[2] - acc4[2] : incl4[3] - acc4[3];
-              const uint32_t wa_s = s == 0 ? wa[0] : s == 1 ? wa[1] : s == 2 ? wa[2] : wa[3];
-              const uint32_t wb_s = s == 0 ? wb[0] : s == 1 ? wb[1] : s == 2 ? wb[2] : wb[3];
-              const uint32_t wc_s = s == 0 ? wc[0] : s == 1 ? wc[1] : s == 2 ? wc[2] : wc[3];
-              F.qpos[w][slot] = (uint32_t)((w + W * (k0 + s)) * SEG + lane4 + c);
-              F.qpre[w][slot] = ex_s + (c == 0 ? 0u : c == 1 ? wa_s : c == 2 ? wb_s : wc_s);
-              ++slot;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              if (sl & (1u << s)) {
+                F.qpos[w][slot] = (uint32_t)((w + W * (k0 + s)) * SEG + lane4);
+                F.qpre[w][slot] = incl4[s] - acc4[s];
+                ++slot;
+              }
             }
             qn += total;
           }
