@@ -82,24 +82,24 @@ LLZ_HD float grid_ulp(int j) {
 LLZ_HD float grid_value(uint32_t N, int j) { return (float)N * grid_ulp(j); }
 
 // RN(x / 2^(j-23)) for a finite x >= 0 (sign bit ignored), saturated at
-// kSat, and whether x / 2^(j-23) is an exact half-integer (a tie).
+// kSat, and whether x / 2^(j-23) is an exact half-integer (a tie).  Without
+// branches: a shift of 25 or more is done as 25 (which leaves 0 with no
+// tie, since the significand is below 2^24), and the cases x >= 2^j
+// (shift <= 0) are selected at the end.
 LLZ_HD uint32_t grid_round(float x, int j, bool& tie) {
   const uint32_t b = as_bits(x) & 0x7fffffffu;
   const uint32_t XE = b >> 23;
   const uint32_t m = XE == 0 ? (b & 0x7fffffu) : ((b & 0x7fffffu) | 0x800000u);
   const int xe = (int)(XE == 0 ? 1u : XE) - 127;  // x = m * 2^(xe-23)
   const int d = j - xe;
-  tie = false;
-  if (d <= 0) {
-    if (d == 0) return m;
-    return m == 0 ? 0u : kSat;  // x >= 2^(j+1): leaves the binade on its own
-  }
-  if (d >= 25) return 0u;  // x < 2^(j-24) = u/2, strictly
-  const uint32_t q = m >> d;
-  const uint32_t rem = m & ((1u << d) - 1u);
-  const uint32_t half = 1u << (d - 1);
-  tie = rem == half;
-  return q + (rem > half ? 1u : 0u);
+  const int dd = d < 1 ? 1 : (d > 25 ? 25 : d);
+  const uint32_t q = m >> dd;
+  const uint32_t rem = m & ((1u << dd) - 1u);
+  const uint32_t half = 1u << (dd - 1);
+  const uint32_t r = q + (rem > half ? 1u : 0u);
+  tie = d > 0 && rem == half;
+  // d == 0: m itself; d < 0: x >= 2^(j+1) leaves the binade on its own
+  return d > 0 ? r : (d == 0 ? m : (m == 0 ? 0u : kSat));
 }
 
 // Largest integer T with T * 2^(j-23) <= thr, or 0xffffffff when thr is at

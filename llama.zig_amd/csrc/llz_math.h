@@ -18,30 +18,13 @@ namespace llz {
 __device__ __forceinline__ uint32_t fbits(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float bitsf(uint32_t u) { return __uint_as_float(u); }
 
-// RN(y * 2^k): two exact power-of-two steps, then one rounding multiply.
-__device__ __forceinline__ float scale_pow2(float y, int k) {
-  if (k > 127) {
-    y *= 0x1p127f;
-    k -= 127;
-    if (k > 127) {
-      y *= 0x1p127f;
-      k -= 127;
-      if (k > 127) k = 127;
-    }
-  } else if (k < -126) {
-    y *= 0x1p-102f;
-    k += 102;
-    if (k < -126) {
-      y *= 0x1p-102f;
-      k += 102;
-      if (k < -126) k = -126;
-    }
-  }
-  return y * bitsf((uint32_t)(0x7f + k) << 23);
-}
-
 // exp(x) for f32, e_expf.c algorithm: reduce x = k ln2 + r with a two-part
-// ln2, evaluate the degree-2 rational approximation of r, scale by 2^k.
+// ln2, evaluate the degree-2 rational approximation of r, scale by 2^k the
+// way scalbnf does (an exact power-of-two step, then one rounding multiply).
+// Written without branches: every lane evaluates the reduction with the k
+// its range selects (k = 0 leaves r = x, lo = 0 exactly, as the reference's
+// small-|x| branch), and the range cases are selected at the end.  Checked
+// against the reference's branchy form on all 2^32 inputs.
 __device__ __forceinline__ float exp_f32(float x) {
   const float ln2hi = 6.9314575195e-1f;   // 0x3f317200
   const float ln2lo = 1.4286067653e-6f;   // 0x35bfbe8e
@@ -49,35 +32,28 @@ __device__ __forceinline__ float exp_f32(float x) {
   const float P1 = 1.6666625440e-1f;      // 0x3e2aaa8f
   const float P2 = -2.7667332906e-3f;     // 0xbb355215
 
-  uint32_t hx = fbits(x);
-  const int sign = (int)(hx >> 31);
-  hx &= 0x7fffffffu;
-  if (hx >= 0x42aeac50u) {                // |x| >= 87.33655, inf or NaN
-    if (hx > 0x7f800000u) return x;        // NaN
-    if (hx >= 0x42b17218u && !sign) return x * 0x1p127f;  // overflow
-    if (sign && hx >= 0x42cff1b5u) return 0.0f;           // underflow to 0
-  }
-  float hi, lo;
-  int k;
-  if (hx > 0x3eb17218u) {                 // |x| > ln2/2
-    if (hx > 0x3f851592u)                  // |x| > 1.5 ln2
-      k = (int)(invln2 * x + (sign ? -0.5f : 0.5f));
-    else
-      k = 1 - sign - sign;
-    hi = x - (float)k * ln2hi;
-    lo = (float)k * ln2lo;
-    x = hi - lo;
-  } else if (hx > 0x39000000u) {          // |x| > 2^-13
-    k = 0;
-    hi = x;
-    lo = 0.0f;
-  } else {
-    return 1.0f + x;
-  }
-  const float xx = x * x;
-  const float c = x - xx * (P1 + xx * P2);
-  const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
-  return k == 0 ? y : scale_pow2(y, k);
+  const uint32_t hx0 = fbits(x);
+  const int sign = (int)(hx0 >> 31);
+  const uint32_t hx = hx0 & 0x7fffffffu;
+  // |x| > 1.5 ln2: k = (int)(x / ln2 +- 1/2); |x| in (ln2/2, 1.5 ln2]: +-1;
+  // below: 0 (the clamp only matters for inputs the specials below replace)
+  const float kt = fminf(fmaxf(invln2 * x + (sign ? -0.5f : 0.5f), -2.0e9f), 2.0e9f);
+  const int k = hx > 0x3f851592u ? (int)kt : (hx > 0x3eb17218u ? 1 - sign - sign : 0);
+  const float kf = (float)k;
+  const float hi = x - kf * ln2hi;
+  const float lo = kf * ln2lo;
+  const float r = hi - lo;
+  const float rr = r * r;
+  const float c = r - rr * (P1 + rr * P2);
+  const float y = 1.0f + (r * c / (2.0f - c) - lo + hi);
+  const float s1 = k > 127 ? 0x1p127f : (k < -126 ? 0x1p-102f : 1.0f);
+  const int k1 = min(max(k > 127 ? k - 127 : (k < -126 ? k + 102 : k), -126), 127);
+  float res = (y * s1) * bitsf((uint32_t)(0x7f + k1) << 23);
+  res = hx <= 0x39000000u ? 1.0f + x : res;                       // |x| <= 2^-13
+  res = (sign && hx >= 0x42cff1b5u) ? 0.0f : res;                 // underflow to 0
+  res = (!sign && hx >= 0x42b17218u) ? x * 0x1p127f : res;        // overflow
+  res = hx > 0x7f800000u ? x : res;                               // NaN
+  return res;
 }
 
 // log(x) for f32, e_logf.c algorithm: x = 2^k (1+f) with 1+f in

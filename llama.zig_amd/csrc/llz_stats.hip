@@ -90,13 +90,17 @@ __device__ __forceinline__ void push_cand(FastShared& F, const RowPtrs& Q, int r
   if (slot < (uint32_t)kCandCap) Q.cand[(int64_t)row * kCandCap + slot] = ((uint64_t)__float_as_uint(e) << 32) | id;
 }
 
-// EXACT slots are spread over the waves: wave w owns slots w, w + W, ...
+// EXACT slots are spread over the waves: slot 0 (the row's first segment,
+// the costliest: it starts at 0 and crosses many binades) to wave 0, the
+// others to waves 1 .. W-1 in turn.
+__device__ __forceinline__ int slot_wave(int slot) { return slot == 0 ? 0 : 1 + (slot - 1) % (W - 1); }
 
 // Issue the re-reads of this wave's EXACT slots into their dump areas (the
 // caller waits for them).
 template <bool FASTLD>
 __device__ __forceinline__ void exact_loads(FastShared& F, const float* xr, int w, int nslot, int n) {
-  for (int slot = w; slot < nslot; slot += W) seg_to_lds(xr, F.slotseg[slot], n, FASTLD, &F.u.x.dump[slot][0]);
+  for (int slot = w == 0 ? 0 : w; slot < nslot; slot += w == 0 ? DCAP : W - 1)
+    seg_to_lds(xr, F.slotseg[slot], n, FASTLD, &F.u.x.dump[slot][0]);
 }
 
 // Exact terms of this wave's EXACT slots (loaded and waited for), their
@@ -105,7 +109,7 @@ __device__ __forceinline__ void exact_loads(FastShared& F, const float* xr, int 
 __device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
                                                int nslot, int n, float m, float theta, bool t1) {
   const int lane = lane_id();
-  for (int slot = w; slot < nslot; slot += W) {
+  for (int slot = w == 0 ? 0 : w; slot < nslot; slot += w == 0 ? DCAP : W - 1) {
     const int seg = F.slotseg[slot];
     const bool pred = F.sflag[seg] == EXACT_PRED;
     float4* p = reinterpret_cast<float4*>(&F.u.x.dump[slot][lane * 4]);
@@ -477,7 +481,8 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     F.fail = fits ? 0u : 1u;
     F.flood = 0;
     F.ncand = 0;
-    F.nslot = 0;
+    F.nslot = 1;  // slot 0 is the row's first segment's
+    F.slotseg[0] = 0;
     F.next_g = 0;
     F.s_run = 0.0f;
     F.done = 0;
@@ -543,8 +548,10 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         F.sng[g] = (uint8_t)max(1, min(ehi - j0 + 1, NG));
         ex = !plain;
       }
-      // EXACT slots (any order; a row with more than DCAP takes further rounds in index order)
-      const uint64_t exm = __ballot(ex);
+      // EXACT slots: 0 for the row's first segment (always EXACT: it starts at
+      // 0), the others in any order from 1 (a row with more than DCAP takes
+      // further rounds in index order)
+      const uint64_t exm = __ballot(ex) & (w == 0 ? ~1ull : ~0ull);
       int base = 0;
       if (lane == 0) {
         if (exm != 0ull) base = (int)atomicAdd((uint32_t*)&F.nslot, (uint32_t)__popcll(exm));
@@ -553,7 +560,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       }
       base = __builtin_amdgcn_readfirstlane(base);
       if (have) {
-        const int slot = base + __popcll(exm & lt_mask);
+        const int slot = (w == 0 && lane == 0) ? 0 : base + __popcll(exm & lt_mask);
         const bool got = ex && slot < DCAP;
         F.sdump[w + W * lane] = (int8_t)(got ? slot : -1);
         if (got) F.slotseg[slot] = (int16_t)(w + W * lane);
@@ -592,7 +599,21 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         asm volatile("" : "+v"(l4));  // recomputed here rather than kept live through the loop
         return *reinterpret_cast<const float4*>(&F.u.data[w][min(max(k - KV, 0), KL - 1)][l4]);
       };
-      for (int k0 = 0; k0 < nseg_w; k0 += 4) {
+      // the batches holding LDS-resident segments first (k0 >= KV - 1), then
+      // one barrier: every wave is past its LDS segments, so the EXACT slots
+      // (which overlay them) can be re-read while the register batches run.
+      // The batch count and the barrier's position are uniform over waves.
+      static_assert((KV - 1) % 4 == 0, "batch KV - 1 is the first to hold LDS-resident segments");
+      const int spw_u = (G + W - 1) / W;
+      const int nbl = spw_u > KV - 1 ? (spw_u - (KV - 1) + 3) / 4 : 0;
+      const int nb = nbl + (KV - 1) / 4;
+      for (int bi = 0; bi < nb; ++bi) {
+        if (bi == nbl) {
+          __syncthreads();
+          exact_loads<FASTLD>(F, xr, w, min(F.nslot, DCAP), n);
+        }
+        const int k0 = bi < nbl ? (KV - 1) + 4 * bi : 4 * (bi - nbl);
+        if (k0 >= nseg_w) continue;
         llz_f4v qa, qb, qc, qd;  // native vectors: an array or HIP's float4 struct here ends up in scratch
         switch (k0 >> 2) {
 #define LLZ_GET(i) to_v4((i) < KV ? d[(i) < KV ? (i) : 0] : lds_q(i))
@@ -682,17 +703,14 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       if (qovf && lane == 0) atomicOr(&F.fail, 1u);
     }
 
-    // ---- phase F+X: the remaining specials and this round's EXACT slots in
-    // one round trip (the slots overlay the LDS-resident segments: every wave
-    // is past phase S)
-    __syncthreads();
+    // ---- phase F+X: this round's EXACT slots (re-read during phase S) and
+    // the remaining specials, whose re-reads land while the slots are
+    // evaluated
     if (!F.fail) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the EXACT slots' re-reads
       reread();
-      const int nslot = min(F.nslot, DCAP);
-      exact_loads<FASTLD>(F, xr, w, nslot, n);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      exact_segments(F, Q, P, row, w, min(F.nslot, DCAP), n, m, theta, t1);
       settle();
-      exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
     }
     __syncthreads();
 
@@ -732,7 +750,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           const int gb = g & ~(kWave - 1);
           const int gend = min(gb + kWave, G);
           const int gg = gb + lane;
-          uint32_t fl = PLAIN, sm = 0, sb = 0;
+          uint32_t fl = PLAIN, sm = 0, sb = 0, sn = 0;
           int jj = 0, sd = -1;
           if (gg < gend) {
             fl = F.sflag[gg];
@@ -740,6 +758,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
             sm = min(F.ssum[gg], kSat);
             sd = F.sdump[gg];
             sb = F.sbump[gg];
+            sn = F.sng[gg];
           }
           // inclusive prefix of the group's sums (each <= 2^25: no wrap)
           const uint32_t pincl = wave_incl_scan_op(sm, 0u, [](uint32_t a, uint32_t b) { return a + b; });
@@ -785,7 +804,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
               more = true;
               break;
             }
-            resolve_exact(s, slot, (int)readlane_u32((uint32_t)jj, fb), F.sng[g], F);
+            resolve_exact(s, slot, (int)readlane_u32((uint32_t)jj, fb), (int)readlane_u32(sn, fb), F);
             ++g;
           }
         }
