@@ -81,6 +81,12 @@ LLZ_HD float grid_ulp(int j) {
 // N * 2^(j-23) as a float; exact for N < 2^24 (or a subnormal on the grid).
 LLZ_HD float grid_value(uint32_t N, int j) { return (float)N * grid_ulp(j); }
 
+// The bits of N * 2^(j-23) for N < 2^24 on grid j: a normal number when
+// N >= 2^23, a subnormal (j = -126) below.  Integer operations only.
+LLZ_HD uint32_t grid_bits(uint32_t N, int j) {
+  return N >= 0x800000u ? (((uint32_t)(j + 127) << 23) + (N - 0x800000u)) : N;
+}
+
 // RN(x / 2^(j-23)) for a finite x >= 0 (sign bit ignored), saturated at
 // kSat, and whether x / 2^(j-23) is an exact half-integer (a tie).  Without
 // branches: a shift of 25 or more is done as 25 (which leaves 0 with no

@@ -79,10 +79,16 @@ static_assert(GMAX <= 8 * 64, "the combine holds eight segments per lane");
 
 // EXACT segments: exact terms, per-lane inclusive prefixes of their
 // roundings on grids sj .. sj + sng - 1, and the lanes holding a tie.
+// and the walk's entries in index order: a run of PLAIN segments on one
+// binade, a PLAIN_TIE segment, or an EXACT segment.  Word a: type (bits
+// 0-1), segment (2-11), binade + 128 (16-23), tie units (24-31); word b: the
+// integer sum of a run or a PLAIN_TIE segment.
 struct ExactSlots {
   float dump[fastp::DCAP][fastp::SEG];
   uint32_t pref[fastp::DCAP][fastp::NG][kWave];
   uint64_t tmask[fastp::DCAP][fastp::NG];
+  uint32_t ent_a[fastp::GMAX];
+  uint32_t ent_b[fastp::GMAX];
 };
 
 struct FastShared {
@@ -113,7 +119,8 @@ struct FastShared {
   int nslot;      // EXACT slots in use this round
   uint32_t fail;
   uint32_t flood;
-  int next_g;     // combine: first segment not consumed yet
+  int next_e;     // combine: first entry not consumed yet
+  int ne;         // combine: number of entries
   float s_run;    // combine: running sum at next_g
   int done;
 };

@@ -483,7 +483,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     F.ncand = 0;
     F.nslot = 1;  // slot 0 is the row's first segment's
     F.slotseg[0] = 0;
-    F.next_g = 0;
+    F.next_e = 0;
     F.s_run = 0.0f;
     F.done = 0;
   }
@@ -710,16 +710,70 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the EXACT slots' re-reads
       reread();
       exact_segments(F, Q, P, row, w, min(F.nslot, DCAP), n, m, theta, t1);
+      if (w == 0 && F.sdump[0] == 0) {
+        // the row's first segment starts at 0: its sum needs nothing else,
+        // so the walk's first entry is resolved here, off its serial path
+        float s0 = 0.0f;
+        resolve_exact(s0, 0, F.sj[0], F.sng[0], F);
+        if (lane == 0) {
+          F.s_run = s0;
+          F.next_e = 1;
+        }
+      }
       settle();
     }
     __syncthreads();
 
-    // ---- phase C: the walk in index order; EXACT segments beyond the slots
-    // in further rounds
+    // ---- phase B: the walk's entries, built in parallel (wave c takes
+    // segments 64c .. 64c + 63, one per lane): a run of PLAIN segments on one
+    // binade becomes one entry with its integer sum; PLAIN_TIE and EXACT
+    // segments are one entry each
+    constexpr uint32_t E_RUN = 0, E_TIE = 1, E_EXACT = 2;
+    if (!F.fail) {
+      const int g = kWave * w + lane;
+      const bool in = g < G;
+      const uint32_t fl = in ? F.sflag[g] : (uint32_t)EXACT_PRED;
+      const int jj = in ? F.sj[g] : 0;
+      const uint32_t sm = in ? min(F.ssum[g], kSat) : 0u;
+      const bool plain = in && fl == PLAIN;
+      const uint32_t key = plain ? (0x10000u | (uint32_t)(jj & 0xffff)) : 0u;
+      const bool head = in && !(plain && wave_shift_up1(key) == key);
+      const uint64_t heads = __ballot(head);
+      // a run's sum up to this lane: the inclusive prefix minus the exclusive
+      // prefix at the run's head (prefixes never decrease, so a max-scan of the
+      // heads' exclusive prefixes yields the latest head's); <= 64 * 2^25: no wrap
+      const uint32_t v = plain ? sm : 0u;
+      const uint32_t pin = wave_incl_scan_op(v, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+      const uint32_t hb = wave_incl_scan_op(head ? pin - v : 0u, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+      const bool tail = plain && (lane == kWave - 1 || g + 1 >= G || ((heads >> (lane + 1)) & 1ull) != 0ull);
+      if (lane == 0) F.wnex[w] = __popcll(heads);
+      __syncthreads();
+      int off = 0, ne = 0;
+      for (int i = 0; i < W; ++i) {
+        if (i < w) off += F.wnex[i];
+        ne += F.wnex[i];
+      }
+      if (head) {
+        const uint32_t type = plain ? E_RUN : (fl == PLAIN_TIE ? E_TIE : E_EXACT);
+        const uint32_t tb = fl == PLAIN_TIE ? (uint32_t)F.sbump[g] : 0u;
+        F.u.x.ent_a[off + __popcll(heads & lt_mask)] =
+            type | ((uint32_t)g << 2) | ((uint32_t)(jj + 128) << 16) | (tb << 24);
+        // PLAIN_TIE: its integer sum; EXACT: its round-0 slot and grid count
+    if (!plain)
+      F.u.x.ent_b[off + __popcll(heads & lt_mask)] =
+          fl == PLAIN_TIE ? sm : (uint32_t)(uint8_t)F.sdump[g] | ((uint32_t)F.sng[g] << 8);
+      }
+      if (tail) F.u.x.ent_b[off + __popcll(heads & (lt_mask | (1ull << lane))) - 1] = pin - hb;
+      if (t == 0) F.ne = ne;
+    }
+    __syncthreads();
+
+    // ---- phase C: the walk over the entries in index order (wave 0); EXACT
+    // segments beyond the slots in further rounds
     for (int round = 0; !F.fail; ++round) {
-      const int g_from = F.next_g;
       if (round > 0) {
-        if (w == 0) {  // slots for the EXACT segments from g_from on, in order
+        if (w == 0) {  // slots for the EXACT segments from the stopping entry's on, in order
+          const int g_from = (int)((F.u.x.ent_a[F.next_e] >> 2) & 1023u);
           int cnt = 0;
           for (int b = g_from; b < G; b += kWave) {
             const int g = b + lane;
@@ -743,74 +797,48 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       }
       if (w == 0) {
         float s = uni_f(F.s_run);
-        int g = g_from;
+        int e = F.next_e;
+        const int ne = F.ne;
         bool fail = false, more = false;
-        while (g < G && !fail && !more) {
-          // this group of 64 segments, one per lane
-          const int gb = g & ~(kWave - 1);
-          const int gend = min(gb + kWave, G);
-          const int gg = gb + lane;
-          uint32_t fl = PLAIN, sm = 0, sb = 0, sn = 0;
-          int jj = 0, sd = -1;
-          if (gg < gend) {
-            fl = F.sflag[gg];
-            jj = F.sj[gg];
-            sm = min(F.ssum[gg], kSat);
-            sd = F.sdump[gg];
-            sb = F.sbump[gg];
-            sn = F.sng[gg];
+        uint32_t ea = 0, eb = 0;
+        int held = -1;  // first entry held in ea / eb (one per lane)
+        while (e < ne) {
+          if ((e & ~(kWave - 1)) != held) {
+            held = e & ~(kWave - 1);
+            const bool ok = held + lane < ne;
+            ea = ok ? F.u.x.ent_a[held + lane] : 0u;
+            eb = ok ? F.u.x.ent_b[held + lane] : 0u;
           }
-          // inclusive prefix of the group's sums (each <= 2^25: no wrap)
-          const uint32_t pincl = wave_incl_scan_op(sm, 0u, [](uint32_t a, uint32_t b) { return a + b; });
-          const uint64_t tie_lanes = __ballot(fl == PLAIN_TIE);
-          while (g < gend) {
+          const uint32_t a = readlane_u32(ea, e - held), b = readlane_u32(eb, e - held);
+          const int j = (int)((a >> 16) & 0xffu) - 128;
+          if ((a & 3u) != E_EXACT) {
+            // a run (or a PLAIN_TIE segment) on grid j: terms are >= 0, so it
+            // stays in the binade exactly when its total does; a PLAIN_TIE
+            // segment adds the units its ties take for the parity of the
+            // integer it starts at
             const Grid gr = grid_of(s);
-            const int p = g - gb;
-            const bool okp = (fl == PLAIN || fl == PLAIN_TIE) && jj == gr.j;
-            const uint64_t bad = __ballot(lane >= p && gg < gend && !okp);
-            const int fb = bad ? __ffsll((long long)bad) - 1 : gend - gb;
-            if (fb > p) {
-              // run [p, fb) on grid gr.j: terms are >= 0, so it stays in the binade
-              // exactly when its total does.  A PLAIN_TIE segment adds the units its
-              // ties take for the parity of the integer it starts at.
-              const uint32_t before = p > 0 ? readlane_u32(pincl, p - 1) : 0u;
-              uint32_t bump = 0;
-              uint64_t tl = tie_lanes & (~0ull << p) & (fb >= kWave ? ~0ull : ((1ull << fb) - 1ull));
-              while (tl != 0ull) {
-                const int L = __ffsll((long long)tl) - 1;
-                tl &= tl - 1ull;
-                const uint32_t at = gr.N + ((L > 0 ? readlane_u32(pincl, L - 1) : 0u) - before) + bump;
-                const uint32_t bb = readlane_u32(sb, L);
-                bump += (at & 1u) ? (bb >> 4) : (bb & 15u);
-              }
-              const uint32_t tot = readlane_u32(pincl, fb - 1) - before + bump;
-              if (gr.N + tot >= kGridTop) {
-                fail = true;  // a crossing the prediction did not see
-                break;
-              }
-              s = uni_f(grid_value(gr.N + tot, gr.j));
-              g = gb + fb;
-            }
-            if (g >= gend) break;
-            // segment g is an event: an EXACT segment, or a PLAIN one whose binade
-            // the running sum is not in
-            const uint32_t flg = readlane_u32(fl, fb);
-            if (flg == PLAIN || flg == PLAIN_TIE) {
-              fail = true;  // the running sum is not in the predicted binade
+            const uint32_t tu = a >> 24;
+            const uint32_t bump = (a & 3u) == E_TIE ? ((gr.N & 1u) ? (tu >> 4) : (tu & 15u)) : 0u;
+            const uint32_t N2 = gr.N + b + bump;
+            if (gr.j != j || N2 >= kGridTop) {
+              fail = true;  // the running sum is not in the predicted binade, or leaves it
               break;
             }
-            const int slot = (int)readlane_u32((uint32_t)sd, fb);
-            if (slot < 0 || g < g_from) {
+            s = __uint_as_float(grid_bits(N2, j));
+          } else {
+            int slot = (int)(int8_t)(b & 0xffu);
+            if (round > 0) slot = F.sdump[(a >> 2) & 1023u];  // slots were reassigned
+            if (slot < 0) {
               more = true;
               break;
             }
-            resolve_exact(s, slot, (int)readlane_u32((uint32_t)jj, fb), (int)readlane_u32(sn, fb), F);
-            ++g;
+            resolve_exact(s, slot, j, (int)((b >> 8) & 0xffu), F);
           }
+          ++e;
         }
         if (lane == 0) {
           F.s_run = s;
-          F.next_g = g;
+          F.next_e = e;
           if (fail) F.fail = 1u;
           F.done = (!fail && !more) ? 1 : 0;
         }
