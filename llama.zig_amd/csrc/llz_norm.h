@@ -97,23 +97,41 @@ __device__ float wave_accumulate(float s, const float (&x)[V]) {
 // Sequential accumulation over a short list by one wave (the reference's
 // loop, one term at a time).  ADD stops at the first s > thr (thr >= 0),
 // SUB at the first s <= 0; absent terms (sign bit set) are skipped.
+//
+// Lane i of a 64-term chunk runs the chain up to term i: at step k every
+// lane from k on adds term k (the others add -0, which leaves any value
+// unchanged), so after the chunk lane i holds the running value after term
+// i.  The steps use constant lane indices and no branches (a wave running
+// alone pays for every dependent step); one ballot then finds the first stop.
+// s - x is computed as s + (-x), which IEEE defines to be the same.
 template <bool SUB, typename TermFn>
 __device__ float wave_seq_list(float s, int len, float thr, int& stop, TermFn term) {
   stop = -1;
   const int lane = lane_id();
   for (int base = 0; base < len; base += kWave) {
     const int p = base + lane;
-    const float x = p < len ? term(p) : -0.0f;
+    const float x0 = p < len ? term(p) : -0.0f;
+    const bool present = p < len && !(as_bits(x0) >> 31);
+    const float x = present ? (SUB ? -x0 : x0) : -0.0f;
     const int cnt = min(kWave, len - base);
-    for (int i = 0; i < cnt; ++i) {
-      const float xi = readlane_f32(x, i);
-      if (as_bits(xi) >> 31) continue;
-      s = SUB ? s - xi : s + xi;
-      if (SUB ? (s <= 0.0f) : (thr >= 0.0f && s > thr)) {
-        stop = base + i;
-        return s;
+    float acc = s;
+#pragma unroll
+    for (int k8 = 0; k8 < kWave; k8 += 8) {
+      if (k8 >= cnt) break;
+#pragma unroll
+      for (int k = k8; k < k8 + 8; ++k) {
+        const float xk = readlane_f32(x, k);
+        acc = acc + (lane >= k ? xk : -0.0f);
       }
     }
+    const bool hit = present && (SUB ? (acc <= 0.0f) : (thr >= 0.0f && acc > thr));
+    const uint64_t hits = __ballot(hit);
+    if (hits != 0ull) {
+      const int L = __ffsll((long long)hits) - 1;
+      stop = base + L;
+      return readlane_f32(acc, L);
+    }
+    s = readlane_f32(acc, kWave - 1);
   }
   return s;
 }

@@ -218,6 +218,131 @@ __device__ __forceinline__ void resolve_exact(float& s_io, int slot, int J0, int
   s_io = s;
 }
 
+// An EXACT slot's data as the walk needs it, read ahead of its entry (it does
+// not depend on the running sum): the lane's four exact terms and the prefix
+// tables and tie masks of the slot's first two grids.  The empty asm keeps
+// the values in registers: a select between two fields of a struct can
+// otherwise become a select between their addresses, with the struct on the
+// stack.
+struct SlotAhead {
+  float4 e4;
+  uint32_t pv0, pv1;
+  uint32_t tm0l, tm0h, tm1l, tm1h;
+};
+
+__device__ __forceinline__ SlotAhead slot_ahead(const FastShared& F, int slot) {
+  const int lane = lane_id();
+  SlotAhead X;
+  X.e4 = *reinterpret_cast<const float4*>(&F.u.x.dump[slot][lane * 4]);
+  X.pv0 = F.u.x.pref[slot][0][lane];
+  X.pv1 = F.u.x.pref[slot][1][lane];
+  const uint64_t t0 = F.u.x.tmask[slot][0], t1 = F.u.x.tmask[slot][1];
+  X.tm0l = (uint32_t)t0;
+  X.tm0h = (uint32_t)(t0 >> 32);
+  X.tm1l = (uint32_t)t1;
+  X.tm1h = (uint32_t)(t1 >> 32);
+  asm volatile("" : "+v"(X.e4.x), "+v"(X.e4.y), "+v"(X.e4.z), "+v"(X.e4.w), "+v"(X.pv0), "+v"(X.pv1));
+  asm volatile("" : "+v"(X.tm0l), "+v"(X.tm0h), "+v"(X.tm1l), "+v"(X.tm1h));
+  return X;
+}
+
+// resolve_exact on the walk's integer state: the running sum is N on grid j
+// (N * 2^(j-23), N < 2^24), kept in scalar registers; the slot's data was
+// read ahead into X.
+__device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slot, int J0, int ng,
+                                              const SlotAhead& X, const FastShared& F) {
+  const int lane = lane_id();
+  uint32_t N = N_io;
+  int j = j_io;
+  int p = 0;  // first lane not consumed
+  if (j == J0) {
+    // the common case, short on dependent steps (a wave running alone waits
+    // out each one): every lane replays its own four terms from the table's
+    // prefix before it, as if it held the first event, while the event lane
+    // is found; then at most one crossing into grid J0 + 1, where the rest of
+    // the segment is one table difference
+    const uint32_t before = N + wave_shift_up1(X.pv0);  // lane 0: N
+    float t = __uint_as_float(grid_bits(before, j));
+    t = t + X.e4.x;
+    t = t + X.e4.y;
+    t = t + X.e4.z;
+    t = t + X.e4.w;
+    const uint64_t tm0 = ((uint64_t)uni_u(X.tm0h) << 32) | uni_u(X.tm0l);
+    const uint64_t ev = __ballot(X.pv0 >= kSat || N + X.pv0 >= kGridTop) | tm0;
+    if (ev == 0ull) {
+      N_io = uni_u(N + readlane_u32(X.pv0, kWave - 1));
+      return;
+    }
+    const int E = __ffsll((long long)ev) - 1;
+    const Grid g = grid_of(uni_f(readlane_f32(t, E)));
+    N = g.N;
+    j = g.j;
+    p = E + 1;
+    if (p == kWave) {
+      N_io = N;
+      j_io = j;
+      return;
+    }
+    if (j == J0 + 1 && ng >= 2) {
+      const uint32_t B = readlane_u32(X.pv1, E), T = readlane_u32(X.pv1, kWave - 1);
+      const uint64_t tm1 = ((uint64_t)uni_u(X.tm1h) << 32) | uni_u(X.tm1l);
+      // table entries are saturating prefix sums: T - B is exact below kSat
+      if (T < kSat && N + (T - B) < kGridTop && (tm1 & (~0ull << p)) == 0ull) {
+        N_io = uni_u(N + (T - B));
+        j_io = j;
+        return;
+      }
+    }
+  }
+  // selects rather than branches: a taken branch costs a wave running alone
+  // far more than the few operations it would skip
+  for (int guard = 0; guard <= kWave && p < kWave; ++guard) {
+    const int k = j - J0;
+    uint32_t pv;
+    uint64_t tm;
+    if ((uint32_t)k < 2u && k < ng) {
+      const uint32_t pv0 = X.pv0, pv1 = X.pv1;
+      pv = k == 0 ? pv0 : pv1;
+      asm volatile("" : "+v"(pv));
+      tm = ((uint64_t)uni_u(k == 0 ? X.tm0h : X.tm1h) << 32) | uni_u(k == 0 ? X.tm0l : X.tm1l);
+    } else if (k >= 2 && k < ng) {
+      pv = F.u.x.pref[slot][k][lane];
+      asm volatile("" : "+v"(pv));
+      tm = uni_u64(F.u.x.tmask[slot][k]);
+    } else {
+      const float s = uni_f(resolve_generic(__uint_as_float(grid_bits(N, j)), X.e4.x, X.e4.y, X.e4.z, X.e4.w, p));
+      const Grid g = grid_of(s);
+      N = g.N;
+      j = g.j;
+      break;
+    }
+    const uint32_t base_l = readlane_u32(pv, (p - 1) & (kWave - 1));
+    const uint32_t base = p > 0 ? base_l : 0u;
+    const uint64_t live = ~0ull << p;
+    const bool cr = lane >= p && (pv >= kSat || N + (pv - base) >= kGridTop);
+    const uint64_t ev = (__ballot(cr) | tm) & live;
+    if (ev == 0ull) {
+      N = uni_u(N + (readlane_u32(pv, kWave - 1) - base));
+      break;
+    }
+    const int E = __ffsll((long long)ev) - 1;
+    const uint32_t NE_l = uni_u(N + (readlane_u32(pv, (E - 1) & (kWave - 1)) - base));
+    const uint32_t NE = E > p ? NE_l : N;
+    // the lane holding the event, term by term (sampler.zig:87)
+    float t = __uint_as_float(grid_bits(NE, j));
+    t = t + readlane_f32(X.e4.x, E);
+    t = t + readlane_f32(X.e4.y, E);
+    t = t + readlane_f32(X.e4.z, E);
+    t = t + readlane_f32(X.e4.w, E);
+    const Grid g = grid_of(uni_f(t));
+    N = g.N;
+    j = g.j;
+    p = E + 1;
+  }
+  N_io = N;
+  j_io = j;
+}
+
 // Owner wave: settle its queued lanes (v4q[h]: the re-read logits of entry
 // h * 64 + lane, four consecutive positions from the entry's position).
 // Each term's lower-bracket rounding is recomputed exactly as phase S summed
@@ -796,48 +921,75 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         __syncthreads();
       }
       if (w == 0) {
-        float s = uni_f(F.s_run);
+        // the running sum as N on grid jc, in scalar registers
+        const Grid g0 = grid_of(uni_f(F.s_run));
+        uint32_t N = g0.N;
+        int jc = g0.j;
         int e = F.next_e;
         const int ne = F.ne;
         bool fail = false, more = false;
-        uint32_t ea = 0, eb = 0;
-        int held = -1;  // first entry held in ea / eb (one per lane)
-        while (e < ne) {
-          if ((e & ~(kWave - 1)) != held) {
-            held = e & ~(kWave - 1);
-            const bool ok = held + lane < ne;
-            ea = ok ? F.u.x.ent_a[held + lane] : 0u;
-            eb = ok ? F.u.x.ent_b[held + lane] : 0u;
-          }
-          const uint32_t a = readlane_u32(ea, e - held), b = readlane_u32(eb, e - held);
-          const int j = (int)((a >> 16) & 0xffu) - 128;
-          if ((a & 3u) != E_EXACT) {
-            // a run (or a PLAIN_TIE segment) on grid j: terms are >= 0, so it
-            // stays in the binade exactly when its total does; a PLAIN_TIE
-            // segment adds the units its ties take for the parity of the
-            // integer it starts at
-            const Grid gr = grid_of(s);
-            const uint32_t tu = a >> 24;
-            const uint32_t bump = (a & 3u) == E_TIE ? ((gr.N & 1u) ? (tu >> 4) : (tu & 15u)) : 0u;
-            const uint32_t N2 = gr.N + b + bump;
-            if (gr.j != j || N2 >= kGridTop) {
-              fail = true;  // the running sum is not in the predicted binade, or leaves it
+        // windows of 64 entries, one per lane; in each, the runs before an
+        // EXACT entry are added together while its slot data is read ahead
+        for (int held = e & ~(kWave - 1); held < ne && !fail && !more; held += kWave) {
+          const bool ok = held + lane < ne;
+          const uint32_t ea = ok ? F.u.x.ent_a[held + lane] : 0u;
+          const uint32_t eb = ok ? F.u.x.ent_b[held + lane] : 0u;
+          const int ej = (int)((ea >> 16) & 0xffu) - 128;
+          const uint64_t exm = __ballot(ok && (ea & 3u) == E_EXACT);
+          const uint64_t tim = __ballot(ok && (ea & 3u) == E_TIE);
+          const int wend = min(ne - held, kWave);
+          int i = e - held;
+          while (i < wend) {
+            const uint64_t rest = exm & (~0ull << i);
+            const int x = rest != 0ull ? __ffsll((long long)rest) - 1 : wend;
+            int xslot = -1;
+            SlotAhead X = {};
+            if (x < wend) {
+              const uint32_t xa = readlane_u32(ea, x), xb = readlane_u32(eb, x);
+              xslot = (int)(int8_t)(xb & 0xffu);
+              if (round > 0) xslot = F.sdump[(xa >> 2) & 1023u];  // slots were reassigned
+              xslot = __builtin_amdgcn_readfirstlane(xslot);
+              if (xslot >= 0) X = slot_ahead(F, xslot);
+            }
+            // runs (and PLAIN_TIE segments) i .. x-1 on grid jc: terms are >=
+            // 0, so they stay in the binade exactly when their total does
+            if (x > i) {
+              const uint64_t span = (x >= kWave ? ~0ull : ((1ull << x) - 1ull)) & (~0ull << i);
+              bool bad;
+              if ((tim & span) == 0ull) {
+                const bool in = ((span >> lane) & 1ull) != 0ull;
+                N += wave_sum_u32(in ? eb : 0u);  // <= 64 * 2^25: no wrap
+                bad = __ballot(in && ej != jc) != 0ull;
+              } else {
+                // a PLAIN_TIE segment adds the units its ties take for the
+                // parity of the integer it starts at: one entry at a time
+                bad = false;
+                for (int r = i; r < x; ++r) {
+                  const uint32_t a = readlane_u32(ea, r), b = readlane_u32(eb, r);
+                  const uint32_t tu = a >> 24;
+                  const uint32_t bump = (a & 3u) == E_TIE ? ((N & 1u) ? (tu >> 4) : (tu & 15u)) : 0u;
+                  bad = bad || (int)((a >> 16) & 0xffu) - 128 != jc || N >= kGridTop;
+                  N += b + bump;
+                }
+              }
+              if (bad || N >= kGridTop) {
+                fail = true;  // the running sum is not in the predicted binade, or leaves it
+                break;
+              }
+            }
+            i = x;
+            if (i >= wend) break;
+            if (xslot < 0) {
+              more = true;  // EXACT segments past this round's slots
               break;
             }
-            s = __uint_as_float(grid_bits(N2, j));
-          } else {
-            int slot = (int)(int8_t)(b & 0xffu);
-            if (round > 0) slot = F.sdump[(a >> 2) & 1023u];  // slots were reassigned
-            if (slot < 0) {
-              more = true;
-              break;
-            }
-            resolve_exact(s, slot, j, (int)((b >> 8) & 0xffu), F);
+            resolve_ahead(N, jc, xslot, (int)readlane_u32((uint32_t)ej, i), (int)((readlane_u32(eb, i) >> 8) & 0xffu), X, F);
+            ++i;
           }
-          ++e;
+          e = held + i;
         }
         if (lane == 0) {
-          F.s_run = s;
+          F.s_run = __uint_as_float(grid_bits(N, jc));
           F.next_e = e;
           if (fail) F.fail = 1u;
           F.done = (!fail && !more) ? 1 : 0;
