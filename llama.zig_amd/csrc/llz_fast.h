@@ -99,7 +99,8 @@ struct FastShared {
   union {
     float aseg[fastp::GMAX];                    // segment sums of q (phases L, M)
   } v;
-  uint32_t ssum[fastp::GMAX];                   // PLAIN: integer sum on grid sj
+  uint32_t ssum[fastp::W * 64];                 // PLAIN: integer sum on grid sj (room for every
+                                                //   wave's 64th segment: phase S stores it unguarded)
   int8_t sj[fastp::GMAX];                       // PLAIN: its binade; EXACT: first binade tabulated
   uint8_t sng[fastp::GMAX];                     // EXACT: number of binades tabulated
   uint8_t sflag[fastp::GMAX];

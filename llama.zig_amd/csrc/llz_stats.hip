@@ -716,61 +716,31 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     };
     bool qovf = false;
     if (!F.fail) {
-      const uint32_t flag_l = have ? (uint32_t)F.sflag[w + W * lane] : (uint32_t)EXACT_PRED;
-      const int j_l = have ? (int)F.sj[w + W * lane] : 0;
-      const GridConst gc_l = grid_const(j_l, Rw, theta);
+      // per-segment constants, lane k for this wave's segment k; segments
+      // that are not PLAIN (or absent) get zero scales and an unreachable
+      // tspec, so every bracket is MAGIC and no lane is special
+      const bool plain_l = have && F.sflag[w + W * lane] == (uint8_t)PLAIN;
+      const GridConst gc_l = grid_const(have ? (int)F.sj[w + W * lane] : 0, Rw, theta);
+      const float sclo_l = plain_l ? gc_l.sc_lo : 0.0f;
+      const float schi_l = plain_l ? gc_l.sc_hi : 0.0f;
+      const uint32_t tspec_l = plain_l ? __float_as_uint(gc_l.tspec) : 0xffffffffu;
       auto lds_q = [&](int k) {
-        int l4 = lane_id() * 4;
-        asm volatile("" : "+v"(l4));  // recomputed here rather than kept live through the loop
-        return *reinterpret_cast<const float4*>(&F.u.data[w][min(max(k - KV, 0), KL - 1)][l4]);
+        return to_v4(reinterpret_cast<const float4*>(&F.u.data[w][min(max(k - KV, 0), KL - 1)][0])[lane]);
       };
-      // the batches holding LDS-resident segments first (k0 >= KV - 1), then
-      // one barrier: every wave is past its LDS segments, so the EXACT slots
-      // (which overlay them) can be re-read while the register batches run.
-      // The batch count and the barrier's position are uniform over waves.
-      static_assert((KV - 1) % 4 == 0, "batch KV - 1 is the first to hold LDS-resident segments");
-      const int spw_u = (G + W - 1) / W;
-      const int nbl = spw_u > KV - 1 ? (spw_u - (KV - 1) + 3) / 4 : 0;
-      const int nb = nbl + (KV - 1) / 4;
-      for (int bi = 0; bi < nb; ++bi) {
-        if (bi == nbl) {
-          __syncthreads();
-          exact_loads<FASTLD>(F, xr, w, min(F.nslot, DCAP), n);
-        }
-        const int k0 = bi < nbl ? (KV - 1) + 4 * bi : 4 * (bi - nbl);
-        if (k0 >= nseg_w) continue;
-        llz_f4v qa, qb, qc, qd;  // native vectors: an array or HIP's float4 struct here ends up in scratch
-        switch (k0 >> 2) {
-#define LLZ_GET(i) to_v4((i) < KV ? d[(i) < KV ? (i) : 0] : lds_q(i))
-#define LLZ_CASE(b)                 \
-      case b:                           \
-        qa = LLZ_GET(4 * (b) + 0);      \
-        qb = LLZ_GET(4 * (b) + 1);      \
-        qc = LLZ_GET(4 * (b) + 2);      \
-        qd = LLZ_GET(4 * (b) + 3);      \
-        break;
-          LLZ_CASE(0) LLZ_CASE(1) LLZ_CASE(2) LLZ_CASE(3) LLZ_CASE(4) LLZ_CASE(5)
-          LLZ_CASE(6) LLZ_CASE(7) LLZ_CASE(8) LLZ_CASE(9) LLZ_CASE(10) LLZ_CASE(11)
-#undef LLZ_CASE
-#undef LLZ_GET
-          default:
-            qa = to_v4(lds_q(k0 + 0));
-            qb = to_v4(lds_q(k0 + 1));
-            qc = to_v4(lds_q(k0 + 2));
-            qd = to_v4(lds_q(k0 + 3));
-        }
-        // per segment s: acc = the lane's integer sum (lower bracket), incl =
-        // its inclusive scan over lanes; bit s of sl: the lane is not certified
-        uint32_t acc4[4], incl4[4], sl = 0;
-        bool pl4[4];
+      // One batch: four segments k0 .. k0 + 3 (k0 a constant).  Per lane and
+      // segment, the lower and upper bracket roundings of its four terms
+      // (bit patterns of MAGIC + rounding); the lane is special when the
+      // sums differ or a term reaches tspec.  Sums are scanned with the
+      // MAGIC offsets in (wrapping; the true values are far below 2^32) and
+      // the offsets taken out where a sum is used.
+      auto batch = [&](const int k0, const llz_f4v qa, const llz_f4v qb, const llz_f4v qc, const llz_f4v qd) {
+        uint32_t raw4[4], incl4[4], sl = 0;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const int k = k0 + s;
-          const int kl = min(k, kWave - 1);
-          pl4[s] = k < nseg_w && readlane_u32(flag_l, kl) == (uint32_t)PLAIN;
-          const float sc_lo = readlane_f32(gc_l.sc_lo, kl);
-          const float sc_hi = readlane_f32(gc_l.sc_hi, kl);
-          const uint32_t tspec = __float_as_uint(readlane_f32(gc_l.tspec, kl));
+          const int kl = min(k0 + s, kWave - 1);
+          const float sc_lo = readlane_f32(sclo_l, kl);
+          const float sc_hi = readlane_f32(schi_l, kl);
+          const uint32_t tspec = readlane_u32(tspec_l, kl);
           const llz_f4v qv4 = s == 0 ? qa : s == 1 ? qb : s == 2 ? qc : qd;  // s is a constant here
           const uint32_t l0 = __float_as_uint(fmaf(qv4.x, sc_lo, MAGIC));
           const uint32_t l1 = __float_as_uint(fmaf(qv4.y, sc_lo, MAGIC));
@@ -786,19 +756,20 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           const uint32_t lsum = (l0 + l1) + (l2 + l3);
           const uint32_t hsum = (h0 + h1) + (h2 + h3);
           const uint32_t hmax = max(max(h0, h1), max(h2, h3));
-          acc4[s] = lsum - 4u * MAGIC_BITS;
+          raw4[s] = lsum;
           // absent positions hold q = 0, so their brackets are MAGIC: never
           // special (tspec > MAGIC for PLAIN segments outside flood mode, and
           // theta is +inf in flood mode)
-          sl |= (pl4[s] && (hsum != lsum || hmax >= tspec)) ? (1u << s) : 0u;
+          sl |= (hsum != lsum || hmax >= tspec) ? (1u << s) : 0u;
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          incl4[s] = wave_incl_scan_op(acc4[s], 0u, [](uint32_t a, uint32_t b) { return a + b; });
+          incl4[s] = wave_incl_scan_op(raw4[s], 0u, [](uint32_t a, uint32_t b) { return a + b; });
+        // segment totals (lane 63 holds them; the MAGIC offsets of 256 terms
+        // taken out).  Every wave has room for 64 segments: absent ones store 0
         if (lane == kWave - 1) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
-            if (pl4[s]) F.ssum[w + W * (k0 + s)] = incl4[s];
+          for (int s = 0; s < 4; ++s) F.ssum[w + W * (k0 + s)] = incl4[s] - (uint32_t)(kWave * 4) * MAGIC_BITS;
         }
         if (__ballot(sl != 0u) != 0ull) {
           // every lane appends its entries after those of the lanes below it
@@ -813,17 +784,37 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
             qovf = true;  // more uncertified lanes in four segments than the queue holds
           } else {
             int slot = qn + (int)(incl - my);
+            const uint32_t below = (uint32_t)(lane * 4) * MAGIC_BITS;  // offsets of the lanes below
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
               if (sl & (1u << s)) {
                 F.qpos[w][slot] = (uint32_t)((w + W * (k0 + s)) * SEG + lane4);
-                F.qpre[w][slot] = incl4[s] - acc4[s];
+                F.qpre[w][slot] = incl4[s] - raw4[s] - below;
                 ++slot;
               }
             }
             qn += total;
           }
         }
+      };
+      // the batches holding LDS-resident segments first (k0 >= KV - 1), then
+      // one barrier: every wave is past its LDS segments, so the EXACT slots
+      // (which overlay them) can be re-read while the register batches run.
+      // Every batch is unrolled with constant register indices (a runtime
+      // switch over them costs a chain of branches per batch).
+      static_assert((KV - 1) % 4 == 0, "batch KV - 1 is the first to hold LDS-resident segments");
+      constexpr int kLdsBatches = (SPWMAX - (KV - 1) + 3) / 4;
+#pragma unroll
+      for (int b = 0; b < kLdsBatches; ++b) {
+        const int k0 = (KV - 1) + 4 * b;
+        if (k0 < nseg_w) batch(k0, k0 < KV ? to_v4(d[k0 < KV ? k0 : 0]) : lds_q(k0), lds_q(k0 + 1), lds_q(k0 + 2), lds_q(k0 + 3));
+      }
+      __syncthreads();
+      exact_loads<FASTLD>(F, xr, w, min(F.nslot, DCAP), n);
+#pragma unroll
+      for (int b = 0; b < (KV - 1) / 4; ++b) {
+        const int k0 = 4 * b;
+        if (k0 < nseg_w) batch(k0, to_v4(d[k0]), to_v4(d[k0 + 1]), to_v4(d[k0 + 2]), to_v4(d[k0 + 3]));
       }
       if (qovf && lane == 0) atomicOr(&F.fail, 1u);
     }
