@@ -90,43 +90,85 @@ __device__ __forceinline__ void push_cand(FastShared& F, const RowPtrs& Q, int r
   if (slot < (uint32_t)kCandCap) Q.cand[(int64_t)row * kCandCap + slot] = ((uint64_t)__float_as_uint(e) << 32) | id;
 }
 
-// EXACT slots are spread over the waves: slot 0 (the row's first segment,
-// the costliest: it starts at 0 and crosses many binades) to wave 0, the
-// others to waves 1 .. W-1 in turn.
-__device__ __forceinline__ int slot_wave(int slot) { return slot == 0 ? 0 : 1 + (slot - 1) % (W - 1); }
+// EXACT slots are spread over the waves in turn: slot s to wave s % W.
+// Slot 0 is the row's first segment in the first round.
 
 // Issue the re-reads of this wave's EXACT slots into their dump areas (the
 // caller waits for them).
 template <bool FASTLD>
 __device__ __forceinline__ void exact_loads(FastShared& F, const float* xr, int w, int nslot, int n) {
-  for (int slot = w == 0 ? 0 : w; slot < nslot; slot += w == 0 ? DCAP : W - 1)
-    seg_to_lds(xr, F.slotseg[slot], n, FASTLD, &F.u.x.dump[slot][0]);
+  for (int slot = w; slot < nslot; slot += W) seg_to_lds(xr, F.slotseg[slot], n, FASTLD, &F.u.x.dump[slot][0]);
+}
+
+// The exact terms of four consecutive positions (sampler.zig:85), without
+// branches per term.
+__device__ __forceinline__ float4 exact_terms4(float4 v, float m, float T, bool t1) {
+  float x0 = v.x - m, x1 = v.y - m, x2 = v.z - m, x3 = v.w - m;
+  if (!t1) {
+    x0 = x0 / T;
+    x1 = x1 / T;
+    x2 = x2 / T;
+    x3 = x3 / T;
+  }
+  return make_float4(exp_f32(x0), exp_f32(x1), exp_f32(x2), exp_f32(x3));
 }
 
 // Exact terms of this wave's EXACT slots (loaded and waited for), their
 // candidates (once per segment), and the per-lane inclusive prefix tables of
 // the roundings on grids sj .. sj + sng - 1 with the lanes holding a tie.
+// The row's first segment (slot 0 of the first round) needs no tables: the
+// caller sums it term by term.
 __device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
-                                               int nslot, int n, float m, float theta, bool t1) {
+                                               int nslot, int n, float m, float theta, bool t1, bool first_round) {
   const int lane = lane_id();
-  for (int slot = w == 0 ? 0 : w; slot < nslot; slot += w == 0 ? DCAP : W - 1) {
+  for (int slot = w; slot < nslot; slot += W) {
     const int seg = F.slotseg[slot];
     const bool pred = F.sflag[seg] == EXACT_PRED;
     float4* p = reinterpret_cast<float4*>(&F.u.x.dump[slot][lane * 4]);
-    const float4 v = *p;
-    const float vs[4] = {v.x, v.y, v.z, v.w};
-    float es[4];
+    const int pos = seg * SEG + lane * 4;
+    float4 e = exact_terms4(*p, m, P.temperature, t1);
+    e.x = pos + 0 < n ? e.x : 0.0f;
+    e.y = pos + 1 < n ? e.y : 0.0f;
+    e.z = pos + 2 < n ? e.z : 0.0f;
+    e.w = pos + 3 < n ? e.w : 0.0f;
+    *p = e;
+    // candidates (absent positions hold 0 < theta)
+    const bool cand_any = e.x >= theta || e.y >= theta || e.z >= theta || e.w >= theta;
+    if (__ballot(pred && cand_any) != 0ull) {
+      const float es[4] = {e.x, e.y, e.z, e.w};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int pos = seg * SEG + lane * 4 + c;
-      es[c] = pos < n ? exact_term(vs[c], m, P.temperature, t1) : 0.0f;
-      if (pred && pos < n && es[c] >= theta) push_cand(F, Q, row, es[c], (uint32_t)pos);
+      for (int c = 0; c < 4; ++c)
+        if (pred && es[c] >= theta) push_cand(F, Q, row, es[c], (uint32_t)(pos + c));
     }
-    *p = make_float4(es[0], es[1], es[2], es[3]);
     if (pred && lane == 0) F.sflag[seg] = EXACT_DONE;  // a later round must not collect them again
+    if (first_round && slot == 0) continue;
     const int J0 = F.sj[seg];
     const int ng = F.sng[seg];
-    for (int kk = 0; kk < ng; ++kk) {
+    const float es[4] = {e.x, e.y, e.z, e.w};
+    // grids J0 and J0 + 1 (the common case: a segment crossing one binade
+    // boundary) in one pass; further grids one at a time
+    {
+      uint32_t sa = 0, sb = 0;
+      bool ta = false, tb = false;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        bool tie;
+        sa = sat_add(sa, grid_round(es[c], J0, tie), kSat);
+        ta = ta || tie;
+        sb = sat_add(sb, grid_round(es[c], J0 + 1, tie), kSat);
+        tb = tb || tie;
+      }
+      const uint32_t pa = wave_incl_scan_sat(sa, kSat);
+      const uint32_t pb = wave_incl_scan_sat(sb, kSat);
+      const uint64_t ma = __ballot(ta), mb = __ballot(tb);
+      F.u.x.pref[slot][0][lane] = pa;
+      F.u.x.pref[slot][1][lane] = pb;  // NG >= 2: room even when ng == 1
+      if (lane == 0) {
+        F.u.x.tmask[slot][0] = ma;
+        F.u.x.tmask[slot][1] = mb;
+      }
+    }
+    for (int kk = 2; kk < ng; ++kk) {
       uint32_t sum = 0;
       bool tie_any = false;
 #pragma unroll
@@ -162,62 +204,6 @@ __device__ __forceinline__ uint64_t uni_u64(uint64_t x) {
   return ((uint64_t)uni_u((uint32_t)(x >> 32)) << 32) | uni_u((uint32_t)x);
 }
 
-// Combine wave: the exact sequential sum across EXACT segment `slot` from
-// the running value s, using the prefix tables (grids J0 .. J0 + ng - 1)
-// between events and replaying the lane that holds an event term by term.
-__device__ __forceinline__ void resolve_exact(float& s_io, int slot, int J0, int ng, const FastShared& F) {
-  const int lane = lane_id();
-  const float4 e4 = *reinterpret_cast<const float4*>(&F.u.x.dump[slot][lane * 4]);
-  float s = uni_f(s_io);
-  int p = 0;  // first lane not consumed
-  if (grid_of(s).j < J0) {
-    if (s != 0.0f || J0 <= -126) {
-      s_io = uni_f(resolve_generic(s, e4.x, e4.y, e4.z, e4.w, 0));
-      return;
-    }
-    // the row's first segment starts at 0, below its tabulated grids: term
-    // by term until the running sum reaches 2^J0
-    const float lim = __uint_as_float((uint32_t)(J0 + 127) << 23);
-    do {
-      float t = s + readlane_f32(e4.x, p);
-      t = t + readlane_f32(e4.y, p);
-      t = t + readlane_f32(e4.z, p);
-      t = t + readlane_f32(e4.w, p);
-      s = uni_f(t);
-      ++p;
-    } while (p < kWave && s < lim);
-  }
-  for (int guard = 0; guard <= kWave && p < kWave; ++guard) {
-    const Grid gr = grid_of(s);
-    const int k = gr.j - J0;
-    if (k < 0 || k >= ng) {
-      s = uni_f(resolve_generic(s, e4.x, e4.y, e4.z, e4.w, p));
-      break;
-    }
-    const uint32_t pv = F.u.x.pref[slot][k][lane];
-    const uint64_t tm = uni_u64(F.u.x.tmask[slot][k]);
-    const uint32_t base = p > 0 ? readlane_u32(pv, p - 1) : 0u;
-    const uint64_t live = p == 0 ? ~0ull : (~0ull << p);
-    const bool cr = lane >= p && (pv >= kSat || gr.N + (pv - base) >= kGridTop);
-    const uint64_t ev = (__ballot(cr) | tm) & live;
-    if (ev == 0ull) {
-      s = uni_f(grid_value(gr.N + (readlane_u32(pv, kWave - 1) - base), gr.j));
-      break;
-    }
-    const int E = __ffsll((long long)ev) - 1;
-    float t = s;
-    if (E > p) t = grid_value(gr.N + (readlane_u32(pv, E - 1) - base), gr.j);
-    // the lane holding the event, term by term (sampler.zig:87)
-    t = t + readlane_f32(e4.x, E);
-    t = t + readlane_f32(e4.y, E);
-    t = t + readlane_f32(e4.z, E);
-    t = t + readlane_f32(e4.w, E);
-    s = uni_f(t);
-    p = E + 1;
-  }
-  s_io = s;
-}
-
 // An EXACT slot's data as the walk needs it, read ahead of its entry (it does
 // not depend on the running sum): the lane's four exact terms and the prefix
 // tables and tie masks of the slot's first two grids.  The empty asm keeps
@@ -246,7 +232,9 @@ __device__ __forceinline__ SlotAhead slot_ahead(const FastShared& F, int slot) {
   return X;
 }
 
-// resolve_exact on the walk's integer state: the running sum is N on grid j
+// Combine wave: the exact sequential sum across EXACT segment `slot`, using
+// its prefix tables (grids J0 .. J0 + ng - 1) between events and replaying
+// the lane that holds an event term by term.  The running sum is N on grid j
 // (N * 2^(j-23), N < 2^24), kept in scalar registers; the slot's data was
 // read ahead into X.
 __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slot, int J0, int ng,
@@ -825,12 +813,21 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     if (!F.fail) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the EXACT slots' re-reads
       reread();
-      exact_segments(F, Q, P, row, w, min(F.nslot, DCAP), n, m, theta, t1);
-      if (w == 0 && F.sdump[0] == 0) {
-        // the row's first segment starts at 0: its sum needs nothing else,
-        // so the walk's first entry is resolved here, off its serial path
+      exact_segments(F, Q, P, row, w, min(F.nslot, DCAP), n, m, theta, t1, true);
+      if (w == 0) {
+        // the row's first segment (slot 0) from 0, term by term as
+        // sampler.zig:87 adds them: every lane runs the same chain over LDS
+        // broadcasts of the exact terms.  The walk starts after it.
+        const float4* d0 = reinterpret_cast<const float4*>(&F.u.x.dump[0][0]);
         float s0 = 0.0f;
-        resolve_exact(s0, 0, F.sj[0], F.sng[0], F);
+#pragma unroll 8
+        for (int i = 0; i < SEG / 4; ++i) {
+          const float4 e4 = d0[i];
+          s0 = s0 + e4.x;
+          s0 = s0 + e4.y;
+          s0 = s0 + e4.z;
+          s0 = s0 + e4.w;
+        }
         if (lane == 0) {
           F.s_run = s0;
           F.next_e = 1;
@@ -908,7 +905,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         const int nslot = F.nslot;
         exact_loads<FASTLD>(F, xr, w, nslot, n);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
+        exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1, false);
         __syncthreads();
       }
       if (w == 0) {
