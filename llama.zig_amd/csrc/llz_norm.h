@@ -120,8 +120,12 @@ __device__ float wave_seq_list(float s, int len, float thr, int& stop, TermFn te
       if (k8 >= cnt) break;
 #pragma unroll
       for (int k = k8; k < k8 + 8; ++k) {
+        // the empty asm keeps each lane test at its step (hoisted, the 64
+        // lane masks would not fit in scalar registers)
+        int kk = k;
+        asm volatile("" : "+s"(kk));
         const float xk = readlane_f32(x, k);
-        acc = acc + (lane >= k ? xk : -0.0f);
+        acc = acc + (lane >= kk ? xk : -0.0f);
       }
     }
     const bool hit = present && (SUB ? (acc <= 0.0f) : (thr >= 0.0f && acc > thr));

@@ -540,7 +540,7 @@ constexpr int kShortMax = 256;  // longest candidate list of the short path
 // as prefix_filters.  Returns false, on every thread, when elements outside
 // the list decide the cut: the caller then takes the full-row fallback.
 __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& Q, SampleShared& sh, int c,
-                                             float m, float S, uint32_t path) {
+                                             float m, float S, uint32_t path, float u_row) {
   const int row = blockIdx.x;
   const int t = (int)threadIdx.x, lane = lane_id(), w = wave_id();
   const int n = P.n;
@@ -607,7 +607,7 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
       uint32_t token = tok0, consumed = 0;
       if (total > 0.0f) {
         consumed = 1;
-        wave_seq_list<true>(Q.uniforms[row] * total, K, -1.0f, st, pq);
+        wave_seq_list<true>(u_row * total, K, -1.0f, st, pq);
         if (st >= 0) token = (uint32_t)srt[st];
       }
       if (Q.kept_ids || Q.kept_probs) {
@@ -639,7 +639,7 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
 // certify, from the streaming normaliser.  Every thread of the workgroup
 // calls it; `sh` may alias the caller's shared memory once all of it is read.
 __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q, SampleShared& sh, float m,
-                                           float S, uint32_t cc_in, bool uncertified) {
+                                           float S, uint32_t cc_in, bool uncertified, float u_row) {
   int bank = 0;
   const int row = blockIdx.x;
   const int t = (int)threadIdx.x;
@@ -712,7 +712,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   const bool ovf = cc > (uint32_t)kCap;
   const int c = ovf ? kCap : (int)cc;
   if (!ovf && c <= kShortMax && !(P.typical_p > 0.0f && P.typical_p < 1.0f)) {
-    if (!select_short(P, Q, sh, c, m, S, path)) select_full_row(P, Q, sh, bank, m, S, path);
+    if (!select_short(P, Q, sh, c, m, S, path, u_row)) select_full_row(P, Q, sh, bank, m, S, path);
     return;
   }
   const int csort = next_pow2(c);
@@ -746,7 +746,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   const float p_nc = ovf ? kInf : P.cand_theta / S;
   K = prefix_filters(LL, M, p_nc, n, P, S, sh, bank);
   const bool typical = P.typical_p > 0.0f && P.typical_p < 1.0f;
-  const float u = Q.uniforms[row];
+  const float u = u_row;
   bool fallback = K < 0;
 
   if (!fallback) {

@@ -206,10 +206,8 @@ __device__ __forceinline__ uint64_t uni_u64(uint64_t x) {
 
 // An EXACT slot's data as the walk needs it, read ahead of its entry (it does
 // not depend on the running sum): the lane's four exact terms and the prefix
-// tables and tie masks of the slot's first two grids.  The empty asm keeps
-// the values in registers: a select between two fields of a struct can
-// otherwise become a select between their addresses, with the struct on the
-// stack.
+// tables and tie masks of the slot's first two grids (loads in flight until
+// first use).
 struct SlotAhead {
   float4 e4;
   uint32_t pv0, pv1;
@@ -227,8 +225,6 @@ __device__ __forceinline__ SlotAhead slot_ahead(const FastShared& F, int slot) {
   X.tm0h = (uint32_t)(t0 >> 32);
   X.tm1l = (uint32_t)t1;
   X.tm1h = (uint32_t)(t1 >> 32);
-  asm volatile("" : "+v"(X.e4.x), "+v"(X.e4.y), "+v"(X.e4.z), "+v"(X.e4.w), "+v"(X.pv0), "+v"(X.pv1));
-  asm volatile("" : "+v"(X.tm0l), "+v"(X.tm0h), "+v"(X.tm1l), "+v"(X.tm1h));
   return X;
 }
 
@@ -257,30 +253,29 @@ __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slo
     t = t + X.e4.w;
     const uint64_t tm0 = ((uint64_t)uni_u(X.tm0h) << 32) | uni_u(X.tm0l);
     const uint64_t ev = __ballot(X.pv0 >= kSat || N + X.pv0 >= kGridTop) | tm0;
-    if (ev == 0ull) {
-      N_io = uni_u(N + readlane_u32(X.pv0, kWave - 1));
+    // three outcomes, computed together and taken with one branch: no event
+    // on grid J0 (the table's total), an event in the last lane, or one
+    // crossing into grid J0 + 1 with the rest of the segment event-free there
+    const int E = ev != 0ull ? __ffsll((long long)ev) - 1 : kWave - 1;
+    const Grid g = grid_of(uni_f(readlane_f32(t, E)));
+    const uint32_t T0 = readlane_u32(X.pv0, kWave - 1);
+    const uint32_t B = readlane_u32(X.pv1, E), T = readlane_u32(X.pv1, kWave - 1);
+    const uint64_t tm1 = ((uint64_t)uni_u(X.tm1h) << 32) | uni_u(X.tm1l);
+    const uint64_t live1 = E < kWave - 1 ? (~0ull << (E + 1)) : 0ull;
+    const bool none = ev == 0ull;
+    const bool last = !none && E == kWave - 1;
+    // table entries are saturating prefix sums: T - B is exact below kSat
+    const bool cross = !none && !last && g.j == J0 + 1 && ng >= 2 && T < kSat && g.N + (T - B) < kGridTop &&
+                       (tm1 & live1) == 0ull;
+    if (none || last || cross) {
+      N_io = none ? N + T0 : (last ? g.N : g.N + (T - B));
+      j_io = none ? j : g.j;
       return;
     }
-    const int E = __ffsll((long long)ev) - 1;
-    const Grid g = grid_of(uni_f(readlane_f32(t, E)));
+    // anything else: the general steps below, from the first event on
     N = g.N;
     j = g.j;
     p = E + 1;
-    if (p == kWave) {
-      N_io = N;
-      j_io = j;
-      return;
-    }
-    if (j == J0 + 1 && ng >= 2) {
-      const uint32_t B = readlane_u32(X.pv1, E), T = readlane_u32(X.pv1, kWave - 1);
-      const uint64_t tm1 = ((uint64_t)uni_u(X.tm1h) << 32) | uni_u(X.tm1l);
-      // table entries are saturating prefix sums: T - B is exact below kSat
-      if (T < kSat && N + (T - B) < kGridTop && (tm1 & (~0ull << p)) == 0ull) {
-        N_io = uni_u(N + (T - B));
-        j_io = j;
-        return;
-      }
-    }
   }
   // selects rather than branches: a taken branch costs a wave running alone
   // far more than the few operations it would skip
@@ -308,21 +303,22 @@ __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slo
     const uint32_t base = p > 0 ? base_l : 0u;
     const uint64_t live = ~0ull << p;
     const bool cr = lane >= p && (pv >= kSat || N + (pv - base) >= kGridTop);
+    // every lane from p replays its own four terms (sampler.zig:87) from the
+    // table's integer before it, as if it held the first event: one readlane
+    // of the event lane's result instead of four dependent steps
+    const uint32_t before = N + (wave_shift_up1(pv) - base);  // lane p: N
+    float t = __uint_as_float(grid_bits(before, j));
+    t = t + X.e4.x;
+    t = t + X.e4.y;
+    t = t + X.e4.z;
+    t = t + X.e4.w;
     const uint64_t ev = (__ballot(cr) | tm) & live;
     if (ev == 0ull) {
       N = uni_u(N + (readlane_u32(pv, kWave - 1) - base));
       break;
     }
     const int E = __ffsll((long long)ev) - 1;
-    const uint32_t NE_l = uni_u(N + (readlane_u32(pv, (E - 1) & (kWave - 1)) - base));
-    const uint32_t NE = E > p ? NE_l : N;
-    // the lane holding the event, term by term (sampler.zig:87)
-    float t = __uint_as_float(grid_bits(NE, j));
-    t = t + readlane_f32(X.e4.x, E);
-    t = t + readlane_f32(X.e4.y, E);
-    t = t + readlane_f32(X.e4.z, E);
-    t = t + readlane_f32(X.e4.w, E);
-    const Grid g = grid_of(uni_f(t));
+    const Grid g = grid_of(uni_f(readlane_f32(t, E)));
     N = g.N;
     j = g.j;
     p = E + 1;
@@ -480,6 +476,9 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   const int G = (n + SEG - 1) / SEG;
   const int SPW = (G + W - 1) / W;
   const bool fits = SPW <= SPWMAX && P.cand_theta > 0.0f && fabsf(l2e_t) <= 0x1p40f;
+  // the row's uniform, read now: the selection stage's draw needs it at the
+  // end of a long serial path (a memory barrier keeps the load here)
+  const float u_row = Q.uniforms[row];
   // wave w owns segments w, w + W, w + 2W, ...: its k-th is segment w + W k
   // (interleaved, so the costly start of the row is shared by every wave)
   const int nseg_w = fits ? max(0, (G - w + W - 1) / W) : 0;
@@ -531,14 +530,42 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     asm volatile("" : "+s"(l));
     return l;
   };
-  {
+  // LDS-resident segments of a 16-byte-load row first: their loads were
+  // issued first, so they land first and are processed while the register
+  // loads are still in flight (a wait for just those: the register loads are
+  // the KV most recent)
+  auto lds_segments = [&]() {
+    for (int k = KV; k < nseg_w; ++k) {
+      float4* p = reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]);
+      const float4 v = *p;
+      mx = fmaxf(mx, max4(v));
+      const float4 q = q_of(v, l2e_t, cw);
+      *p = q;
+      const float a = wave_sum_f32((q.x + q.y) + (q.z + q.w));
+      if (lane == 0) F.v.aseg[w + W * k] = a;
+      nanf |= a != a ? 1u : 0u;
+    }
+  };
+  const bool lds_first = FASTLD && nseg_w > KV;
+  float mr;
+  if (lds_first) {
+    static_assert(KV == 45, "the wait below counts KV register loads");
+    asm volatile("s_waitcnt vmcnt(45)" ::: "memory");
+    if ((w + W * (nseg_w - 1) + 1) * SEG > n) {  // the row's partial last segment
+      const int k = nseg_w - 1;
+      *reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]) = ld4(xr, base_w + k * (W * SEG), n);
+    }
+    // any finite reference of this wave: |m - mr| is checked in phase M
+    mr = wave_max_f32(max4(*reinterpret_cast<const float4*>(&F.u.data[w][0][lane * 4])));
+  } else {
     const bool ok0 = lane4 < seg_lim(0);
-    float mr = wave_max_f32(ok0 ? max4(d[0]) : -kInfS);
-    if (!(fabsf(mr) <= 3.0e38f)) mr = 0.0f;  // any finite reference: |m - mr| is checked below
-    cw = mr * l2e_t;
+    mr = wave_max_f32(ok0 ? max4(d[0]) : -kInfS);
   }
+  if (!(fabsf(mr) <= 3.0e38f)) mr = 0.0f;
+  cw = mr * l2e_t;
+  if (lds_first) lds_segments();
   // segment sums are kept one per lane (lane k: segment k) and stored after
-  // the loop: an LDS access here would wait for the LDS-bound loads
+  // the loop
   float my_a = 0.0f;
 #pragma unroll
   for (int k = 0; k < KV; ++k) {
@@ -558,24 +585,8 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     __builtin_amdgcn_sched_barrier(0);  // one segment at a time: bounded live ranges
   }
   if (lane < min(nseg_w, KV)) F.v.aseg[w + W * lane] = my_a;
-  nanf = (lane < min(nseg_w, KV) && my_a != my_a) ? 1u : 0u;
-  if (nseg_w > KV) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (FASTLD && (w + W * (nseg_w - 1) + 1) * SEG > n) {  // the row's partial last segment
-      const int k = nseg_w - 1;
-      *reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]) = ld4(xr, base_w + k * (W * SEG), n);
-    }
-  }
-  for (int k = KV; k < nseg_w; ++k) {
-    float4* p = reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]);
-    const float4 v = *p;
-    mx = fmaxf(mx, max4(v));
-    const float4 q = q_of(v, l2e_t, cw);
-    *p = q;
-    const float a = wave_sum_f32((q.x + q.y) + (q.z + q.w));
-    if (lane == 0) F.v.aseg[w + W * k] = a;
-    nanf |= a != a ? 1u : 0u;
-  }
+  nanf |= (lane < min(nseg_w, KV) && my_a != my_a) ? 1u : 0u;
+  if (!lds_first && nseg_w > KV) lds_segments();  // element loads: waited for where they are read
   if (!fits) {  // rows the fast path does not take: maximum and NaN scan only
     for (int i = t; i < n; i += NT) {
       const float v = xr[i];
@@ -917,37 +928,50 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         const int ne = F.ne;
         bool fail = false, more = false;
         // windows of 64 entries, one per lane; in each, the runs before an
-        // EXACT entry are added together while its slot data is read ahead
+        // EXACT entry are added as one difference of a prefix sum over the
+        // window, and the next EXACT entry's slot data is read while this one
+        // is resolved
         for (int held = e & ~(kWave - 1); held < ne && !fail && !more; held += kWave) {
           const bool ok = held + lane < ne;
           const uint32_t ea = ok ? F.u.x.ent_a[held + lane] : 0u;
           const uint32_t eb = ok ? F.u.x.ent_b[held + lane] : 0u;
           const int ej = (int)((ea >> 16) & 0xffu) - 128;
-          const uint64_t exm = __ballot(ok && (ea & 3u) == E_EXACT);
+          const bool isx = ok && (ea & 3u) == E_EXACT;
+          const uint64_t exm = __ballot(isx);
           const uint64_t tim = __ballot(ok && (ea & 3u) == E_TIE);
+          // <= 64 * 2^25: no wrap
+          const uint32_t psum =
+              wave_incl_scan_op(ok && !isx ? eb : 0u, 0u, [](uint32_t a, uint32_t b) { return a + b; });
           const int wend = min(ne - held, kWave);
+          auto slot_at = [&](int x) {
+            int sl = (int)(int8_t)(readlane_u32(eb, x) & 0xffu);
+            if (round > 0) sl = F.sdump[(readlane_u32(ea, x) >> 2) & 1023u];  // slots were reassigned
+            return __builtin_amdgcn_readfirstlane(sl);
+          };
+          auto next_x = [&](int from) {  // first EXACT entry at or after `from` (wend: none)
+            const uint64_t r = from < kWave ? exm & (~0ull << from) : 0ull;
+            return r != 0ull ? __ffsll((long long)r) - 1 : wend;
+          };
           int i = e - held;
-          while (i < wend) {
-            const uint64_t rest = exm & (~0ull << i);
-            const int x = rest != 0ull ? __ffsll((long long)rest) - 1 : wend;
-            int xslot = -1;
-            SlotAhead X = {};
-            if (x < wend) {
-              const uint32_t xa = readlane_u32(ea, x), xb = readlane_u32(eb, x);
-              xslot = (int)(int8_t)(xb & 0xffu);
-              if (round > 0) xslot = F.sdump[(xa >> 2) & 1023u];  // slots were reassigned
-              xslot = __builtin_amdgcn_readfirstlane(xslot);
-              if (xslot >= 0) X = slot_ahead(F, xslot);
-            }
+          int x = next_x(i);
+          int xslot = x < wend ? slot_at(x) : -1;
+          SlotAhead X = {};
+          if (xslot >= 0) X = slot_ahead(F, xslot);
+          while (true) {
+            const int x2 = x < wend ? next_x(x + 1) : wend;
+            const int xslot2 = x2 < wend ? slot_at(x2) : -1;
+            SlotAhead X2 = {};
+            if (xslot2 >= 0) X2 = slot_ahead(F, xslot2);
             // runs (and PLAIN_TIE segments) i .. x-1 on grid jc: terms are >=
             // 0, so they stay in the binade exactly when their total does
             if (x > i) {
               const uint64_t span = (x >= kWave ? ~0ull : ((1ull << x) - 1ull)) & (~0ull << i);
               bool bad;
               if ((tim & span) == 0ull) {
-                const bool in = ((span >> lane) & 1ull) != 0ull;
-                N += wave_sum_u32(in ? eb : 0u);  // <= 64 * 2^25: no wrap
-                bad = __ballot(in && ej != jc) != 0ull;
+                const uint32_t hi = readlane_u32(psum, x - 1);
+                const uint32_t lo = readlane_u32(psum, (i - 1) & (kWave - 1));
+                N += hi - (i > 0 ? lo : 0u);
+                bad = __ballot(((span >> lane) & 1ull) != 0ull && ej != jc) != 0ull;
               } else {
                 // a PLAIN_TIE segment adds the units its ties take for the
                 // parity of the integer it starts at: one entry at a time
@@ -971,8 +995,12 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
               more = true;  // EXACT segments past this round's slots
               break;
             }
-            resolve_ahead(N, jc, xslot, (int)readlane_u32((uint32_t)ej, i), (int)((readlane_u32(eb, i) >> 8) & 0xffu), X, F);
+            resolve_ahead(N, jc, xslot, (int)readlane_u32((uint32_t)ej, x), (int)((readlane_u32(eb, x) >> 8) & 0xffu),
+                          X, F);
             ++i;
+            x = x2;
+            xslot = xslot2;
+            X = X2;
           }
           e = held + i;
         }
@@ -995,7 +1023,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
 
   // ---- the selection stage, on the same workgroup and shared memory
   __syncthreads();  // F is read: the selection reuses the memory
-  select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified);
+  select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified, u_row);
 }
 
 }  // namespace
