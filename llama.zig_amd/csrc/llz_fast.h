@@ -185,6 +185,27 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return __uint_as_float(lane_readlast(r));
 }
 
+// A wave's total of v in lane 63 only, in six folded DPP additions (row
+// sums, then rows 0-1 and 2-3, then all four; the other lanes end with
+// partial sums).  The order of the additions differs from a lane-order
+// scan: for estimates only.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add_f32(float s) {
+  // -0 is the exact identity of f32 addition, so the addition folds into one
+  // DPP instruction
+  return s + __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-0.0f), __float_as_int(s), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float wave_total_f32(float v) {
+  float s = v;
+  s = dpp_add_f32<0x111>(s);  // row_shr:1
+  s = dpp_add_f32<0x112>(s);  // row_shr:2
+  s = dpp_add_f32<0x114>(s);  // row_shr:4
+  s = dpp_add_f32<0x118>(s);  // row_shr:8: lane 15 of each row holds its row's sum
+  s = dpp_add_f32<0x142>(s);  // row_bcast:15: lane 63 holds rows 2 + 3
+  s = dpp_add_f32<0x143>(s);  // row_bcast:31: lane 63 holds all four rows
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
+}
+
 __device__ __forceinline__ float wave_max_f32(float v) {
   const uint32_t r = wave_incl_scan_op(__float_as_uint(v), __float_as_uint(-__builtin_inff()),
                                        [](uint32_t a, uint32_t b) {

@@ -541,7 +541,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       mx = fmaxf(mx, max4(v));
       const float4 q = q_of(v, l2e_t, cw);
       *p = q;
-      const float a = wave_sum_f32((q.x + q.y) + (q.z + q.w));
+      const float a = wave_total_f32((q.x + q.y) + (q.z + q.w));
       if (lane == 0) F.v.aseg[w + W * k] = a;
       nanf |= a != a ? 1u : 0u;
     }
@@ -571,7 +571,9 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   for (int k = 0; k < KV; ++k) {
     const float4 v = d[k];
     const bool ok = lane4 < seg_lim(k);  // this wave's and inside the row
-    mx = fmaxf(mx, ok ? max4(v) : -kInfS);
+    float m4 = max4(v);
+    asm volatile("" : "+v"(m4));  // a select, not a branch around max4
+    mx = fmaxf(mx, ok ? m4 : -kInfS);
     float4 q = q_of(v, l2e_t, cw);  // a NaN logit makes its segment sum NaN
     q.x = ok ? q.x : 0.0f;
     q.y = ok ? q.y : 0.0f;
@@ -580,7 +582,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     // materialise q here, while the loads land (not sunk into phase S)
     asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
     d[k] = q;
-    const float a = wave_sum_f32((q.x + q.y) + (q.z + q.w));
+    const float a = wave_total_f32((q.x + q.y) + (q.z + q.w));
     my_a = lane == k ? a : my_a;
     __builtin_amdgcn_sched_barrier(0);  // one segment at a time: bounded live ranges
   }
