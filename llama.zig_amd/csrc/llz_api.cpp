@@ -164,6 +164,12 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   P.src_stride = src_stride;
   P.orig_stride = row_stride;
   P.flags = (cfg->temperature == 1.0f ? kFlagTIsOne : 0u) | (vec ? kFlagVecSrc : 0u) | kFlagFallback;
+  // LLZ_TEST_QUEUE_CAP: a smaller special-queue chunk, so that tests reach
+  // the chunked queue on ordinary rows (the kernel clamps it to its own)
+  {
+    const char* qc = std::getenv("LLZ_TEST_QUEUE_CAP");
+    P.qcap = qc ? (uint32_t)std::strtoul(qc, nullptr, 10) : 0u;
+  }
 
   RowPtrs Q{};
   Q.src = src;

@@ -31,14 +31,16 @@
 // Error bound of the estimate relative to the reference's term e =
 // exp(RN(RN(v - m) / T)) for the terms that can round to a non-zero integer
 // (X = (v - m) log2(e) / T, |X| <= 25 - j): the reference's own two
-// roundings of its argument and the rounding of log2(e)/T contribute
-// 3|X| 2^-24 (in log2 units), the rounding of v RN(log2(e)/T) - c_w at most
-// (|X| + 32) 2^-24 and that of the argument of R_w at most 32 2^-24 (the
-// kernel requires |(m - m_w) RN(log2(e)/T)| <= 32), so together
-// ln2 (4|X| + 64) 2^-24; the two hardware exp2 (<= 2^-23 each), the final
-// multiply (2^-24) and the reference exp (< 2^-23) add < 2^-21.  eps(j) is
-// twice that bound.  For |X| < 25 - j the terms are below 1/4 of the grid
-// and round to 0 on both sides.
+// roundings of its argument (one when T == 1: RN(x / 1) is exact) and the
+// rounding of log2(e)/T contribute 3|X| 2^-24 (2|X| when T == 1, in log2
+// units); with B_w = c_w - m RN(log2(e)/T) (|B_w| <= 32, checked; the kernel
+// bounds with the wave's rounded value |aw| = |RN(B_w)|), the rounding of
+// v RN(log2(e)/T) - c_w adds at most (|X| + |B_w|) 2^-24 and that of the
+// argument of R_w at most |B_w| 2^-24, so together ln2 (4|X| + 2|B_w|) 2^-24
+// (3|X| when T == 1), taken with 3 units to spare; the two hardware exp2
+// (<= 2^-23 each), the final multiply (2^-24) and the reference exp
+// (< 2^-23) add < 2^-21.  eps(j) is twice that bound.  For |X| > 25 - j the
+// terms are below 1/4 of the grid and round to 0 on both sides.
 //
 // Anything the fast path cannot certify (an unpredicted binade crossing, a
 // grid mismatch, a queue overflow, a row longer than the resident capacity)
@@ -112,6 +114,7 @@ struct FastShared {
   int16_t slotseg[fastp::DCAP];                 // segment held by each EXACT slot
   float mw[fastp::W];
   float cw[fastp::W];
+  float bw[fastp::W];       // per wave: |aw|, the R_w argument's magnitude (error bound)
   uint32_t nanw[fastp::W];
   float wtot[fastp::W];     // per wave: sum of its scaled segment sums
   uint32_t wflag[fastp::W]; //   bit 0: not certifiable, bit 1: candidate flood
@@ -219,10 +222,13 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
 }
 
 // Relative error bound of the estimate for terms that matter on grid j
-// (see the header comment), doubled.
-__device__ __forceinline__ float fast_eps(int j) {
+// (see the header comment), doubled.  bw = |B_w|, the magnitude of the wave's
+// rounded R_w argument fma(m, -RN(log2(e)/T), c_w) (at most 32); t1: T == 1,
+// where the reference's argument takes one rounding instead of two.
+__device__ __forceinline__ float fast_eps(int j, float bw, bool t1) {
   const float ax = (float)(25 - j);
-  return 2.0f * (0.6931472f * (4.0f * ax + 64.0f) * 0x1p-24f + 0x1p-21f);
+  const float coef = (t1 ? 3.0f : 4.0f) * ax + 2.0f * bw + 3.0f;
+  return 2.0f * (0.6931472f * coef * 0x1p-24f + 0x1p-21f);
 }
 
 // A float with its mantissa LSB forced to 1 (see the no-tie argument: an
@@ -236,11 +242,11 @@ struct GridConst {
   float tspec;         // rh >= tspec: large term or candidate
 };
 
-__device__ __forceinline__ GridConst grid_const(int j, float R, float theta) {
+__device__ __forceinline__ GridConst grid_const(int j, float R, float theta, float bw, bool t1) {
   GridConst c;
   c.j = j;
   const float sc = ldexpf(R, 23 - j);
-  const float eps = fast_eps(j);
+  const float eps = fast_eps(j, bw, t1);
   c.sc_lo = odd_mantissa(sc * (1.0f - eps));
   c.sc_hi = odd_mantissa(sc * (1.0f + eps));
   // candidates: e >= theta  =>  e / u >= theta 2^(23-j)

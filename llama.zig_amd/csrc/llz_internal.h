@@ -34,7 +34,7 @@ struct RowParams {
   int64_t src_stride;
   int64_t orig_stride;
   uint32_t flags;
-  uint32_t pad;
+  uint32_t qcap;  // special-queue chunk size override for tests (0: the kernel's own)
 };
 
 struct RowPtrs {

@@ -340,6 +340,7 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
                                                 int qn, const float4 (&v4q)[2], float Rw, float cw, float m,
                                                 float theta, bool t1) {
   const int lane = lane_id();
+  const float bw = F.bw[w];  // |aw| of this wave (phase M)
   const int n = P.n;
   uint32_t pos2[2], pre2[2], rl[2][4], rx[2][4];
   int j2[2];
@@ -353,7 +354,7 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
     pos2[h] = act2[h] ? F.qpos[w][i] : 0u;
     pre2[h] = act2[h] ? F.qpre[w][i] : 0u;
     j2[h] = F.sj[pos2[h] >> 8];
-    const GridConst gc = grid_const(j2[h], Rw, theta);
+    const GridConst gc = grid_const(j2[h], Rw, theta, bw, t1);
     const uint32_t tspec = __float_as_uint(gc.tspec);
     const float vv[4] = {v4q[h].x, v4q[h].y, v4q[h].z, v4q[h].w};
 #pragma unroll
@@ -632,6 +633,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   if (!nan_sum) {
     const float aw = fmaf(m, -l2e_t, cw);
     const float Rw = __builtin_amdgcn_exp2f(aw);  // q * Rw ~ e = exp((v - m) / T)
+    if (lane == 0) F.bw[w] = fabsf(aw);
     // Prediction in index order: lane k takes round k (segments W k .. W k +
     // W - 1, one per wave, each scaled by its wave's R); a scan over the rounds
     // gives every segment's running sum.  Every wave computes it for its own
@@ -703,25 +705,34 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     // integer sum before it), and the queue is settled when full.
     int qn = 0;
     float4 v4q[2];
-    auto reread = [&]() {  // the queued lanes' logits (wave-uniform count qn)
+    auto reread = [&](int cnt) {  // the logits of the first cnt queued lanes (wave-uniform)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int i = h * kWave + lane;
-        const int pos = i < qn ? (int)F.qpos[w][i] : 0;
+        const int pos = i < cnt ? (int)F.qpos[w][i] : 0;
         v4q[h] = FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n);
       }
     };
-    auto settle = [&]() {
-      settle_specials(F, Q, P, row, w, qn, v4q, Rw, cw, m, theta, t1);
-      qn = 0;
-    };
+    auto settle = [&](int cnt) { settle_specials(F, Q, P, row, w, cnt, v4q, Rw, cw, m, theta, t1); };
+    // The queue is filled in chunks of at most qcap <= QCAP entries, each holding
+    // whole batches (a segment's lanes are settled together): chunk 0 in LDS,
+    // chunks 1.. in this row's part of the fallback buffers 0 (positions) and
+    // 1 (prefixes), SPW * 64 entries per wave (a wave queues each of its lanes
+    // at most once per segment).  All are settled in phase F+X: phase S never
+    // settles.  qch: current chunk, qn: its entries, lane c of ccnt: the
+    // entries of an earlier chunk c.
+    uint32_t* const ovp = Q.fb + (int64_t)row * n + (int64_t)w * SPW * kWave;
+    uint32_t* const ovq = ovp + (int64_t)P.rows * n;
+    const int qcap = (P.qcap > 0u && P.qcap < (uint32_t)QCAP) ? (int)P.qcap : QCAP;  // entries per chunk
+    int qch = 0;
+    uint32_t ccnt = 0;
     bool qovf = false;
     if (!F.fail) {
       // per-segment constants, lane k for this wave's segment k; segments
       // that are not PLAIN (or absent) get zero scales and an unreachable
       // tspec, so every bracket is MAGIC and no lane is special
       const bool plain_l = have && F.sflag[w + W * lane] == (uint8_t)PLAIN;
-      const GridConst gc_l = grid_const(have ? (int)F.sj[w + W * lane] : 0, Rw, theta);
+      const GridConst gc_l = grid_const(have ? (int)F.sj[w + W * lane] : 0, Rw, theta, fabsf(aw), t1);
       const float sclo_l = plain_l ? gc_l.sc_lo : 0.0f;
       const float schi_l = plain_l ? gc_l.sc_hi : 0.0f;
       const uint32_t tspec_l = plain_l ? __float_as_uint(gc_l.tspec) : 0xffffffffu;
@@ -777,20 +788,33 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           const uint32_t my = (uint32_t)__popc(sl);
           const uint32_t incl = wave_incl_scan_op(my, 0u, [](uint32_t a, uint32_t b) { return a + b; });
           const int total = (int)lane_readlast(incl);
-          if (qn + total > QCAP) {
-            reread();
-            settle();
-          }
-          if (total > QCAP) {
-            qovf = true;  // more uncertified lanes in four segments than the queue holds
+          if (total > qcap) {
+            qovf = true;  // more uncertified lanes in four segments than a chunk holds
           } else {
+            if (qn + total > qcap) {  // the batch starts the next chunk (chunks hold whole batches)
+              ccnt = lane == qch ? qn : ccnt;
+              ++qch;
+              qn = 0;
+              // chunk qch occupies entries [(qch - 1) qcap, qch qcap) of the wave's
+              // SPW * 64 (always enough: a wave has at most SPW / 4 + 2 batches)
+              if (qch * qcap > SPW * kWave || qch >= kWave) qovf = true;
+            }
             int slot = qn + (int)(incl - my);
             const uint32_t below = (uint32_t)(lane * 4) * MAGIC_BITS;  // offsets of the lanes below
+            uint32_t* const op = ovp + (qch - 1) * qcap;
+            uint32_t* const oq = ovq + (qch - 1) * qcap;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
               if (sl & (1u << s)) {
-                F.qpos[w][slot] = (uint32_t)((w + W * (k0 + s)) * SEG + lane4);
-                F.qpre[w][slot] = incl4[s] - raw4[s] - below;
+                const uint32_t pos = (uint32_t)((w + W * (k0 + s)) * SEG + lane4);
+                const uint32_t pre = incl4[s] - raw4[s] - below;
+                if (qch == 0) {
+                  F.qpos[w][slot] = pos;
+                  F.qpre[w][slot] = pre;
+                } else if (!qovf) {
+                  op[slot] = pos;
+                  oq[slot] = pre;
+                }
                 ++slot;
               }
             }
@@ -817,6 +841,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         const int k0 = 4 * b;
         if (k0 < nseg_w) batch(k0, to_v4(d[k0]), to_v4(d[k0 + 1]), to_v4(d[k0 + 2]), to_v4(d[k0 + 3]));
       }
+      ccnt = lane == qch ? qn : ccnt;  // the last chunk's entries
       if (qovf && lane == 0) atomicOr(&F.fail, 1u);
     }
 
@@ -824,8 +849,9 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     // the remaining specials, whose re-reads land while the slots are
     // evaluated
     if (!F.fail) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the EXACT slots' re-reads
-      reread();
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the EXACT slots' re-reads (and phase S's stores)
+      const int qn0 = (int)readlane_u32(ccnt, 0);
+      reread(qn0);
       exact_segments(F, Q, P, row, w, min(F.nslot, DCAP), n, m, theta, t1, true);
       if (w == 0) {
         // the row's first segment (slot 0) from 0, term by term as
@@ -846,7 +872,17 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           F.next_e = 1;
         }
       }
-      settle();
+      settle(qn0);
+      // the chunks past the LDS queue (rare)
+      for (int c = 1; c <= qch; ++c) {
+        const int cn = (int)readlane_u32(ccnt, c);
+        for (int i = lane; i < cn; i += kWave) {
+          F.qpos[w][i] = ovp[(c - 1) * qcap + i];
+          F.qpre[w][i] = ovq[(c - 1) * qcap + i];
+        }
+        reread(cn);
+        settle(cn);
+      }
     }
     __syncthreads();
 

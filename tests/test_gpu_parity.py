@@ -348,3 +348,42 @@ def test_non_finite_rows(cuda):
             assert g["kept_count"][r] == o.kept_count, r
             k = min(o.kept_count, g["cap"])
             assert np.array_equal(g["kept_ids"][r, :k], o.kept_ids()[:k]), r
+
+
+# ---------------------------------------------------------------------------
+# the special queue's chunks past the LDS queue
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("qcap", [8, 32, 64])
+def test_special_queue_chunks(cuda, monkeypatch, qcap):
+    """LLZ_TEST_QUEUE_CAP shrinks the special-queue chunk, so ordinary rows fill
+    several chunks (kept in the workspace's fallback buffers); a batch with
+    more specials than a chunk holds (the row's first segments have many
+    large terms) sends its row to the streaming normaliser.  Results stay
+    bit-exact; at 32 and 64 some rows (each with over 64 specials per wave,
+    so several chunks) still take the fast path."""
+    import torch
+
+    monkeypatch.setenv("LLZ_TEST_QUEUE_CAP", str(qcap))
+    for name, rows in [("headline", 8), ("c2", 6)]:
+        w = WORKLOADS[name]
+        x = w.logits(rows)
+        u = llz.rng_uniforms(w.uniform_seed, rows)
+        cfg = llz.SamplerConfig.of(w.params)
+        ws = torch.zeros(llz.workspace_bytes(rows, w.vocab, cfg), dtype=torch.uint8, device=cuda)
+        xt = torch.from_numpy(np.ascontiguousarray(x)).to(cuda)
+        ut = torch.from_numpy(np.ascontiguousarray(u, dtype=np.float32)).to(cuda)
+        res = llz.sample_rows(xt, cfg, ut, kept_cap=256, stats=True, workspace=ws)
+        torch.cuda.synchronize()
+        status = ws[: rows * 4].view(torch.int32).cpu().numpy()  # per-row path bits (workspace offset 0)
+        if qcap >= 32 and name == "headline":
+            assert ((status & 8) == 0).any(), f"{name}: no row kept the fast path: {status}"
+        g = dict(
+            tokens=res.tokens.cpu().numpy().view(np.uint32),
+            consumed=res.consumed.cpu().numpy(),
+            kept_count=res.kept_count.cpu().numpy().view(np.uint32),
+            kept_ids=res.kept_ids.cpu().numpy().view(np.uint32),
+            kept_probs=res.kept_probs.cpu().numpy(),
+            stats=res.row_stats.cpu().numpy(),
+            cap=256,
+        )
+        compare_rows(x, w.params, u, g)
