@@ -94,16 +94,39 @@ __device__ float wave_accumulate(float s, const float (&x)[V]) {
   }
 }
 
+// The chain of one 64-term chunk, the terms held one per lane (lane i: term
+// i, i < len <= 64; absent terms have the sign bit set): lane i ends with the
+// running value after term i, the lanes from len on with the value after
+// the last.  At step k every lane from k on adds term k (the others add -0,
+// which leaves any value unchanged).  The steps use constant lane indices and
+// no branches (a wave running alone pays for every dependent step).  SUB
+// subtracts: s - x is computed as s + (-x), which IEEE defines to be the same.
+template <bool SUB>
+__device__ __forceinline__ float wave_chain_lanes(float s, float x0, int len) {
+  const int lane = lane_id();
+  const bool present = lane < len && !(as_bits(x0) >> 31);
+  const float x = present ? (SUB ? -x0 : x0) : -0.0f;
+  float acc = s;
+#pragma unroll
+  for (int k8 = 0; k8 < kWave; k8 += 8) {
+    if (k8 >= len) break;
+#pragma unroll
+    for (int k = k8; k < k8 + 8; ++k) {
+      // the empty asm keeps each lane test at its step (hoisted, the 64
+      // lane masks would not fit in scalar registers)
+      int kk = k;
+      asm volatile("" : "+s"(kk));
+      const float xk = readlane_f32(x, k);
+      acc = acc + (lane >= kk ? xk : -0.0f);
+    }
+  }
+  return acc;
+}
+
 // Sequential accumulation over a short list by one wave (the reference's
 // loop, one term at a time).  ADD stops at the first s > thr (thr >= 0),
-// SUB at the first s <= 0; absent terms (sign bit set) are skipped.
-//
-// Lane i of a 64-term chunk runs the chain up to term i: at step k every
-// lane from k on adds term k (the others add -0, which leaves any value
-// unchanged), so after the chunk lane i holds the running value after term
-// i.  The steps use constant lane indices and no branches (a wave running
-// alone pays for every dependent step); one ballot then finds the first stop.
-// s - x is computed as s + (-x), which IEEE defines to be the same.
+// SUB at the first s <= 0; absent terms (sign bit set) are skipped.  Chunk by
+// chunk of 64 (wave_chain_lanes), one ballot per chunk for the first stop.
 template <bool SUB, typename TermFn>
 __device__ float wave_seq_list(float s, int len, float thr, int& stop, TermFn term) {
   stop = -1;
@@ -111,23 +134,9 @@ __device__ float wave_seq_list(float s, int len, float thr, int& stop, TermFn te
   for (int base = 0; base < len; base += kWave) {
     const int p = base + lane;
     const float x0 = p < len ? term(p) : -0.0f;
-    const bool present = p < len && !(as_bits(x0) >> 31);
-    const float x = present ? (SUB ? -x0 : x0) : -0.0f;
     const int cnt = min(kWave, len - base);
-    float acc = s;
-#pragma unroll
-    for (int k8 = 0; k8 < kWave; k8 += 8) {
-      if (k8 >= cnt) break;
-#pragma unroll
-      for (int k = k8; k < k8 + 8; ++k) {
-        // the empty asm keeps each lane test at its step (hoisted, the 64
-        // lane masks would not fit in scalar registers)
-        int kk = k;
-        asm volatile("" : "+s"(kk));
-        const float xk = readlane_f32(x, k);
-        acc = acc + (lane >= kk ? xk : -0.0f);
-      }
-    }
+    const bool present = lane < cnt && !(as_bits(x0) >> 31);
+    const float acc = wave_chain_lanes<SUB>(s, x0, cnt);
     const bool hit = present && (SUB ? (acc <= 0.0f) : (thr >= 0.0f && acc > thr));
     const uint64_t hits = __ballot(hit);
     if (hits != 0ull) {

@@ -572,12 +572,18 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
   lds_barrier();
   if (w == 0) {
     auto pq = [&](int q) { return __uint_as_float(~(uint32_t)(srt[q] >> 32)); };
+    // the list's first 64 probabilities, one per lane, read once (xl; the
+    // lanes past the list hold -0, an absent term): every chain over at most
+    // 64 terms, and the counts over a list of at most 64, use them
+    const float xl = lane < c ? pq(lane) : -0.0f;
     // certified prefix M: every element outside the list has p <= theta / S
     const float p_nc = P.cand_theta / S;
     int M = c;
     if (P.cand_theta > 0.0f) {
       M = 0;
-      for (int b = 0; b < c; b += kWave) M += __popcll(__ballot(b + lane < c && pq(b + lane) > p_nc));
+      if (c <= kWave) M = __popcll(__ballot(lane < c && xl > p_nc));
+      else
+        for (int b = 0; b < c; b += kWave) M += __popcll(__ballot(b + lane < c && pq(b + lane) > p_nc));
     }
     // top-k, min-p, top-p (sampler.zig:106-126): each keeps a prefix
     const int Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
@@ -585,29 +591,55 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
     if (P.min_p > 0.0f) {
       const float thr = (1.0f / S) * P.min_p;  // probs[indices[0]] = 1 / S: the row maximum has e = 1
       int cnt = 0;
-      for (int b = 0; b < M; b += kWave) cnt += __popcll(__ballot(b + lane < M && pq(b + lane) >= thr));
+      if (M <= kWave) cnt = __popcll(__ballot(lane < M && xl >= thr));
+      else
+        for (int b = 0; b < M; b += kWave) cnt += __popcll(__ballot(b + lane < M && pq(b + lane) >= thr));
       if (cnt < M) Km = cnt;
       else if (M < n && thr > p_nc) Km = M;
     }
     int K = min(Kk, Km);
     bool undecided = false;
+    // acc, lane i: the running sum from 0 after term i, over the first
+    // `covered` terms (the top-p chain and the total add the same terms in
+    // the same order from 0, so the total is a value of the same chain)
+    float acc = 0.0f;
+    int covered = 0;
     if (P.top_p > 0.0f && P.top_p < 1.0f) {
       const int lim = min(K, M);
       int st;
-      wave_seq_list<false>(0.0f, lim, P.top_p, st, pq);
+      if (lim <= kWave) {
+        acc = wave_chain_lanes<false>(0.0f, xl, lim);
+        covered = lim;
+        const uint64_t hits = __ballot(lane < lim && acc > P.top_p);
+        st = hits != 0ull ? __ffsll((long long)hits) - 1 : -1;
+      } else {
+        wave_seq_list<false>(0.0f, lim, P.top_p, st, pq);
+      }
       if (st >= 0) K = min(K, st);
       else if (K > M) undecided = true;
     }
     if (K > M) undecided = true;
     if (!undecided) {
-      // total and draw (sampler.zig:156-168)
+      // total and draw (sampler.zig:156-168); K <= M <= c here
       int st;
-      const float total = wave_seq_list<false>(0.0f, K, -1.0f, st, pq);
+      float total;
+      if (K <= kWave) {
+        if (covered < K) acc = wave_chain_lanes<false>(0.0f, xl, K);
+        total = K > 0 ? readlane_f32(acc, K - 1) : 0.0f;
+      } else {
+        total = wave_seq_list<false>(0.0f, K, -1.0f, st, pq);
+      }
       const uint32_t tok0 = (uint32_t)srt[0];
       uint32_t token = tok0, consumed = 0;
       if (total > 0.0f) {
         consumed = 1;
-        wave_seq_list<true>(u_row * total, K, -1.0f, st, pq);
+        if (K <= kWave) {
+          const float r = wave_chain_lanes<true>(u_row * total, xl, K);
+          const uint64_t hits = __ballot(lane < K && r <= 0.0f);
+          st = hits != 0ull ? __ffsll((long long)hits) - 1 : -1;
+        } else {
+          wave_seq_list<true>(u_row * total, K, -1.0f, st, pq);
+        }
         if (st >= 0) token = (uint32_t)srt[st];
       }
       if (Q.kept_ids || Q.kept_probs) {
