@@ -563,7 +563,12 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
     for (int i = lane; i < c; i += kWave) {
       const uint64_t ki = key[i];
       uint32_t r = 0;
-      for (int j = j0; j < j1; ++j) r += key[j] < ki ? 1u : 0u;
+      int j = j0;
+      for (; j + 4 <= j1; j += 4) {  // four LDS reads in flight
+        const uint64_t a0 = key[j], a1 = key[j + 1], a2 = key[j + 2], a3 = key[j + 3];
+        r += (a0 < ki ? 1u : 0u) + (a1 < ki ? 1u : 0u) + (a2 < ki ? 1u : 0u) + (a3 < ki ? 1u : 0u);
+      }
+      for (; j < j1; ++j) r += key[j] < ki ? 1u : 0u;
       if (r != 0u) atomicAdd(&rank[i], r);
     }
   }
@@ -670,8 +675,11 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
 // candidate list in Q.cand (cc entries), or, for a row k_stats could not
 // certify, from the streaming normaliser.  Every thread of the workgroup
 // calls it; `sh` may alias the caller's shared memory once all of it is read.
+// pre_ok: thread 64 + i holds candidate i in cand_pre for i < cand_n0, and
+// cc_in <= 448 (the later ones are read here).
 __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q, SampleShared& sh, float m,
-                                           float S, uint32_t cc_in, bool uncertified, float u_row) {
+                                           float S, uint32_t cc_in, bool uncertified, float u_row, bool pre_ok,
+                                           uint64_t cand_pre, uint32_t cand_n0) {
   int bank = 0;
   const int row = blockIdx.x;
   const int t = (int)threadIdx.x;
@@ -687,8 +695,13 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
     path |= kPathNormFallback;
   } else {
     const int c = cc_in > (uint32_t)kCap ? kCap : (int)cc_in;
-    const uint64_t* gc = Q.cand + (int64_t)row * kCap;
-    for (int i = t; i < c; i += kNT) sh.cand[i] = gc[i];
+    if (pre_ok) {
+      const int i = t - kWave;
+      if (t >= kWave && i < c) sh.cand[i] = i < (int)cand_n0 ? cand_pre : Q.cand[(int64_t)row * kCap + i];
+    } else {
+      const uint64_t* gc = Q.cand + (int64_t)row * kCap;
+      for (int i = t; i < c; i += kNT) sh.cand[i] = gc[i];
+    }
     if (t == 0) sh.cand_count = cc_in;
   }
   uint32_t token = 0, consumed = 0;

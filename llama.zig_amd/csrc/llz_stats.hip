@@ -113,74 +113,86 @@ __device__ __forceinline__ float4 exact_terms4(float4 v, float m, float T, bool 
   return make_float4(exp_f32(x0), exp_f32(x1), exp_f32(x2), exp_f32(x3));
 }
 
-// Exact terms of this wave's EXACT slots (loaded and waited for), their
-// candidates (once per segment), and the per-lane inclusive prefix tables of
-// the roundings on grids sj .. sj + sng - 1 with the lanes holding a tie.
-// The row's first segment (slot 0 of the first round) needs no tables: the
-// caller sums it term by term.
-__device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
-                                               int nslot, int n, float m, float theta, bool t1, bool first_round) {
+// The exact terms of EXACT slot `slot` (loaded and waited for) into its dump
+// area, and its candidates (once per segment).
+__device__ __forceinline__ void slot_terms(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int slot,
+                                           int n, float m, float theta, bool t1) {
   const int lane = lane_id();
-  for (int slot = w; slot < nslot; slot += W) {
-    const int seg = F.slotseg[slot];
-    const bool pred = F.sflag[seg] == EXACT_PRED;
-    float4* p = reinterpret_cast<float4*>(&F.u.x.dump[slot][lane * 4]);
-    const int pos = seg * SEG + lane * 4;
-    float4 e = exact_terms4(*p, m, P.temperature, t1);
-    e.x = pos + 0 < n ? e.x : 0.0f;
-    e.y = pos + 1 < n ? e.y : 0.0f;
-    e.z = pos + 2 < n ? e.z : 0.0f;
-    e.w = pos + 3 < n ? e.w : 0.0f;
-    *p = e;
-    // candidates (absent positions hold 0 < theta)
-    const bool cand_any = e.x >= theta || e.y >= theta || e.z >= theta || e.w >= theta;
-    if (__ballot(pred && cand_any) != 0ull) {
-      const float es[4] = {e.x, e.y, e.z, e.w};
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (pred && es[c] >= theta) push_cand(F, Q, row, es[c], (uint32_t)(pos + c));
-    }
-    if (pred && lane == 0) F.sflag[seg] = EXACT_DONE;  // a later round must not collect them again
-    if (first_round && slot == 0) continue;
-    const int J0 = F.sj[seg];
-    const int ng = F.sng[seg];
+  const int seg = F.slotseg[slot];
+  const bool pred = F.sflag[seg] == EXACT_PRED;
+  float4* p = reinterpret_cast<float4*>(&F.u.x.dump[slot][lane * 4]);
+  const int pos = seg * SEG + lane * 4;
+  float4 e = exact_terms4(*p, m, P.temperature, t1);
+  e.x = pos + 0 < n ? e.x : 0.0f;
+  e.y = pos + 1 < n ? e.y : 0.0f;
+  e.z = pos + 2 < n ? e.z : 0.0f;
+  e.w = pos + 3 < n ? e.w : 0.0f;
+  *p = e;
+  // candidates (absent positions hold 0 < theta)
+  const bool cand_any = e.x >= theta || e.y >= theta || e.z >= theta || e.w >= theta;
+  if (__ballot(pred && cand_any) != 0ull) {
     const float es[4] = {e.x, e.y, e.z, e.w};
-    // grids J0 and J0 + 1 (the common case: a segment crossing one binade
-    // boundary) in one pass; further grids one at a time
-    {
-      uint32_t sa = 0, sb = 0;
-      bool ta = false, tb = false;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        bool tie;
-        sa = sat_add(sa, grid_round(es[c], J0, tie), kSat);
-        ta = ta || tie;
-        sb = sat_add(sb, grid_round(es[c], J0 + 1, tie), kSat);
-        tb = tb || tie;
-      }
-      const uint32_t pa = wave_incl_scan_sat(sa, kSat);
-      const uint32_t pb = wave_incl_scan_sat(sb, kSat);
-      const uint64_t ma = __ballot(ta), mb = __ballot(tb);
-      F.u.x.pref[slot][0][lane] = pa;
-      F.u.x.pref[slot][1][lane] = pb;  // NG >= 2: room even when ng == 1
-      if (lane == 0) {
-        F.u.x.tmask[slot][0] = ma;
-        F.u.x.tmask[slot][1] = mb;
-      }
-    }
-    for (int kk = 2; kk < ng; ++kk) {
-      uint32_t sum = 0;
-      bool tie_any = false;
+    for (int c = 0; c < 4; ++c)
+      if (pred && es[c] >= theta) push_cand(F, Q, row, es[c], (uint32_t)(pos + c));
+  }
+  if (pred && lane == 0) F.sflag[seg] = EXACT_DONE;  // a later round must not collect them again
+}
+
+// The per-lane inclusive prefix tables of slot `slot`'s exact terms rounded
+// on grids sj .. sj + sng - 1, with the lanes holding a tie: grids J0 and
+// J0 + 1 (the common case: a segment crossing one binade boundary) in one
+// pass, further grids one at a time.
+__device__ __forceinline__ void slot_tables(FastShared& F, int slot) {
+  const int lane = lane_id();
+  const int seg = F.slotseg[slot];
+  const float4 e = *reinterpret_cast<const float4*>(&F.u.x.dump[slot][lane * 4]);
+  const float es[4] = {e.x, e.y, e.z, e.w};
+  const int J0 = F.sj[seg];
+  const int ng = F.sng[seg];
+  {
+    uint32_t sa = 0, sb = 0;
+    bool ta = false, tb = false;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        bool tie;
-        sum = sat_add(sum, grid_round(es[c], J0 + kk, tie), kSat);
-        tie_any = tie_any || tie;
-      }
-      F.u.x.pref[slot][kk][lane] = wave_incl_scan_sat(sum, kSat);
-      const uint64_t tm = __ballot(tie_any);
-      if (lane == 0) F.u.x.tmask[slot][kk] = tm;
+    for (int c = 0; c < 4; ++c) {
+      bool tie;
+      sa = sat_add(sa, grid_round(es[c], J0, tie), kSat);
+      ta = ta || tie;
+      sb = sat_add(sb, grid_round(es[c], J0 + 1, tie), kSat);
+      tb = tb || tie;
     }
+    const uint32_t pa = wave_incl_scan_sat(sa, kSat);
+    const uint32_t pb = wave_incl_scan_sat(sb, kSat);
+    const uint64_t ma = __ballot(ta), mb = __ballot(tb);
+    F.u.x.pref[slot][0][lane] = pa;
+    F.u.x.pref[slot][1][lane] = pb;  // NG >= 2: room even when ng == 1
+    if (lane == 0) {
+      F.u.x.tmask[slot][0] = ma;
+      F.u.x.tmask[slot][1] = mb;
+    }
+  }
+  for (int kk = 2; kk < ng; ++kk) {
+    uint32_t sum = 0;
+    bool tie_any = false;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      bool tie;
+      sum = sat_add(sum, grid_round(es[c], J0 + kk, tie), kSat);
+      tie_any = tie_any || tie;
+    }
+    F.u.x.pref[slot][kk][lane] = wave_incl_scan_sat(sum, kSat);
+    const uint64_t tm = __ballot(tie_any);
+    if (lane == 0) F.u.x.tmask[slot][kk] = tm;
+  }
+}
+
+// Rounds after the first: the terms and tables of this wave's slots (slot s
+// on wave s % W, all loaded by this wave and waited for).
+__device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
+                                               int nslot, int n, float m, float theta, bool t1) {
+  for (int slot = w; slot < nslot; slot += W) {
+    slot_terms(F, Q, P, row, slot, n, m, theta, t1);
+    slot_tables(F, slot);
   }
 }
 
@@ -630,6 +642,9 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   bool certified = true;
   float S = __builtin_nanf("");
   uint32_t cc = 0;
+  bool pre_ok = false;     // candidates 0 .. cand_n0 - 1 are in cand_pre (read during the walk)
+  uint64_t cand_pre = 0;
+  uint32_t cand_n0 = 0;
   if (!nan_sum) {
     const float aw = fmaf(m, -l2e_t, cw);
     const float Rw = __builtin_amdgcn_exp2f(aw);  // q * Rw ~ e = exp((v - m) / T)
@@ -852,7 +867,13 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the EXACT slots' re-reads (and phase S's stores)
       const int qn0 = (int)readlane_u32(ccnt, 0);
       reread(qn0);
-      exact_segments(F, Q, P, row, w, min(F.nslot, DCAP), n, m, theta, t1, true);
+      // this wave's EXACT slots (slot s on wave s % W, loaded by this wave),
+      // while the re-reads land; slot 0, the row's first segment, needs no
+      // tables: wave 0 sums it term by term
+      for (int slot = w; slot < min(F.nslot, DCAP); slot += W) {
+        slot_terms(F, Q, P, row, slot, n, m, theta, t1);
+        if (slot != 0) slot_tables(F, slot);
+      }
       if (w == 0) {
         // the row's first segment (slot 0) from 0, term by term as
         // sampler.zig:87 adds them: every lane runs the same chain over LDS
@@ -930,6 +951,12 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     }
     __syncthreads();
 
+    // waves 1.. read the candidate list while wave 0 walks, one entry per
+    // thread from thread 64 on (entries a later round collects are read at
+    // the hand-over)
+    cand_n0 = F.ncand;
+    if (w > 0 && t - kWave < (int)min(cand_n0, (uint32_t)kCandCap))
+      cand_pre = Q.cand[(int64_t)row * kCandCap + (t - kWave)];
     // ---- phase C: the walk over the entries in index order (wave 0); EXACT
     // segments beyond the slots in further rounds
     for (int round = 0; !F.fail; ++round) {
@@ -954,7 +981,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         const int nslot = F.nslot;
         exact_loads<FASTLD>(F, xr, w, nslot, n);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1, false);
+        exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
         __syncthreads();
       }
       if (w == 0) {
@@ -1057,11 +1084,13 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     certified = F.fail == 0u;
     S = F.s_run;
     cc = flood ? (uint32_t)kCandCap + 1u : F.ncand;
+    pre_ok = !flood && cc <= (uint32_t)(NT - kWave);
   }
 
   // ---- the selection stage, on the same workgroup and shared memory
   __syncthreads();  // F is read: the selection reuses the memory
-  select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified, u_row);
+  select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified, u_row, certified && pre_ok,
+             cand_pre, cand_n0);
 }
 
 }  // namespace
