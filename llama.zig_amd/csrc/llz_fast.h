@@ -64,6 +64,7 @@ constexpr int KL = 18;              // LDS-resident segments per wave
 constexpr int SPWMAX = KV + KL;     // segments per wave at most (<= 64: one lane each)
 constexpr int GMAX = W * SPWMAX;    // 504 segments = 129024 logits
 constexpr int QCAP = 128;           // special queue capacity per wave (flushed when full)
+constexpr int kLoadWindow = 8;     // phase L: segment loads in flight per wave
 constexpr int DCAP = 48;            // EXACT segments evaluated per round
 constexpr int NG = 6;               // grids tabulated per EXACT segment at most
 constexpr float DELTA = 0x1p-10f;   // relative margin of the binade prediction
@@ -159,6 +160,33 @@ __device__ __forceinline__ void dma16(const float* gaddr, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_base) : "m0", "memory");
 }
 
+// The same from a buffer resource (address as in buf_ld4): reads past the
+// resource's byte count write zeros.  Non-temporal.
+__device__ __forceinline__ void dma_buf16(llz_i4v rsrc, int voffset, int soffset, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, %3 offen nt lds" ::"v"(voffset), "s"(rsrc), "s"(lds_base),
+               "s"(soffset)
+               : "m0", "memory");
+}
+
+// v_writelane: old with lane `lane` (uniform) replaced by src (uniform).
+__device__ int llz_writelane_i32(int src, int lane, int old) __asm("llvm.amdgcn.writelane.i32");
+
+// max(a, b, c) of the values as they are: in IEEE mode a quiet NaN operand
+// is skipped, a signalling one makes the result NaN (the compiler's fmaxf
+// quiets every operand first, one more instruction each).
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// Wait until at most N vector memory loads of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void lds_dma_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt holds 0 .. 63");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 __device__ __forceinline__ float4 buf_ld4(llz_i4v rsrc, int voffset, int soffset) {
   const llz_i4v v = llz_raw_buffer_load_v4i32(rsrc, voffset, soffset, 2);
   return make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
@@ -188,7 +216,8 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return __uint_as_float(lane_readlast(r));
 }
 
-// A wave's total of v in lane 63 only, in six folded DPP additions (row
+// A wave's total of v in lane 63 only (wave_fold_f32; wave_total_f32 reads
+// it into a scalar register), in six folded DPP additions (row
 // sums, then rows 0-1 and 2-3, then all four; the other lanes end with
 // partial sums).  The order of the additions differs from a lane-order
 // scan: for estimates only.
@@ -198,7 +227,7 @@ __device__ __forceinline__ float dpp_add_f32(float s) {
   // DPP instruction
   return s + __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-0.0f), __float_as_int(s), CTRL, 0xf, 0xf, true));
 }
-__device__ __forceinline__ float wave_total_f32(float v) {
+__device__ __forceinline__ float wave_fold_f32(float v) {
   float s = v;
   s = dpp_add_f32<0x111>(s);  // row_shr:1
   s = dpp_add_f32<0x112>(s);  // row_shr:2
@@ -206,7 +235,10 @@ __device__ __forceinline__ float wave_total_f32(float v) {
   s = dpp_add_f32<0x118>(s);  // row_shr:8: lane 15 of each row holds its row's sum
   s = dpp_add_f32<0x142>(s);  // row_bcast:15: lane 63 holds rows 2 + 3
   s = dpp_add_f32<0x143>(s);  // row_bcast:31: lane 63 holds all four rows
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
+  return s;
+}
+__device__ __forceinline__ float wave_total_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_fold_f32(v)), 63));
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {

@@ -498,110 +498,114 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   const int base_w = w * SEG + lane * 4;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
 
-  // ---- phase L: every load in flight, then per segment as it lands: running
-  // maximum, the estimate q (stored over v) and the segment sum of q
-  // Every load is issued unconditionally and fully unrolled (a guarded load
-  // is sunk into its guard and waited for on its own): segments this wave
-  // does not own read a valid address and are masked to -inf.
+  // ---- phase L: per segment as it lands: running maximum, the estimate q
+  // (stored over v) and the segment sum of q (lane 63 stores it)
   float4 d[KV];
-  if constexpr (FASTLD) {
-    // LDS-resident segments straight to LDS (full ones; the partial last
-    // segment and absent ones read the row start and are redone or unused)
-#pragma unroll
-    for (int k = KV; k < SPWMAX; ++k) {
-      int kk = k;
-      asm volatile("" : "+s"(kk));
-      const bool full = kk < nseg_w && (w + W * kk + 1) * SEG <= n;
-      dma16(xr + (full ? base_w + kk * (W * SEG) : lane * 4),
-            (uint32_t)__builtin_amdgcn_readfirstlane((int)(uintptr_t)&F.u.data[w][k - KV][0]));
-    }
-    // register segments: one shared lane offset, the segment offset in an
-    // SGPR; reads past the row return 0
-    const llz_i4v rs = row_rsrc(xr, (uint32_t)n * 4u);
-    const int soff = __builtin_amdgcn_readfirstlane(w * SEG * 4);
-#pragma unroll
-    for (int k = 0; k < KV; ++k) {
-      d[k] = buf_ld4(rs, lane * 16, soff + k * (W * SEG * 4));
-      __builtin_amdgcn_sched_barrier(0);  // keep the issue order: segment k lands k-th
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < KV; ++k) d[k] = ld1x4(xr, base_w + k * (W * SEG), k < nseg_w ? n : 0);
-    for (int k = KV; k < nseg_w; ++k) seg_to_lds(xr, w + W * k, n, false, &F.u.data[w][k - KV][0]);
-  }
-  __builtin_amdgcn_sched_barrier(0);  // every load in flight before any use
-
   float mx = -kInfS, cw = 0.0f;
   uint32_t nanf = 0;
-  // bounds as (lane offset, VGPR) < (scalar limit of the segment); the
-  // limits are recomputed in place (an empty asm keeps the compiler from
-  // hoisting 45 of them into live registers)
   const int lane4 = lane * 4;
   const int lim_w = nseg_w > 0 ? n - w * SEG : 0;  // segment k holds positions lane4 < lim_w - k W SEG
+  // bounds as (lane offset, VGPR) < (scalar limit of the segment); the
+  // limits are recomputed in place (an empty asm keeps the compiler from
+  // hoisting them all into live registers)
   auto seg_lim = [&](int k) {
     int l = k < nseg_w ? lim_w - k * (W * SEG) : 0;
     asm volatile("" : "+s"(l));
     return l;
   };
-  // LDS-resident segments of a 16-byte-load row first: their loads were
-  // issued first, so they land first and are processed while the register
-  // loads are still in flight (a wait for just those: the register loads are
-  // the KV most recent)
-  auto lds_segments = [&]() {
+  // one segment's estimate: positions outside the row or the wave's segments
+  // get an infinite offset, so q = 0, and no part in the maximum.  The
+  // maximum takes the logits as they are (max3_raw: a signalling NaN makes it
+  // NaN; its segment sum is NaN too, and phase M redoes such a row's maximum)
+  auto seg_q = [&](const int k, float4 v) {
+    const bool ok = lane4 < seg_lim(k);
+    const float ck = ok ? cw : kInfS;
+    const float m = max3_raw(max3_raw(mx, v.x, v.y), v.z, v.w);
+    mx = ok ? m : mx;
+    return q_of(v, l2e_t, ck);
+  };
+  // segment sums: lane k of my_a holds segment k's (stored after the loop)
+  float my_a = 0.0f;
+  auto seg_sum = [&](const int k, float4 q) {
+    const float a = wave_fold_f32((q.x + q.y) + (q.z + q.w));
+    my_a = __int_as_float(llz_writelane_i32(__builtin_amdgcn_readlane(__float_as_int(a), kWave - 1), k, __float_as_int(my_a)));
+  };
+  auto set_cw = [&](float mr) {
+    // any finite reference of this wave: |m - mr| is checked in phase M
+    if (!(fabsf(mr) <= 3.0e38f)) mr = 0.0f;
+    cw = mr * l2e_t;
+  };
+  if constexpr (FASTLD) {
+    // A window of kLoadWindow loads in flight per wave, one issued as each
+    // segment is done: each CU's share of HBM arrives spread over the whole
+    // read, and each segment's work overlaps the loads behind it (with every
+    // load issued at once, a CU's data lands in one burst and the work
+    // follows it).  Issue order = processing order: the LDS-resident segments
+    // KV .. SPWMAX - 1 first (straight to LDS), then the register segments
+    // 0 .. KV - 1.  Every slot issues exactly one load (reads past the row
+    // return zeros), so the wait for slot i counts the loads behind it.
+    const llz_i4v rs = row_rsrc(xr, (uint32_t)n * 4u);
+    const int soff = __builtin_amdgcn_readfirstlane(w * SEG * 4);
+    const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uintptr_t)&F.u.data[w][0][0]);
+    auto issue = [&](const int i) {
+      if (i < KL)
+        dma_buf16(rs, lane * 16, soff + (KV + i) * (W * SEG * 4), lds0 + (uint32_t)(i * SEG * 4));
+      else
+        d[i - KL] = buf_ld4(rs, lane * 16, soff + (i - KL) * (W * SEG * 4));
+      __builtin_amdgcn_sched_barrier(0);  // keep the issue order
+    };
+    static_assert(kLoadWindow >= 1 && kLoadWindow <= KV, "a full window behind every LDS-resident segment");
+#pragma unroll
+    for (int i = 0; i < kLoadWindow; ++i) issue(i);
+#pragma unroll
+    for (int i = 0; i < SPWMAX; ++i) {
+      if (i < KL) {
+        const int k = KV + i;
+        if (k < nseg_w) {
+          lds_dma_wait<kLoadWindow - 1>();  // the window's loads behind it (the register ones come later)
+          float4* p = reinterpret_cast<float4*>(&F.u.data[w][i][lane * 4]);
+          const float4 v = *p;
+          if (i == 0) set_cw(wave_max_f32(lane4 < seg_lim(k) ? max4(v) : -kInfS));  // the first segment processed
+          const float4 q = seg_q(k, v);
+          *p = q;
+          seg_sum(k, q);
+        }
+      } else {
+        const int k = i - KL;
+        if (k == 0 && nseg_w <= KV) set_cw(wave_max_f32(lane4 < seg_lim(0) ? max4(d[0]) : -kInfS));
+        float4 q = seg_q(k, d[k]);  // a NaN logit makes its segment sum NaN
+        // materialise q here, while the loads land (not sunk into phase S)
+        asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
+        d[k] = q;
+        seg_sum(k, q);
+      }
+      if (i + kLoadWindow < SPWMAX) issue(i + kLoadWindow);
+      __builtin_amdgcn_sched_barrier(0);  // one segment at a time: bounded live ranges
+    }
+  } else {
+    // element loads, all in flight at once (guarded loads are waited for
+    // where they are read)
+#pragma unroll
+    for (int k = 0; k < KV; ++k) d[k] = ld1x4(xr, base_w + k * (W * SEG), k < nseg_w ? n : 0);
+    for (int k = KV; k < nseg_w; ++k) seg_to_lds(xr, w + W * k, n, false, &F.u.data[w][k - KV][0]);
+    __builtin_amdgcn_sched_barrier(0);
+    set_cw(wave_max_f32(lane4 < seg_lim(0) ? max4(d[0]) : -kInfS));
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      float4 q = seg_q(k, d[k]);
+      asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
+      d[k] = q;
+      seg_sum(k, q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     for (int k = KV; k < nseg_w; ++k) {
       float4* p = reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]);
-      const float4 v = *p;
-      mx = fmaxf(mx, max4(v));
-      const float4 q = q_of(v, l2e_t, cw);
+      const float4 q = seg_q(k, *p);
       *p = q;
-      const float a = wave_total_f32((q.x + q.y) + (q.z + q.w));
-      if (lane == 0) F.v.aseg[w + W * k] = a;
-      nanf |= a != a ? 1u : 0u;
+      seg_sum(k, q);
     }
-  };
-  const bool lds_first = FASTLD && nseg_w > KV;
-  float mr;
-  if (lds_first) {
-    static_assert(KV == 45, "the wait below counts KV register loads");
-    asm volatile("s_waitcnt vmcnt(45)" ::: "memory");
-    if ((w + W * (nseg_w - 1) + 1) * SEG > n) {  // the row's partial last segment
-      const int k = nseg_w - 1;
-      *reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]) = ld4(xr, base_w + k * (W * SEG), n);
-    }
-    // any finite reference of this wave: |m - mr| is checked in phase M
-    mr = wave_max_f32(max4(*reinterpret_cast<const float4*>(&F.u.data[w][0][lane * 4])));
-  } else {
-    const bool ok0 = lane4 < seg_lim(0);
-    mr = wave_max_f32(ok0 ? max4(d[0]) : -kInfS);
   }
-  if (!(fabsf(mr) <= 3.0e38f)) mr = 0.0f;
-  cw = mr * l2e_t;
-  if (lds_first) lds_segments();
-  // segment sums are kept one per lane (lane k: segment k) and stored after
-  // the loop
-  float my_a = 0.0f;
-#pragma unroll
-  for (int k = 0; k < KV; ++k) {
-    const float4 v = d[k];
-    const bool ok = lane4 < seg_lim(k);  // this wave's and inside the row
-    float m4 = max4(v);
-    asm volatile("" : "+v"(m4));  // a select, not a branch around max4
-    mx = fmaxf(mx, ok ? m4 : -kInfS);
-    float4 q = q_of(v, l2e_t, cw);  // a NaN logit makes its segment sum NaN
-    q.x = ok ? q.x : 0.0f;
-    q.y = ok ? q.y : 0.0f;
-    q.z = ok ? q.z : 0.0f;
-    q.w = ok ? q.w : 0.0f;
-    // materialise q here, while the loads land (not sunk into phase S)
-    asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
-    d[k] = q;
-    const float a = wave_total_f32((q.x + q.y) + (q.z + q.w));
-    my_a = lane == k ? a : my_a;
-    __builtin_amdgcn_sched_barrier(0);  // one segment at a time: bounded live ranges
-  }
-  if (lane < min(nseg_w, KV)) F.v.aseg[w + W * lane] = my_a;
-  nanf |= (lane < min(nseg_w, KV) && my_a != my_a) ? 1u : 0u;
-  if (!lds_first && nseg_w > KV) lds_segments();  // element loads: waited for where they are read
+  if (lane < nseg_w) F.v.aseg[w + W * lane] = my_a;
   if (!fits) {  // rows the fast path does not take: maximum and NaN scan only
     for (int i = t; i < n; i += NT) {
       const float v = xr[i];
@@ -635,6 +639,30 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   for (int i = 0; i < W; ++i) {
     m = fmaxf(m, F.mw[i]);
     nanrow = nanrow || F.nanw[i] != 0u;
+  }
+  if (fits) {
+    // a NaN logit makes its segment's sum of q NaN (q >= 0 otherwise, so
+    // no inf - inf)
+    bool nl = false;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      const int g = W * lane + i;
+      nl = nl || (g < G && F.v.aseg[g] != F.v.aseg[g]);
+    }
+    if (__ballot(nl) != 0ull) {
+      // a NaN logit: phase L's maximum did not quiet signalling NaNs, so the
+      // row's maximum is taken again (sampler.zig:80-81: NaNs are skipped)
+      nanrow = true;
+      float mm = -kInfS;
+      for (int i = t; i < n; i += NT) mm = fmaxf(mm, xr[i]);
+      mm = wave_max_f32(mm);
+      __syncthreads();  // every wave has read F.mw
+      if (lane == 0) F.mw[w] = mm;
+      __syncthreads();
+      m = -kInfS;
+#pragma unroll
+      for (int i = 0; i < W; ++i) m = fmaxf(m, F.mw[i]);
+    }
   }
   // a NaN logit or an infinite maximum makes the reference's sum NaN: the
   // selection handles that row without the phases below
