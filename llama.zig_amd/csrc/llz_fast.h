@@ -64,7 +64,7 @@ constexpr int KL = 18;              // LDS-resident segments per wave
 constexpr int SPWMAX = KV + KL;     // segments per wave at most (<= 64: one lane each)
 constexpr int GMAX = W * SPWMAX;    // 504 segments = 129024 logits
 constexpr int QCAP = 128;           // special queue capacity per wave (flushed when full)
-constexpr int kLoadWindow = 8;     // phase L: segment loads in flight per wave
+constexpr int kLoadWindow = 6;     // phase L: segment loads in flight per wave
 constexpr int DCAP = 48;            // EXACT segments evaluated per round
 constexpr int NG = 6;               // grids tabulated per EXACT segment at most
 constexpr float DELTA = 0x1p-10f;   // relative margin of the binade prediction

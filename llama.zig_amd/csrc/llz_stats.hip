@@ -638,17 +638,23 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
 #pragma unroll
   for (int i = 0; i < W; ++i) {
     m = fmaxf(m, F.mw[i]);
-    nanrow = nanrow || F.nanw[i] != 0u;
+    nanrow = nanrow | (F.nanw[i] != 0u);
   }
+  // the segment sums of q of round `lane` (segments W lane .. W lane + W - 1,
+  // one per wave), all read at once; absent ones are 0 (selects, not
+  // branches: each branch here would wait out an LDS read of its own)
+  float av[W];
+  const int glast = min(G, GMAX) - 1;
+#pragma unroll
+  for (int i = 0; i < W; ++i) av[i] = F.v.aseg[min(W * lane + i, glast)];
+#pragma unroll
+  for (int i = 0; i < W; ++i) av[i] = W * lane + i < G ? av[i] : 0.0f;
   if (fits) {
     // a NaN logit makes its segment's sum of q NaN (q >= 0 otherwise, so
     // no inf - inf)
     bool nl = false;
 #pragma unroll
-    for (int i = 0; i < W; ++i) {
-      const int g = W * lane + i;
-      nl = nl || (g < G && F.v.aseg[g] != F.v.aseg[g]);
-    }
+    for (int i = 0; i < W; ++i) nl = nl | (av[i] != av[i]);
     if (__ballot(nl) != 0ull) {
       // a NaN logit: phase L's maximum did not quiet signalling NaNs, so the
       // row's maximum is taken again (sampler.zig:80-81: NaNs are skipped)
@@ -685,12 +691,12 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     {
       float rtot = 0.0f, before_w = 0.0f, b_w = 0.0f;
       bool bad = false;
-  #pragma unroll
+#pragma unroll
       for (int i = 0; i < W; ++i) {
         const float awi = fmaf(m, -l2e_t, F.cw[i]);
-        bad = bad || ((G > i) && !(fabsf(awi) <= 32.0f));
-        const int g = W * lane + i;
-        const float b = g < G ? F.v.aseg[g] * __builtin_amdgcn_exp2f(awi) : 0.0f;
+        bad = bad | ((G > i) & !(fabsf(awi) <= 32.0f));
+        const float ri = __builtin_amdgcn_exp2f(awi);
+        const float b = W * lane + i < G ? av[i] * ri : 0.0f;
         rtot += b;
         before_w += i < w ? b : 0.0f;
         b_w = i == w ? b : b_w;
