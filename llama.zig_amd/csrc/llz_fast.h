@@ -101,17 +101,18 @@ struct FastShared {
   } u;
   union {
     float aseg[fastp::GMAX];                    // segment sums of q (phases L, M)
+    alignas(16) uint32_t ssum4[fastp::W * 64][4];  // PLAIN: integer sum on grid sj in four parts, plus
+                                                //   4 * 64 * MAGIC_BITS (mod 2^32) (from phase S; room
+                                                //   for every wave's 64th segment: stored unguarded)
   } v;
-  uint32_t ssum[fastp::W * 64];                 // PLAIN: integer sum on grid sj (room for every
-                                                //   wave's 64th segment: phase S stores it unguarded)
   int8_t sj[fastp::GMAX];                       // PLAIN: its binade; EXACT: first binade tabulated
   uint8_t sng[fastp::GMAX];                     // EXACT: number of binades tabulated
   uint8_t sflag[fastp::GMAX];
   int8_t sdump[fastp::GMAX];                    // EXACT: slot in `dump`, or -1
   uint8_t sbump[fastp::GMAX];                   // PLAIN_TIE: units its ties add when the segment
                                                 //   starts at an even (bits 0-3) or odd (4-7) integer
-  uint32_t qpos[fastp::W][fastp::QCAP];         // special queue: position
-  uint32_t qpre[fastp::W][fastp::QCAP];         //   and its segment's integer sum before it (lower bracket)
+  uint32_t qpos[fastp::W][fastp::QCAP];         // special queue: position (bits 0-30) and the parity of its
+                                                //   segment's integer sum before it (bit 31, lower brackets)
   int16_t slotseg[fastp::DCAP];                 // segment held by each EXACT slot
   float mw[fastp::W];
   float cw[fastp::W];
@@ -239,6 +240,29 @@ __device__ __forceinline__ float wave_fold_f32(float v) {
 }
 __device__ __forceinline__ float wave_total_f32(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_fold_f32(v)), 63));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, true);
+}
+
+// Sums of four per-lane values over each 16-lane row, transposed: lane
+// 16 r + 12 + c ends with the sum of a_c over row r (wrapping u32 adds).
+// Eleven instructions, where four wave totals take 24.
+__device__ __forceinline__ uint32_t row_sums4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
+  const int lane = lane_id();
+  const bool odd = (lane & 1) != 0, b1 = (lane & 2) != 0;
+  // lane pairs (quad_perm 1,0,3,2): the even lane ends with the pair's sum of
+  // a0 (a2), the odd lane with that of a1 (a3)
+  const uint32_t s01 = (odd ? a1 : a0) + dpp_u32<0xB1>(odd ? a0 : a1);
+  const uint32_t s23 = (odd ? a3 : a2) + dpp_u32<0xB1>(odd ? a2 : a3);
+  // quads (quad_perm 2,3,0,1): lane 4 i + c ends with the quad's sum of a_c
+  uint32_t t = (b1 ? s23 : s01) + dpp_u32<0x4E>(b1 ? s01 : s23);
+  // the row's four quads (row_shr 4, then 8)
+  t = t + dpp_u32<0x114>(t);
+  t = t + dpp_u32<0x118>(t);
+  return t;
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {

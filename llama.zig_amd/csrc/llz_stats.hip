@@ -345,9 +345,10 @@ __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slo
 // it; the terms it could not certify are evaluated with the exact exp and
 // the difference corrects the segment sum.  Candidates are collected, and
 // per segment with ties the units they add (PLAIN_TIE, sbump).  A
-// segment's lanes are always queued and settled together, so the integer
-// sum before a tie is the lane's queued prefix, plus the corrections of the
-// segment's lanes below it, plus the lane's exact roundings before it.
+// segment's lanes are always queued and settled together, so the parity of
+// the integer sum before a tie (all that decides it) is that of the lane's
+// queued prefix, plus the corrections of the segment's lanes below it, plus
+// the lane's exact roundings before it.
 __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
                                                 int qn, const float4 (&v4q)[2], float Rw, float cw, float m,
                                                 float theta, bool t1) {
@@ -363,8 +364,9 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
   for (int h = 0; h < 2; ++h) {
     const int i = h * kWave + lane;
     act2[h] = i < qn;
-    pos2[h] = act2[h] ? F.qpos[w][i] : 0u;
-    pre2[h] = act2[h] ? F.qpre[w][i] : 0u;
+    const uint32_t qp = act2[h] ? F.qpos[w][i] : 0u;
+    pos2[h] = qp & 0x7fffffffu;
+    pre2[h] = qp >> 31;  // parity: only that decides a tie
     j2[h] = F.sj[pos2[h] >> 8];
     const GridConst gc = grid_const(j2[h], Rw, theta, bw, t1);
     const uint32_t tspec = __float_as_uint(gc.tspec);
@@ -402,7 +404,7 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     corr2[h] = (rx[h][0] - rl[h][0]) + (rx[h][1] - rl[h][1]) + (rx[h][2] - rl[h][2]) + (rx[h][3] - rl[h][3]);
-    if (act2[h] && corr2[h] != 0u) atomicAdd(&F.ssum[pos2[h] >> 8], corr2[h]);
+    if (act2[h] && corr2[h] != 0u) atomicAdd(&F.v.ssum4[pos2[h] >> 8][0], corr2[h]);
   }
   if (__ballot(tiem != 0u) == 0ull) return;
 
@@ -758,20 +760,18 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int i = h * kWave + lane;
-        const int pos = i < cnt ? (int)F.qpos[w][i] : 0;
+        const int pos = i < cnt ? (int)(F.qpos[w][i] & 0x7fffffffu) : 0;
         v4q[h] = FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n);
       }
     };
     auto settle = [&](int cnt) { settle_specials(F, Q, P, row, w, cnt, v4q, Rw, cw, m, theta, t1); };
     // The queue is filled in chunks of at most qcap <= QCAP entries, each holding
     // whole batches (a segment's lanes are settled together): chunk 0 in LDS,
-    // chunks 1.. in this row's part of the fallback buffers 0 (positions) and
-    // 1 (prefixes), SPW * 64 entries per wave (a wave queues each of its lanes
-    // at most once per segment).  All are settled in phase F+X: phase S never
-    // settles.  qch: current chunk, qn: its entries, lane c of ccnt: the
-    // entries of an earlier chunk c.
+    // chunks 1.. in this row's part of fallback buffer 0, SPW * 64 entries per
+    // wave (a wave queues each of its lanes at most once per segment).  All
+    // are settled in phase F+X: phase S never settles.  qch: current chunk,
+    // qn: its entries, lane c of ccnt: the entries of an earlier chunk c.
     uint32_t* const ovp = Q.fb + (int64_t)row * n + (int64_t)w * SPW * kWave;
-    uint32_t* const ovq = ovp + (int64_t)P.rows * n;
     const int qcap = (P.qcap > 0u && P.qcap < (uint32_t)QCAP) ? (int)P.qcap : QCAP;  // entries per chunk
     int qch = 0;
     uint32_t ccnt = 0;
@@ -791,11 +791,11 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       // One batch: four segments k0 .. k0 + 3 (k0 a constant).  Per lane and
       // segment, the lower and upper bracket roundings of its four terms
       // (bit patterns of MAGIC + rounding); the lane is special when the
-      // sums differ or a term reaches tspec.  Sums are scanned with the
-      // MAGIC offsets in (wrapping; the true values are far below 2^32) and
-      // the offsets taken out where a sum is used.
+      // sums differ or a term reaches tspec.  Sums keep the MAGIC offsets
+      // (wrapping; the true values are far below 2^32), taken out where a
+      // sum is used.
       auto batch = [&](const int k0, const llz_f4v qa, const llz_f4v qb, const llz_f4v qc, const llz_f4v qd) {
-        uint32_t raw4[4], incl4[4], sl = 0;
+        uint32_t raw4[4], sl = 0;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const int kl = min(k0 + s, kWave - 1);
@@ -823,16 +823,21 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           // theta is +inf in flood mode)
           sl |= (hsum != lsum || hmax >= tspec) ? (1u << s) : 0u;
         }
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          incl4[s] = wave_incl_scan_op(raw4[s], 0u, [](uint32_t a, uint32_t b) { return a + b; });
-        // segment totals (lane 63 holds them; the MAGIC offsets of 256 terms
-        // taken out).  Every wave has room for 64 segments: absent ones store 0
-        if (lane == kWave - 1) {
-#pragma unroll
-          for (int s = 0; s < 4; ++s) F.ssum[w + W * (k0 + s)] = incl4[s] - (uint32_t)(kWave * 4) * MAGIC_BITS;
-        }
+        // segment sums in four parts, one per 16-lane row (lane 16 r + 12 + s
+        // holds row r's part of segment k0 + s).  Every wave has room for 64
+        // segments: absent ones store MAGIC offsets only
+        const uint32_t rsum = row_sums4(raw4[0], raw4[1], raw4[2], raw4[3]);
+        if ((lane & 12) == 12) F.v.ssum4[w + W * (k0 + (lane & 3))][lane >> 4] = rsum;
         if (__ballot(sl != 0u) != 0ull) {
+          // a tie is decided by the parity of the integer before it: per
+          // segment, that of the lower bracket sum of the lanes below (the
+          // offsets, 4 MAGIC_BITS a lane, are even)
+          uint32_t par4[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const uint64_t pm = __ballot((raw4[s] & 1u) != 0u);
+            par4[s] = __builtin_amdgcn_mbcnt_hi((uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u)) << 31;
+          }
           // every lane appends its entries after those of the lanes below it
           const uint32_t my = (uint32_t)__popc(sl);
           const uint32_t incl = wave_incl_scan_op(my, 0u, [](uint32_t a, uint32_t b) { return a + b; });
@@ -849,21 +854,15 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
               if (qch * qcap > SPW * kWave || qch >= kWave) qovf = true;
             }
             int slot = qn + (int)(incl - my);
-            const uint32_t below = (uint32_t)(lane * 4) * MAGIC_BITS;  // offsets of the lanes below
             uint32_t* const op = ovp + (qch - 1) * qcap;
-            uint32_t* const oq = ovq + (qch - 1) * qcap;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
               if (sl & (1u << s)) {
-                const uint32_t pos = (uint32_t)((w + W * (k0 + s)) * SEG + lane4);
-                const uint32_t pre = incl4[s] - raw4[s] - below;
-                if (qch == 0) {
-                  F.qpos[w][slot] = pos;
-                  F.qpre[w][slot] = pre;
-                } else if (!qovf) {
-                  op[slot] = pos;
-                  oq[slot] = pre;
-                }
+                const uint32_t qp = (uint32_t)((w + W * (k0 + s)) * SEG + lane4) | par4[s];
+                if (qch == 0)
+                  F.qpos[w][slot] = qp;
+                else if (!qovf)
+                  op[slot] = qp;
                 ++slot;
               }
             }
@@ -931,10 +930,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       // the chunks past the LDS queue (rare)
       for (int c = 1; c <= qch; ++c) {
         const int cn = (int)readlane_u32(ccnt, c);
-        for (int i = lane; i < cn; i += kWave) {
-          F.qpos[w][i] = ovp[(c - 1) * qcap + i];
-          F.qpre[w][i] = ovq[(c - 1) * qcap + i];
-        }
+        for (int i = lane; i < cn; i += kWave) F.qpos[w][i] = ovp[(c - 1) * qcap + i];
         reread(cn);
         settle(cn);
       }
@@ -951,7 +947,11 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       const bool in = g < G;
       const uint32_t fl = in ? F.sflag[g] : (uint32_t)EXACT_PRED;
       const int jj = in ? F.sj[g] : 0;
-      const uint32_t sm = in ? min(F.ssum[g], kSat) : 0u;
+      uint32_t sm = 0u;
+      if (in) {
+        const uint4 p4 = *reinterpret_cast<const uint4*>(&F.v.ssum4[g][0]);
+        sm = min(p4.x + p4.y + p4.z + p4.w - (uint32_t)(kWave * 4) * MAGIC_BITS, kSat);
+      }
       const bool plain = in && fl == PLAIN;
       const uint32_t key = plain ? (0x10000u | (uint32_t)(jj & 0xffff)) : 0u;
       const bool head = in && !(plain && wave_shift_up1(key) == key);
