@@ -251,6 +251,16 @@ __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slo
   uint32_t N = N_io;
   int j = j_io;
   int p = 0;  // first lane not consumed
+  if (j == J0 + 1 && ng >= 2) {
+    // the sum crossed into the segment's second grid before it (a segment
+    // with no event there adds the table's total)
+    const uint32_t T1 = readlane_u32(X.pv1, kWave - 1);
+    const uint64_t tm1 = ((uint64_t)uni_u(X.tm1h) << 32) | uni_u(X.tm1l);
+    if (tm1 == 0ull && T1 < kSat && N + T1 < kGridTop) {
+      N_io = N + T1;
+      return;
+    }
+  }
   if (j == J0) {
     // the common case, short on dependent steps (a wave running alone waits
     // out each one): every lane replays its own four terms from the table's
@@ -1026,10 +1036,15 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         int e = F.next_e;
         const int ne = F.ne;
         bool fail = false, more = false;
-        // windows of 64 entries, one per lane; in each, the runs before an
-        // EXACT entry are added as one difference of a prefix sum over the
-        // window, and the next EXACT entry's slot data is read while this one
-        // is resolved
+        // windows of 64 entries, one per lane.  What does not depend on the
+        // running sum is computed for every lane at once: for an EXACT lane x,
+        // its slot, grids and the stretch of runs (and PLAIN_TIE segments)
+        // between the previous EXACT entry and x: the stretch's sum (a
+        // difference of a prefix sum), its grid, and whether it can be added
+        // in one step (no tie, one grid).  The walk then takes the EXACT
+        // entries in order, reading ahead the next one's slot data while it
+        // resolves this one.
+        constexpr uint32_t XI_CLEAN = 1u << 27, XI_EMPTY = 1u << 28;
         for (int held = e & ~(kWave - 1); held < ne && !fail && !more; held += kWave) {
           const bool ok = held + lane < ne;
           const uint32_t ea = ok ? F.u.x.ent_a[held + lane] : 0u;
@@ -1042,45 +1057,53 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           const uint32_t psum =
               wave_incl_scan_op(ok && !isx ? eb : 0u, 0u, [](uint32_t a, uint32_t b) { return a + b; });
           const int wend = min(ne - held, kWave);
-          auto slot_at = [&](int x) {
-            int sl = (int)(int8_t)(readlane_u32(eb, x) & 0xffu);
-            if (round > 0) sl = F.sdump[(readlane_u32(ea, x) >> 2) & 1023u];  // slots were reassigned
-            return __builtin_amdgcn_readfirstlane(sl);
-          };
-          auto next_x = [&](int from) {  // first EXACT entry at or after `from` (wend: none)
-            const uint64_t r = from < kWave ? exm & (~0ull << from) : 0ull;
-            return r != 0ull ? __ffsll((long long)r) - 1 : wend;
-          };
+          const int ejp = (int)wave_shift_up1((uint32_t)ej);  // the entry before's grid
+          // entries whose grid differs from the entry before (neither EXACT)
+          const uint64_t chg = __ballot(ok && !isx && lane > 0 && ej != ejp) & ~(exm << 1);
+          // the stretch ending at this lane: entries pv + 1 .. lane - 1
+          const uint64_t xb = exm & lt_mask;
+          const int pv = xb != 0ull ? 63 - __builtin_clzll(xb) : -1;
+          const uint32_t psum_pv = (uint32_t)__builtin_amdgcn_ds_bpermute(max(pv, 0) << 2, (int)psum);
+          const uint32_t sts = psum - (pv >= 0 ? psum_pv : 0u);  // an EXACT lane adds 0 to psum
+          const uint64_t upto = pv >= 0 ? (~0ull >> (63 - pv)) : 0ull;  // lanes 0 .. pv
+          const uint64_t span = lt_mask & ~upto;
+          const bool clean = (tim & span) == 0ull && (chg & span & ~(upto << 1 | 1ull)) == 0ull;
+          int slot_l = (int)(int8_t)(eb & 0xffu);
+          if (round > 0 && isx) slot_l = F.sdump[(ea >> 2) & 1023u];  // slots were reassigned
+          const uint32_t xi = (uint32_t)(slot_l & 0xff) | ((uint32_t)(ej + 128) << 8) | ((uint32_t)(ejp + 128) << 16) |
+                              (((eb >> 8) & 7u) << 24) | (clean ? XI_CLEAN : 0u) | (pv == lane - 1 ? XI_EMPTY : 0u);
+          auto xslot_of = [](uint32_t a) { return (int)(int8_t)(a & 0xffu); };
           int i = e - held;
-          int x = next_x(i);
-          int xslot = x < wend ? slot_at(x) : -1;
+          int last = i - 1;  // the last entry consumed
+          uint64_t rem = exm & (~0ull << i);
+          int x = rem != 0ull ? __ffsll((long long)rem) - 1 : -1;
+          uint32_t a = x >= 0 ? uni_u(readlane_u32(xi, x)) : 0u;
           SlotAhead X = {};
-          if (xslot >= 0) X = slot_ahead(F, xslot);
-          while (true) {
-            const int x2 = x < wend ? next_x(x + 1) : wend;
-            const int xslot2 = x2 < wend ? slot_at(x2) : -1;
+          if (x >= 0 && xslot_of(a) >= 0) X = slot_ahead(F, xslot_of(a));
+          while (x >= 0) {
+            rem &= rem - 1ull;
+            const int x2 = rem != 0ull ? __ffsll((long long)rem) - 1 : -1;
+            const uint32_t a2 = x2 >= 0 ? uni_u(readlane_u32(xi, x2)) : 0u;
             SlotAhead X2 = {};
-            if (xslot2 >= 0) X2 = slot_ahead(F, xslot2);
-            // runs (and PLAIN_TIE segments) i .. x-1 on grid jc: terms are >=
-            // 0, so they stay in the binade exactly when their total does
-            if (x > i) {
-              const uint64_t span = (x >= kWave ? ~0ull : ((1ull << x) - 1ull)) & (~0ull << i);
+            if (x2 >= 0 && xslot_of(a2) >= 0) X2 = slot_ahead(F, xslot_of(a2));
+            // the stretch before x on grid jc (added already when x resumes a
+            // round): terms are >= 0, so it stays in the binade exactly when
+            // its total does
+            if ((a & XI_EMPTY) == 0u && !(x == i && round > 0)) {
               bool bad;
-              if ((tim & span) == 0ull) {
-                const uint32_t hi = readlane_u32(psum, x - 1);
-                const uint32_t lo = readlane_u32(psum, (i - 1) & (kWave - 1));
-                N += hi - (i > 0 ? lo : 0u);
-                bad = __ballot(((span >> lane) & 1ull) != 0ull && ej != jc) != 0ull;
+              if ((a & XI_CLEAN) != 0u) {
+                N += readlane_u32(sts, x);
+                bad = (int)((a >> 16) & 0xffu) - 128 != jc;
               } else {
                 // a PLAIN_TIE segment adds the units its ties take for the
                 // parity of the integer it starts at: one entry at a time
                 bad = false;
-                for (int r = i; r < x; ++r) {
-                  const uint32_t a = readlane_u32(ea, r), b = readlane_u32(eb, r);
-                  const uint32_t tu = a >> 24;
-                  const uint32_t bump = (a & 3u) == E_TIE ? ((N & 1u) ? (tu >> 4) : (tu & 15u)) : 0u;
-                  bad = bad || (int)((a >> 16) & 0xffu) - 128 != jc || N >= kGridTop;
-                  N += b + bump;
+                for (int r = last + 1; r < x; ++r) {
+                  const uint32_t ra = readlane_u32(ea, r), rb = readlane_u32(eb, r);
+                  const uint32_t tu = ra >> 24;
+                  const uint32_t bump = (ra & 3u) == E_TIE ? ((N & 1u) ? (tu >> 4) : (tu & 15u)) : 0u;
+                  bad = bad || (int)((ra >> 16) & 0xffu) - 128 != jc || N >= kGridTop;
+                  N += rb + bump;
                 }
               }
               if (bad || N >= kGridTop) {
@@ -1088,20 +1111,39 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
                 break;
               }
             }
-            i = x;
-            if (i >= wend) break;
-            if (xslot < 0) {
+            if (xslot_of(a) < 0) {
               more = true;  // EXACT segments past this round's slots
+              last = x - 1;
               break;
             }
-            resolve_ahead(N, jc, xslot, (int)readlane_u32((uint32_t)ej, x), (int)((readlane_u32(eb, x) >> 8) & 0xffu),
-                          X, F);
-            ++i;
+            resolve_ahead(N, jc, xslot_of(a), (int)((a >> 8) & 0xffu) - 128, (int)((a >> 24) & 7u), X, F);
+            last = x;
             x = x2;
-            xslot = xslot2;
+            a = a2;
             X = X2;
           }
-          e = held + i;
+          if (!fail && !more && last < wend - 1) {
+            // the window's last stretch: entries last + 1 .. wend - 1
+            const uint64_t tspan = (wend >= kWave ? ~0ull : ((1ull << wend) - 1ull)) & (~0ull << (last + 1));
+            const uint64_t gspan = tspan & ~(1ull << (last + 1));
+            bool bad;
+            if ((tim & tspan) == 0ull && (chg & gspan) == 0ull) {
+              N += readlane_u32(psum, wend - 1) - (last >= 0 ? readlane_u32(psum, last) : 0u);
+              bad = (int)readlane_u32((uint32_t)ej, last + 1) != jc;
+            } else {
+              bad = false;
+              for (int r = last + 1; r < wend; ++r) {
+                const uint32_t ra = readlane_u32(ea, r), rb = readlane_u32(eb, r);
+                const uint32_t tu = ra >> 24;
+                const uint32_t bump = (ra & 3u) == E_TIE ? ((N & 1u) ? (tu >> 4) : (tu & 15u)) : 0u;
+                bad = bad || (int)((ra >> 16) & 0xffu) - 128 != jc || N >= kGridTop;
+                N += rb + bump;
+              }
+            }
+            if (bad || N >= kGridTop) fail = true;
+            last = wend - 1;
+          }
+          e = held + last + 1;
         }
         if (lane == 0) {
           F.s_run = __uint_as_float(grid_bits(N, jc));
