@@ -98,6 +98,10 @@ struct FastShared {
   union {
     float data[fastp::W][fastp::KL][fastp::SEG];  // LDS-resident segments (q), phases L and S
     ExactSlots x;                                 // after phase S
+    struct {
+      ExactSlots x;
+      float4 ctab[fastp::W][kWave];               // phase S: the register batches' per-segment constants,
+    } s;                                          //   past everything phases F+X .. C write
   } u;
   union {
     float aseg[fastp::GMAX];                    // segment sums of q (phases L, M)

@@ -794,24 +794,39 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       const GridConst gc_l = grid_const(have ? (int)F.sj[w + W * lane] : 0, Rw, theta, fabsf(aw), t1);
       const float sclo_l = plain_l ? gc_l.sc_lo : 0.0f;
       const float schi_l = plain_l ? gc_l.sc_hi : 0.0f;
-      const uint32_t tspec_l = plain_l ? __float_as_uint(gc_l.tspec) : 0xffffffffu;
+      const uint32_t tsp_l = plain_l ? __float_as_uint(gc_l.tspec) : 0xffffffffu;
+      // the same constants as an LDS table, read by the register batches
+      // (an LDS read instead of three readlanes per segment), in LDS no
+      // other wave writes before the walk ends
+      float4* const ctab = &F.u.s.ctab[w][0];
       auto lds_q = [&](int k) {
         return to_v4(reinterpret_cast<const float4*>(&F.u.data[w][min(max(k - KV, 0), KL - 1)][0])[lane]);
       };
       // One batch: four segments k0 .. k0 + 3 (k0 a constant).  Per lane and
       // segment, the lower and upper bracket roundings of its four terms
       // (bit patterns of MAGIC + rounding); the lane is special when the
-      // sums differ or a term reaches tspec.  Sums keep the MAGIC offsets
-      // (wrapping; the true values are far below 2^32), taken out where a
-      // sum is used.
-      auto batch = [&](const int k0, const llz_f4v qa, const llz_f4v qb, const llz_f4v qc, const llz_f4v qd) {
-        uint32_t raw4[4], sl = 0;
+      // sums differ or a term reaches tspec (tsp).  Sums
+      // wrap (the true values are far below 2^32); the segment sums keep the
+      // offsets (4 MAGIC_BITS a lane, even), taken out in phase B.
+      auto batch = [&](const int k0, const bool tab, const llz_f4v qa, const llz_f4v qb, const llz_f4v qc,
+                       const llz_f4v qd) {
+        uint32_t raw4[4];
+        uint64_t spm[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const int kl = min(k0 + s, kWave - 1);
-          const float sc_lo = readlane_f32(sclo_l, kl);
-          const float sc_hi = readlane_f32(schi_l, kl);
-          const uint32_t tspec = readlane_u32(tspec_l, kl);
+          float sc_lo, sc_hi;
+          uint32_t tsp;
+          if (tab) {
+            const float4 c = ctab[min(k0 + s, kWave - 1)];
+            sc_lo = c.x;
+            sc_hi = c.y;
+            tsp = __float_as_uint(c.z);
+          } else {
+            const int kl = min(k0 + s, kWave - 1);
+            sc_lo = readlane_f32(sclo_l, kl);
+            sc_hi = readlane_f32(schi_l, kl);
+            tsp = readlane_u32(tsp_l, kl);
+          }
           const llz_f4v qv4 = s == 0 ? qa : s == 1 ? qb : s == 2 ? qc : qd;  // s is a constant here
           const uint32_t l0 = __float_as_uint(fmaf(qv4.x, sc_lo, MAGIC));
           const uint32_t l1 = __float_as_uint(fmaf(qv4.y, sc_lo, MAGIC));
@@ -823,35 +838,24 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           const uint32_t h3 = __float_as_uint(fmaf(qv4.w, sc_hi, MAGIC));
           // bit patterns of non-negative floats order like their values: each
           // upper bracket is >= its lower one, so the sums agree exactly when
-          // every pair does (no wrap below tspec <= MAGIC + 2^15)
+          // every pair does
           const uint32_t lsum = (l0 + l1) + (l2 + l3);
           const uint32_t hsum = (h0 + h1) + (h2 + h3);
           const uint32_t hmax = max(max(h0, h1), max(h2, h3));
           raw4[s] = lsum;
           // absent positions hold q = 0, so their brackets are MAGIC: never
           // special (tspec > MAGIC for PLAIN segments outside flood mode, and
-          // theta is +inf in flood mode)
-          sl |= (hsum != lsum || hmax >= tspec) ? (1u << s) : 0u;
+          // theta is +inf in flood mode; the other segments have zero scales).
+          // Two ballots straight from the compares
+          spm[s] = __builtin_amdgcn_ballot_w64(hsum != lsum) | __builtin_amdgcn_ballot_w64(hmax >= tsp);
         }
         // segment sums in four parts, one per 16-lane row (lane 16 r + 12 + s
         // holds row r's part of segment k0 + s).  Every wave has room for 64
-        // segments: absent ones store MAGIC offsets only
+        // segments: absent ones store offsets only
         const uint32_t rsum = row_sums4(raw4[0], raw4[1], raw4[2], raw4[3]);
         if ((lane & 12) == 12) F.v.ssum4[w + W * (k0 + (lane & 3))][lane >> 4] = rsum;
-        if (__ballot(sl != 0u) != 0ull) {
-          // a tie is decided by the parity of the integer before it: per
-          // segment, that of the lower bracket sum of the lanes below (the
-          // offsets, 4 MAGIC_BITS a lane, are even)
-          uint32_t par4[4];
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const uint64_t pm = __ballot((raw4[s] & 1u) != 0u);
-            par4[s] = __builtin_amdgcn_mbcnt_hi((uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u)) << 31;
-          }
-          // every lane appends its entries after those of the lanes below it
-          const uint32_t my = (uint32_t)__popc(sl);
-          const uint32_t incl = wave_incl_scan_op(my, 0u, [](uint32_t a, uint32_t b) { return a + b; });
-          const int total = (int)lane_readlast(incl);
+        const int total = __popcll(spm[0]) + __popcll(spm[1]) + __popcll(spm[2]) + __popcll(spm[3]);
+        if (total != 0) {
           if (total > qcap) {
             qovf = true;  // more uncertified lanes in four segments than a chunk holds
           } else {
@@ -863,20 +867,28 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
               // SPW * 64 (always enough: a wave has at most SPW / 4 + 2 batches)
               if (qch * qcap > SPW * kWave || qch >= kWave) qovf = true;
             }
-            int slot = qn + (int)(incl - my);
             uint32_t* const op = ovp + (qch - 1) * qcap;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-              if (sl & (1u << s)) {
-                const uint32_t qp = (uint32_t)((w + W * (k0 + s)) * SEG + lane4) | par4[s];
-                if (qch == 0)
-                  F.qpos[w][slot] = qp;
-                else if (!qovf)
-                  op[slot] = qp;
-                ++slot;
+              if (spm[s] != 0ull) {
+                // segment by segment, in lane order; a tie is decided by the
+                // parity of the integer before it: per segment, that of the
+                // lower bracket sum of the lanes below
+                const uint64_t pm = __builtin_amdgcn_ballot_w64((raw4[s] & 1u) != 0u);
+                const uint32_t par =
+                    __builtin_amdgcn_mbcnt_hi((uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u));
+                const int slot =
+                    qn + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(spm[s] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)spm[s], 0u));
+                const uint32_t qp = (uint32_t)((w + W * (k0 + s)) * SEG + lane4) | (par << 31);
+                if ((spm[s] >> lane) & 1ull) {
+                  if (qch == 0)
+                    F.qpos[w][slot] = qp;
+                  else if (!qovf)
+                    op[slot] = qp;
+                }
+                qn += __popcll(spm[s]);
               }
             }
-            qn += total;
           }
         }
       };
@@ -890,14 +902,16 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
 #pragma unroll
       for (int b = 0; b < kLdsBatches; ++b) {
         const int k0 = (KV - 1) + 4 * b;
-        if (k0 < nseg_w) batch(k0, k0 < KV ? to_v4(d[k0 < KV ? k0 : 0]) : lds_q(k0), lds_q(k0 + 1), lds_q(k0 + 2), lds_q(k0 + 3));
+        if (k0 < nseg_w)
+          batch(k0, false, k0 < KV ? to_v4(d[k0 < KV ? k0 : 0]) : lds_q(k0), lds_q(k0 + 1), lds_q(k0 + 2), lds_q(k0 + 3));
       }
       __syncthreads();
       exact_loads<FASTLD>(F, xr, w, min(F.nslot, DCAP), n);
+      ctab[lane] = make_float4(sclo_l, schi_l, __uint_as_float(tsp_l), 0.0f);  // read by this wave only
 #pragma unroll
       for (int b = 0; b < (KV - 1) / 4; ++b) {
         const int k0 = 4 * b;
-        if (k0 < nseg_w) batch(k0, to_v4(d[k0]), to_v4(d[k0 + 1]), to_v4(d[k0 + 2]), to_v4(d[k0 + 3]));
+        if (k0 < nseg_w) batch(k0, true, to_v4(d[k0]), to_v4(d[k0 + 1]), to_v4(d[k0 + 2]), to_v4(d[k0 + 3]));
       }
       ccnt = lane == qch ? qn : ccnt;  // the last chunk's entries
       if (qovf && lane == 0) atomicOr(&F.fail, 1u);
