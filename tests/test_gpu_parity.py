@@ -351,6 +351,34 @@ def test_non_finite_rows(cuda):
 
 
 # ---------------------------------------------------------------------------
+# the fast path is the one taken (a row it cannot certify is still exact,
+# through the streaming normaliser, but several times slower)
+# ---------------------------------------------------------------------------
+def test_headline_rows_take_fast_path(cuda):
+    """Every row of the headline batch is certified by the single-pass
+    statistics (path bit 8 clear); a few rows are also checked against the
+    oracle."""
+    import torch
+
+    w = WORKLOADS["headline"]
+    rows = w.rows
+    x = w.logits(rows)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    cfg = llz.SamplerConfig.of(w.params)
+    ws = torch.zeros(llz.workspace_bytes(rows, w.vocab, cfg), dtype=torch.uint8, device=cuda)
+    xt = torch.from_numpy(np.ascontiguousarray(x)).to(cuda)
+    ut = torch.from_numpy(np.ascontiguousarray(u, dtype=np.float32)).to(cuda)
+    res = llz.sample_rows(xt, cfg, ut, kept_cap=256, stats=True, workspace=ws)
+    torch.cuda.synchronize()
+    status = ws[: rows * 4].view(torch.int32).cpu().numpy()  # per-row path bits (workspace offset 0)
+    slow = np.flatnonzero(status & 8)
+    assert slow.size == 0, f"rows not certified by the fast path: {slow.tolist()}"
+    tok = res.tokens.cpu().numpy().view(np.uint32)
+    for r in range(0, rows, 37):
+        assert tok[r] == O.sample_row(x[r], w.params, u[r]).token, r
+
+
+# ---------------------------------------------------------------------------
 # the special queue's chunks past the LDS queue
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("qcap", [8, 32, 64])
