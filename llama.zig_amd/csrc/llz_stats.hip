@@ -365,13 +365,14 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
   const int lane = lane_id();
   const float bw = F.bw[w];  // |aw| of this wave (phase M)
   const int n = P.n;
-  uint32_t pos2[2], pre2[2], rl[2][4], rx[2][4];
-  int j2[2];
-  bool act2[2];
+  uint32_t pos2[2] = {0u, 0u}, pre2[2] = {0u, 0u}, rl[2][4] = {}, rx[2][4] = {};
+  int j2[2] = {0, 0};
+  bool act2[2] = {false, false};
   uint32_t spm = 0;
-  // brackets as phase S computed them
+  // brackets as phase S computed them (the second half only when in use)
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
+    if (h == 1 && qn <= kWave) break;
     const int i = h * kWave + lane;
     act2[h] = i < qn;
     const uint32_t qp = act2[h] ? F.qpos[w][i] : 0u;
