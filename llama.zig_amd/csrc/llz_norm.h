@@ -95,30 +95,28 @@ __device__ float wave_accumulate(float s, const float (&x)[V]) {
 }
 
 // The chain of one 64-term chunk, the terms held one per lane (lane i: term
-// i, i < len <= 64; absent terms have the sign bit set): lane i ends with the
-// running value after term i, the lanes from len on with the value after
-// the last.  At step k every lane from k on adds term k (the others add -0,
-// which leaves any value unchanged).  The steps use constant lane indices and
-// no branches (a wave running alone pays for every dependent step).  SUB
-// subtracts: s - x is computed as s + (-x), which IEEE defines to be the same.
+// i, i < len <= 64; absent terms have the sign bit set): lane i < len ends
+// with the running value after term i (lanes from len on hold no useful
+// value).  Lane 0 starts as s + x_0 and every other lane as its own term;
+// each step adds to every lane the value of the lane below it (one DPP
+// instruction, wave_shr:1), so lane i holds the sequential chain through
+// term i from step i on and keeps it: (value after term i-1) + x_i is the
+// reference's own next operation.  SUB subtracts: s - x is computed as s +
+// (-x), which IEEE defines to be the same.
 template <bool SUB>
 __device__ __forceinline__ float wave_chain_lanes(float s, float x0, int len) {
   const int lane = lane_id();
   const bool present = lane < len && !(as_bits(x0) >> 31);
   const float x = present ? (SUB ? -x0 : x0) : -0.0f;
-  float acc = s;
+  const float y = lane == 0 ? s + x : x;
+  float acc = y;
+  // steps in groups of eight (a step past len leaves lanes < len unchanged)
 #pragma unroll
-  for (int k8 = 0; k8 < kWave; k8 += 8) {
+  for (int k8 = 1; k8 < kWave; k8 += 8) {
     if (k8 >= len) break;
 #pragma unroll
-    for (int k = k8; k < k8 + 8; ++k) {
-      // the empty asm keeps each lane test at its step (hoisted, the 64
-      // lane masks would not fit in scalar registers)
-      int kk = k;
-      asm volatile("" : "+s"(kk));
-      const float xk = readlane_f32(x, k);
-      acc = acc + (lane >= kk ? xk : -0.0f);
-    }
+    for (int k = 0; k < 8; ++k)
+      acc = y + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xf, 0xf, true));
   }
   return acc;
 }
@@ -144,7 +142,7 @@ __device__ float wave_seq_list(float s, int len, float thr, int& stop, TermFn te
       stop = base + L;
       return readlane_f32(acc, L);
     }
-    s = readlane_f32(acc, kWave - 1);
+    s = readlane_f32(acc, cnt - 1);
   }
   return s;
 }
