@@ -934,18 +934,14 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       }
       if (w == 0) {
         // the row's first segment (slot 0) from 0, term by term as
-        // sampler.zig:87 adds them: every lane runs the same chain over LDS
-        // broadcasts of the exact terms.  The walk starts after it.
-        const float4* d0 = reinterpret_cast<const float4*>(&F.u.x.dump[0][0]);
-        float s0 = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < SEG / 4; ++i) {
-          const float4 e4 = d0[i];
-          s0 = s0 + e4.x;
-          s0 = s0 + e4.y;
-          s0 = s0 + e4.z;
-          s0 = s0 + e4.w;
-        }
+        // sampler.zig:87 adds them: four chains of 64 terms, one term per
+        // lane (absent positions hold 0).  The walk starts after it.
+        const float* d0 = &F.u.x.dump[0][0];
+        const float x0 = d0[lane], x1 = d0[kWave + lane], x2 = d0[2 * kWave + lane], x3 = d0[3 * kWave + lane];
+        float s0 = readlane_f32(wave_chain_lanes<false>(0.0f, x0, kWave), kWave - 1);
+        s0 = readlane_f32(wave_chain_lanes<false>(s0, x1, kWave), kWave - 1);
+        s0 = readlane_f32(wave_chain_lanes<false>(s0, x2, kWave), kWave - 1);
+        s0 = readlane_f32(wave_chain_lanes<false>(s0, x3, kWave), kWave - 1);
         if (lane == 0) {
           F.s_run = s0;
           F.next_e = 1;
