@@ -1086,43 +1086,46 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           auto xslot_of = [](uint32_t a) { return (int)(int8_t)(a & 0xffu); };
           int i = e - held;
           int last = i - 1;  // the last entry consumed
+          // the next EXACT entry's data is read without branches (an absent
+          // one reads lane 0 and slot 0, unused)
           uint64_t rem = exm & (~0ull << i);
           int x = rem != 0ull ? __ffsll((long long)rem) - 1 : -1;
-          uint32_t a = x >= 0 ? uni_u(readlane_u32(xi, x)) : 0u;
-          SlotAhead X = {};
-          if (x >= 0 && xslot_of(a) >= 0) X = slot_ahead(F, xslot_of(a));
+          uint32_t a = uni_u(readlane_u32(xi, x & (kWave - 1)));
+          SlotAhead X = slot_ahead(F, max(xslot_of(a), 0));
           while (x >= 0) {
             rem &= rem - 1ull;
             const int x2 = rem != 0ull ? __ffsll((long long)rem) - 1 : -1;
-            const uint32_t a2 = x2 >= 0 ? uni_u(readlane_u32(xi, x2)) : 0u;
-            SlotAhead X2 = {};
-            if (x2 >= 0 && xslot_of(a2) >= 0) X2 = slot_ahead(F, xslot_of(a2));
+            const uint32_t a2 = uni_u(readlane_u32(xi, x2 & (kWave - 1)));
+            const SlotAhead X2 = slot_ahead(F, max(xslot_of(a2), 0));
             // the stretch before x on grid jc (added already when x resumes a
             // round): terms are >= 0, so it stays in the binade exactly when
-            // its total does
-            if ((a & XI_EMPTY) == 0u && !(x == i && round > 0)) {
-              bool bad;
-              if ((a & XI_CLEAN) != 0u) {
-                N += readlane_u32(sts, x);
-                bad = (int)((a >> 16) & 0xffu) - 128 != jc;
-              } else {
-                // a PLAIN_TIE segment adds the units its ties take for the
-                // parity of the integer it starts at: one entry at a time
-                bad = false;
-                for (int r = last + 1; r < x; ++r) {
-                  const uint32_t ra = readlane_u32(ea, r), rb = readlane_u32(eb, r);
-                  const uint32_t tu = ra >> 24;
-                  const uint32_t bump = (ra & 3u) == E_TIE ? ((N & 1u) ? (tu >> 4) : (tu & 15u)) : 0u;
-                  bad = bad || (int)((ra >> 16) & 0xffu) - 128 != jc || N >= kGridTop;
-                  N += rb + bump;
-                }
-              }
-              if (bad || N >= kGridTop) {
+            // its total does.  The common case (one step, or nothing) without
+            // a branch
+            const bool skip = (a & XI_EMPTY) != 0u || (x == i && round > 0);
+            if (__builtin_expect(skip || (a & XI_CLEAN) != 0u, 1)) {
+              N += skip ? 0u : readlane_u32(sts, x);
+              const bool bad = !skip && (int)((a >> 16) & 0xffu) - 128 != jc;
+              if (__builtin_expect(bad || N >= kGridTop, 0)) {
                 fail = true;  // the running sum is not in the predicted binade, or leaves it
                 break;
               }
+            } else {
+              // a PLAIN_TIE segment adds the units its ties take for the
+              // parity of the integer it starts at: one entry at a time
+              bool bad = false;
+              for (int r = last + 1; r < x; ++r) {
+                const uint32_t ra = readlane_u32(ea, r), rb = readlane_u32(eb, r);
+                const uint32_t tu = ra >> 24;
+                const uint32_t bump = (ra & 3u) == E_TIE ? ((N & 1u) ? (tu >> 4) : (tu & 15u)) : 0u;
+                bad = bad || (int)((ra >> 16) & 0xffu) - 128 != jc || N >= kGridTop;
+                N += rb + bump;
+              }
+              if (bad || N >= kGridTop) {
+                fail = true;
+                break;
+              }
             }
-            if (xslot_of(a) < 0) {
+            if (__builtin_expect(xslot_of(a) < 0, 0)) {
               more = true;  // EXACT segments past this round's slots
               last = x - 1;
               break;
