@@ -44,7 +44,7 @@ __device__ float tile_accumulate(float s, const float (&x)[V], int L, float thr,
     // one barrier: per-wave saturated sums with the wave's tie flag in bit 31
     {
       const uint32_t ws = wave_sum_sat(tsum, kSat);
-      const bool wt = __ballot(ttie) != 0ull;
+      const bool wt = bal64(ttie) != 0ull;
       if (lane_id() == 0) sh.red[bank][wave_id()] = ws | (wt ? 0x80000000u : 0u);
       lds_barrier();
     }
@@ -137,7 +137,7 @@ __device__ float tile_accumulate_fn(float s, RFn R, EFn E, PFn present, WgScratc
     }
     {
       const uint32_t ws = wave_sum_sat(tsum, kSat);
-      const bool wt = __ballot(ttie) != 0ull;
+      const bool wt = bal64(ttie) != 0ull;
       if (lane_id() == 0) sh.red[bank][wave_id()] = ws | (wt ? 0x80000000u : 0u);
       lds_barrier();
     }

@@ -84,7 +84,7 @@ __device__ float wave_accumulate(float s, const float (&x)[V]) {
         }
       }
     }
-    const uint64_t mask = __ballot(my_evt >= 0);
+    const uint64_t mask = bal64(my_evt >= 0);
     if (mask == 0ull) return grid_value(g.N + readlane_u32(incl, kWave - 1), g.j);
     const int L = __ffsll((long long)mask) - 1;
     const int P = (int)readlane_u32((uint32_t)my_evt, L);
@@ -136,7 +136,7 @@ __device__ float wave_seq_list(float s, int len, float thr, int& stop, TermFn te
     const bool present = lane < cnt && !(as_bits(x0) >> 31);
     const float acc = wave_chain_lanes<SUB>(s, x0, cnt);
     const bool hit = present && (SUB ? (acc <= 0.0f) : (thr >= 0.0f && acc > thr));
-    const uint64_t hits = __ballot(hit);
+    const uint64_t hits = bal64(hit);
     if (hits != 0ull) {
       const int L = __ffsll((long long)hits) - 1;
       stop = base + L;

@@ -74,7 +74,7 @@ __device__ __forceinline__ void slice_sums(const SliceState& S, int sb, int n, i
   for (int c = 0; c < kSub; ++c) sums[c] = c < c_from ? 0u : wave_sum_sat(acc[c], kSat);
   uint32_t tie_w = 0;
 #pragma unroll
-  for (int c = 0; c < kSub; ++c) tie_w |= (__ballot((tie_c >> c) & 1u) != 0ull) ? (1u << c) : 0u;
+  for (int c = 0; c < kSub; ++c) tie_w |= (bal64((tie_c >> c) & 1u) != 0ull) ? (1u << c) : 0u;
   if (lane == 0) {
 #pragma unroll
     for (int c = 0; c < kSub; ++c)
@@ -111,13 +111,13 @@ __device__ __forceinline__ void slice_state(const float (&v)[kSub][kV], int sb, 
       if (spec) S.spec |= 1u << (c * kV + k);
     }
   }
-  if (__ballot(S.spec != 0) == 0ull) return;
+  if (bal64(S.spec != 0) == 0ull) return;
   const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
   int qn = 0;
 #pragma unroll
   for (int e = 0; e < kSub * kV; ++e) {
     const bool sp = (S.spec >> e) & 1u;
-    const uint64_t mk = __ballot(sp);
+    const uint64_t mk = bal64(sp);
     if (sp) {
       ns.ev[w][e][lane] = v[e / kV][e % kV];
       const int slot = qn + (int)__popcll(mk & lt);
@@ -210,7 +210,7 @@ __device__ __forceinline__ bool wave_resolve(float& s, int& done, const SliceSta
         }
       }
     }
-    const uint64_t mask = __ballot(my_evt >= 0);
+    const uint64_t mask = bal64(my_evt >= 0);
     if (mask == 0ull) {
       s = grid_value(g.N + lane_readlast(incl), g.j);
       done = kWave * kV - 1;
@@ -311,7 +311,7 @@ __device__ float row_normaliser(const float* xr, int n, const RowParams& P, Samp
           const uint32_t incl = wave_incl_scan_sat(psum, kSat);
           const uint32_t excl = wave_shift_up1(incl);
           const bool evt = act && ((pv >> 31) || g_top_reached(N, incl));
-          const uint64_t mask = __ballot(evt);
+          const uint64_t mask = bal64(evt);
           if (mask == 0ull) {
             s = grid_value(N + lane_readlast(incl), j);
             c0 = NC;
@@ -586,9 +586,9 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
     int M = c;
     if (P.cand_theta > 0.0f) {
       M = 0;
-      if (c <= kWave) M = __popcll(__ballot(lane < c && xl > p_nc));
+      if (c <= kWave) M = __popcll(bal64(lane < c && xl > p_nc));
       else
-        for (int b = 0; b < c; b += kWave) M += __popcll(__ballot(b + lane < c && pq(b + lane) > p_nc));
+        for (int b = 0; b < c; b += kWave) M += __popcll(bal64(b + lane < c && pq(b + lane) > p_nc));
     }
     // top-k, min-p, top-p (sampler.zig:106-126): each keeps a prefix
     const int Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
@@ -596,9 +596,9 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
     if (P.min_p > 0.0f) {
       const float thr = (1.0f / S) * P.min_p;  // probs[indices[0]] = 1 / S: the row maximum has e = 1
       int cnt = 0;
-      if (M <= kWave) cnt = __popcll(__ballot(lane < M && xl >= thr));
+      if (M <= kWave) cnt = __popcll(bal64(lane < M && xl >= thr));
       else
-        for (int b = 0; b < M; b += kWave) cnt += __popcll(__ballot(b + lane < M && pq(b + lane) >= thr));
+        for (int b = 0; b < M; b += kWave) cnt += __popcll(bal64(b + lane < M && pq(b + lane) >= thr));
       if (cnt < M) Km = cnt;
       else if (M < n && thr > p_nc) Km = M;
     }
@@ -615,7 +615,7 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
       if (lim <= kWave) {
         acc = wave_chain_lanes<false>(0.0f, xl, lim);
         covered = lim;
-        const uint64_t hits = __ballot(lane < lim && acc > P.top_p);
+        const uint64_t hits = bal64(lane < lim && acc > P.top_p);
         st = hits != 0ull ? __ffsll((long long)hits) - 1 : -1;
       } else {
         wave_seq_list<false>(0.0f, lim, P.top_p, st, pq);
@@ -640,7 +640,7 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
         consumed = 1;
         if (K <= kWave) {
           const float r = wave_chain_lanes<true>(u_row * total, xl, K);
-          const uint64_t hits = __ballot(lane < K && r <= 0.0f);
+          const uint64_t hits = bal64(lane < K && r <= 0.0f);
           st = hits != 0ull ? __ffsll((long long)hits) - 1 : -1;
         } else {
           wave_seq_list<true>(u_row * total, K, -1.0f, st, pq);

@@ -130,7 +130,7 @@ __device__ __forceinline__ void slot_terms(FastShared& F, const RowPtrs& Q, cons
   *p = e;
   // candidates (absent positions hold 0 < theta)
   const bool cand_any = e.x >= theta || e.y >= theta || e.z >= theta || e.w >= theta;
-  if (__ballot(pred && cand_any) != 0ull) {
+  if (bal64(pred && cand_any) != 0ull) {
     const float es[4] = {e.x, e.y, e.z, e.w};
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -163,7 +163,7 @@ __device__ __forceinline__ void slot_tables(FastShared& F, int slot) {
     }
     const uint32_t pa = wave_incl_scan_sat(sa, kSat);
     const uint32_t pb = wave_incl_scan_sat(sb, kSat);
-    const uint64_t ma = __ballot(ta), mb = __ballot(tb);
+    const uint64_t ma = bal64(ta), mb = bal64(tb);
     F.u.x.pref[slot][0][lane] = pa;
     F.u.x.pref[slot][1][lane] = pb;  // NG >= 2: room even when ng == 1
     if (lane == 0) {
@@ -181,7 +181,7 @@ __device__ __forceinline__ void slot_tables(FastShared& F, int slot) {
       tie_any = tie_any || tie;
     }
     F.u.x.pref[slot][kk][lane] = wave_incl_scan_sat(sum, kSat);
-    const uint64_t tm = __ballot(tie_any);
+    const uint64_t tm = bal64(tie_any);
     if (lane == 0) F.u.x.tmask[slot][kk] = tm;
   }
 }
@@ -274,7 +274,7 @@ __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slo
     t = t + X.e4.z;
     t = t + X.e4.w;
     const uint64_t tm0 = ((uint64_t)uni_u(X.tm0h) << 32) | uni_u(X.tm0l);
-    const uint64_t ev = __ballot(X.pv0 >= kSat || N + X.pv0 >= kGridTop) | tm0;
+    const uint64_t ev = bal64(X.pv0 >= kSat || N + X.pv0 >= kGridTop) | tm0;
     // three outcomes, computed together and taken with one branch: no event
     // on grid J0 (the table's total), an event in the last lane, or one
     // crossing into grid J0 + 1 with the rest of the segment event-free there
@@ -334,7 +334,7 @@ __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slo
     t = t + X.e4.y;
     t = t + X.e4.z;
     t = t + X.e4.w;
-    const uint64_t ev = (__ballot(cr) | tm) & live;
+    const uint64_t ev = (bal64(cr) | tm) & live;
     if (ev == 0ull) {
       N = uni_u(N + (readlane_u32(pv, kWave - 1) - base));
       break;
@@ -417,7 +417,7 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
     corr2[h] = (rx[h][0] - rl[h][0]) + (rx[h][1] - rl[h][1]) + (rx[h][2] - rl[h][2]) + (rx[h][3] - rl[h][3]);
     if (act2[h] && corr2[h] != 0u) atomicAdd(&F.v.ssum4[pos2[h] >> 8][0], corr2[h]);
   }
-  if (__ballot(tiem != 0u) == 0ull) return;
+  if (bal64(tiem != 0u) == 0ull) return;
 
   // ties (rare): the integer sum before each, then per segment the units
   // its ties add for an even and an odd starting integer (a tie rounds up
@@ -427,7 +427,7 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
   int nt = 0;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    uint64_t lanes = __ballot((tiem >> (4 * h)) & 15u);
+    uint64_t lanes = bal64((tiem >> (4 * h)) & 15u);
     while (lanes != 0ull) {
       const int L = __ffsll((long long)lanes) - 1;
       lanes &= lanes - 1ull;
@@ -461,14 +461,14 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
     return;
   }
   bool open_t = lane < nt;
-  while (__ballot(open_t) != 0ull) {
+  while (bal64(open_t) != 0ull) {
     // the segment of the first remaining tie, its ties in position order
     const uint32_t g = wave_min_u32(open_t ? tpos : 0xffffffffu) >> 8;
     bool mine = open_t && (tpos >> 8) == g;
     uint32_t b0 = 0, b1 = 0;
-    while (__ballot(mine) != 0ull) {
+    while (bal64(mine) != 0ull) {
       const uint32_t pmin = wave_min_u32(mine ? tpos : 0xffffffffu);
-      const int L = __ffsll((long long)__ballot(mine && tpos == pmin)) - 1;
+      const int L = __ffsll((long long)bal64(mine && tpos == pmin)) - 1;
       const uint32_t pr = readlane_u32(tpre, L), kk = readlane_u32(tk, L);
       b0 += ((0u + pr + b0 + kk) & 1u);
       b1 += ((1u + pr + b1 + kk) & 1u);
@@ -627,7 +627,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     }
   }
   mx = wave_max_f32(mx);
-  const bool wnan = __ballot(nanf != 0u) != 0ull;
+  const bool wnan = bal64(nanf != 0u) != 0ull;
   if (lane == 0) {
     F.mw[w] = mx;
     F.cw[w] = cw;
@@ -668,7 +668,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     bool nl = false;
 #pragma unroll
     for (int i = 0; i < W; ++i) nl = nl | (av[i] != av[i]);
-    if (__ballot(nl) != 0ull) {
+    if (bal64(nl) != 0ull) {
       // a NaN logit: phase L's maximum did not quiet signalling NaNs, so the
       // row's maximum is taken again (sampler.zig:80-81: NaNs are skipped)
       nanrow = true;
@@ -741,12 +741,12 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       // EXACT slots: 0 for the row's first segment (always EXACT: it starts at
       // 0), the others in any order from 1 (a row with more than DCAP takes
       // further rounds in index order)
-      const uint64_t exm = __ballot(ex) & (w == 0 ? ~1ull : ~0ull);
+      const uint64_t exm = bal64(ex) & (w == 0 ? ~1ull : ~0ull);
       int base = 0;
       if (lane == 0) {
         if (exm != 0ull) base = (int)atomicAdd((uint32_t*)&F.nslot, (uint32_t)__popcll(exm));
         if (bad) atomicOr(&F.fail, 1u);
-        if (__ballot(fl) != 0ull) atomicOr(&F.flood, 1u);
+        if (bal64(fl) != 0ull) atomicOr(&F.flood, 1u);
       }
       base = __builtin_amdgcn_readfirstlane(base);
       if (have) {
@@ -976,7 +976,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       const bool plain = in && fl == PLAIN;
       const uint32_t key = plain ? (0x10000u | (uint32_t)(jj & 0xffff)) : 0u;
       const bool head = in && !(plain && wave_shift_up1(key) == key);
-      const uint64_t heads = __ballot(head);
+      const uint64_t heads = bal64(head);
       // a run's sum up to this lane: the inclusive prefix minus the exclusive
       // prefix at the run's head (prefixes never decrease, so a max-scan of the
       // heads' exclusive prefixes yields the latest head's); <= 64 * 2^25: no wrap
@@ -1022,7 +1022,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           for (int b = g_from; b < G; b += kWave) {
             const int g = b + lane;
             const bool ex = g < G && (F.sflag[g] == EXACT_PRED || F.sflag[g] == EXACT_DONE);
-            const uint64_t mk = __ballot(ex);
+            const uint64_t mk = bal64(ex);
             const int slot = cnt + __popcll(mk & lt_mask);
             if (ex) {
               F.sdump[g] = (int8_t)(slot < DCAP ? slot : -1);
@@ -1062,15 +1062,15 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
           const uint32_t eb = ok ? F.u.x.ent_b[held + lane] : 0u;
           const int ej = (int)((ea >> 16) & 0xffu) - 128;
           const bool isx = ok && (ea & 3u) == E_EXACT;
-          const uint64_t exm = __ballot(isx);
-          const uint64_t tim = __ballot(ok && (ea & 3u) == E_TIE);
+          const uint64_t exm = bal64(isx);
+          const uint64_t tim = bal64(ok && (ea & 3u) == E_TIE);
           // <= 64 * 2^25: no wrap
           const uint32_t psum =
               wave_incl_scan_op(ok && !isx ? eb : 0u, 0u, [](uint32_t a, uint32_t b) { return a + b; });
           const int wend = min(ne - held, kWave);
           const int ejp = (int)wave_shift_up1((uint32_t)ej);  // the entry before's grid
           // entries whose grid differs from the entry before (neither EXACT)
-          const uint64_t chg = __ballot(ok && !isx && lane > 0 && ej != ejp) & ~(exm << 1);
+          const uint64_t chg = bal64(ok && !isx && lane > 0 && ej != ejp) & ~(exm << 1);
           // the stretch ending at this lane: entries pv + 1 .. lane - 1
           const uint64_t xb = exm & lt_mask;
           const int pv = xb != 0ull ? 63 - __builtin_clzll(xb) : -1;

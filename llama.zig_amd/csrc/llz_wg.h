@@ -53,6 +53,10 @@ __device__ __forceinline__ uint32_t wave_incl_scan_op(uint32_t x, uint32_t id, O
   return s;
 }
 
+// A wave's ballot of a bool.  HIP's __ballot takes an int, and the compiler
+// then rebuilds the mask of a compound condition through a vector register.
+__device__ __forceinline__ uint64_t bal64(bool b) { return __builtin_amdgcn_ballot_w64(b); }
+
 __device__ __forceinline__ uint32_t lane_readlast(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, kWave - 1);
 }
