@@ -1177,8 +1177,11 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     pre_ok = !flood && cc <= (uint32_t)(NT - kWave);
   }
 
-  // ---- the selection stage, on the same workgroup and shared memory
-  __syncthreads();  // F is read: the selection reuses the memory
+  // ---- the selection stage, on the same workgroup and shared memory.  It
+  // writes only the first sizeof(SampleShared) bytes, inside F.u, which
+  // nothing reads after the walk's last barrier (the fields read since, the
+  // walk's results, lie past F.u): no barrier here
+  static_assert(sizeof(SampleShared) <= sizeof(F.u), "the selection's memory must lie inside F.u");
   select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified, u_row, certified && pre_ok,
              cand_pre, cand_n0);
 }
