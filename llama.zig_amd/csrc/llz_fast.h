@@ -2,11 +2,13 @@
 // sequential f32 normaliser and the candidate list (sampler.zig:80-88) with
 // one HBM read per logit.
 //
-// One 512-thread workgroup owns a row.  Wave w owns the contiguous run of
-// 256-element segments [w*SPW, (w+1)*SPW); the first KV segments of the run
-// stay in VGPRs (one float4 per lane per segment), the next KL in LDS.
+// One 512-thread workgroup owns a row.  Wave w owns the 256-element segments
+// w, w + W, w + 2W, ... (interleaved, so the costly start of the row is
+// shared by every wave); its first KV segments stay in VGPRs (one float4 per
+// lane per segment), the next KL in LDS.
 //
-// Phase L (while the loads land): per-lane running maximum; the estimate
+// Phase L (as the loads land, a window of kLoadWindow in flight per wave):
+// per-lane running maximum; the estimate
 //     q = exp2(v * RN(log2(e)/T) - c_w),   c_w = RN(m_w * RN(log2(e)/T))
 // with m_w the maximum of the wave's first segment, stored over v; the
 // segment sum of q.
@@ -19,14 +21,18 @@
 // u = 2^(j-23): with sc = R_w 2^(23-j), fma(q, sc(1 -+ eps), 1.5*2^23) gives
 // RN(q sc (1 -+ eps)) as an integer.  When both agree the true RN(e / u) is
 // that integer and is not a tie; the others (and the large terms and the
-// candidates) are "special": re-read, evaluated with the exact exp
-// (llz_math.h) and corrected.  A special whose exact term is a tie turns its
-// segment EXACT.
-// Phase X: EXACT segments are re-read and evaluated exactly into LDS.
-// Phase C: one wave walks the segments in index order: runs of PLAIN
-// segments add their integer sums while the running sum stays in their
-// binade; EXACT segments are replayed term by term with the exact
-// parallel accumulation (wave_accumulate, llz_norm.h).
+// candidates) are "special": queued, re-read, evaluated with the exact exp
+// (llz_math.h) and corrected.  A segment holding a tie becomes PLAIN_TIE: its
+// ties add units that depend only on the parity of the integer it starts at.
+// Phase F+X: EXACT segments are re-read and evaluated exactly into LDS, with
+// per-lane prefix tables of their roundings on the grids they span.
+// Phase B: the walk's entries (runs of PLAIN segments on one grid, PLAIN_TIE
+// and EXACT segments).
+// Phase C: one wave walks the entries in index order: runs add their integer
+// sums while the running sum stays in their binade; an EXACT segment is
+// resolved from its tables, replaying in floating point only the lane that
+// holds an event (a tie or a binade crossing); anything the tables do not
+// cover takes the exact parallel accumulation (wave_accumulate, llz_norm.h).
 //
 // Error bound of the estimate relative to the reference's term e =
 // exp(RN(RN(v - m) / T)) for the terms that can round to a non-zero integer
@@ -221,8 +227,7 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return __uint_as_float(lane_readlast(r));
 }
 
-// A wave's total of v in lane 63 only (wave_fold_f32; wave_total_f32 reads
-// it into a scalar register), in six folded DPP additions (row
+// A wave's total of v in lane 63 only, in six folded DPP additions (row
 // sums, then rows 0-1 and 2-3, then all four; the other lanes end with
 // partial sums).  The order of the additions differs from a lane-order
 // scan: for estimates only.
@@ -242,9 +247,7 @@ __device__ __forceinline__ float wave_fold_f32(float v) {
   s = dpp_add_f32<0x143>(s);  // row_bcast:31: lane 63 holds all four rows
   return s;
 }
-__device__ __forceinline__ float wave_total_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_fold_f32(v)), 63));
-}
+
 
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {

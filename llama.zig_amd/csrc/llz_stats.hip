@@ -763,8 +763,9 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     // ---- phase S: integer sums of PLAIN segments, four segments per step.
     // A lane whose roundings a segment cannot certify (its lower and upper
     // bracket sums differ, or a term reaches tspec: large terms and
-    // candidates) is queued as (position of its first term, the segment's
-    // integer sum before it), and the queue is settled when full.
+    // candidates) is queued as the position of its first term and the parity
+    // of the segment's integer sum before it; the queue is settled in phase
+    // F+X.
     int qn = 0;
     float4 v4q[2];
     auto reread = [&](int cnt) {  // the logits of the first cnt queued lanes (wave-uniform)
