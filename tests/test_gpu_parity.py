@@ -188,6 +188,35 @@ def test_edge_configs(cuda, n, name, params):
     compare_rows(x, params, u, g)
 
 
+@pytest.mark.parametrize("n", [100004, 129020, 129024, 129028])
+def test_long_rows_lds_segments(cuda, n):
+    """Rows long enough for LDS-resident segments (more than 45 segments a
+    wave), with a partial last segment among them (100004, 129020: it is
+    read straight to LDS through the buffer resource, which returns zeros
+    past the row), the longest row the single pass holds (129024), and one
+    element more (129028: the streaming normaliser)."""
+    import torch
+
+    rows = 3
+    x = _rand_rows(rows, n, seed=n % 1000)
+    x[1, n - 1] = 12.0  # the row maximum in the last (partial) segment
+    p = Params(temperature=1.0, top_k=40, top_p=0.95, min_p=0.05, repetition_penalty=1.0)
+    u = llz.rng_uniforms(n % 97, rows)
+    cfg = llz.SamplerConfig.of(p)
+    ws = torch.zeros(llz.workspace_bytes(rows, n, cfg), dtype=torch.uint8, device=cuda)
+    res = llz.sample_rows(torch.from_numpy(x).to(cuda), cfg, torch.from_numpy(u).to(cuda), kept_cap=256,
+                          stats=True, workspace=ws)
+    torch.cuda.synchronize()
+    status = ws[: rows * 4].view(torch.int32).cpu().numpy()  # per-row path bits (workspace offset 0)
+    fast = (status & 8) == 0
+    assert fast.all() if n <= 129024 else not fast.any(), status
+    g = dict(tokens=res.tokens.cpu().numpy().view(np.uint32), consumed=res.consumed.cpu().numpy(),
+             kept_count=res.kept_count.cpu().numpy().view(np.uint32),
+             kept_ids=res.kept_ids.cpu().numpy().view(np.uint32),
+             kept_probs=res.kept_probs.cpu().numpy(), stats=res.row_stats.cpu().numpy(), cap=256)
+    compare_rows(x, p, u, g)
+
+
 def test_repetition_penalty(cuda):
     n, rows = 5000, 4
     x = _rand_rows(rows, n, seed=3)
