@@ -592,8 +592,9 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         d[k] = q;
         seg_sum(k, q);
       }
+      // (issue() ends with a scheduling barrier: segments stay in order while
+      // loads are issued; the last kLoadWindow may interleave)
       if (i + kLoadWindow < SPWMAX) issue(i + kLoadWindow);
-      __builtin_amdgcn_sched_barrier(0);  // one segment at a time: bounded live ranges
     }
   } else {
     // element loads, all in flight at once (guarded loads are waited for
