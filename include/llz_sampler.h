@@ -147,8 +147,9 @@ int llz_debug_math(const float *d_in, float *d_exp, float *d_log, int64_t n, voi
 /* Measurement hook (no counterpart in the reference): while set, every
  * llz_sample_rows call records `begin_event` right before and `end_event`
  * right after its per-row sampling kernel, on the call's stream (both are
- * hipEvent_t).  NULL, NULL clears.  Process-wide, not thread-safe; used by
- * the benchmark to time the dominant kernel alone. */
+ * hipEvent_t).  NULL, NULL clears.  Process-wide, not thread-safe; times
+ * single launches (each pair of events adds a few microseconds of stream
+ * time, so throughput runs leave it cleared). */
 int llz_debug_kernel_events(void *begin_event, void *end_event);
 
 /* Name of a return code. */
