@@ -1,17 +1,24 @@
 #!/usr/bin/env python3
-"""Headline benchmark: sampled rows/s and achieved HBM GB/s on the batch of
-256 rows x 128256 vocab fp32 (configuration 2's logits and filter chain:
-T 1.0, top-k 40, top-p 0.95, min-p 0.05), one MI355X.
+"""Sampling-chain benchmark: sampled rows/s and achieved HBM GB/s, one MI355X.
+
+With no flags it measures the headline workload -- 256 rows x 128256 vocab
+fp32 with configuration 2's logits and filter chain (T 1.0, top-k 40, top-p
+0.95, min-p 0.05) -- and prints ONE JSON line.  ``--workload c1 .. c5`` (or
+``all``) measures the reference's other configurations, one JSON line each.
 
 A step is one llz_sample_rows call over one resident batch.  Inputs rotate
-over enough distinct batches that each step reads its logits from HBM, not
-from the 256 MB Infinity Cache.  Prints one JSON line.
+over enough distinct device buffers that each step reads its logits from HBM,
+not from the 256 MB Infinity Cache.  Each line carries the roofline of the
+step's only kernel (k_stats), the fraction of rows on each path, and the CPU
+baseline (the reference sampler restated in C) timed on this host with one
+thread and with the host's share of threads.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 
@@ -22,28 +29,45 @@ for _p in (os.path.join(ROOT, "llama.zig_amd"), os.path.join(ROOT, "tests")):
 
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, AMD public specification
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+HOST_THREADS = 16       # the CPU share of one GPU on the GPU box
+METRIC = "sampled rows/sec + achieved HBM GB/s, batch 256 x vocab 128256 fp32"
 
 
-def cpu_baseline(w, x_host, u_host, rows: int, threads: int) -> dict:
-    """The oracle (sampler.zig restated in C, -O2, no fast-math) on host cores."""
-    import numpy as np
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
 
+
+def cpu_baseline(w, x_host, u_host, threads: int, budget_s: float) -> dict:
+    """The oracle (sampler.zig restated in C, -O2, no fast-math) on host cores:
+    whole batches of the workload's first rows, repeated until budget_s."""
     import oracle_lib as O
 
-    reps = max(1, rows // x_host.shape[0])
+    rows = x_host.shape[0]
     n_rows = 0
     t0 = time.perf_counter()
-    for _ in range(reps):
+    while True:
         O.sample_rows(x_host, w.params, u_host, threads=threads)
-        n_rows += x_host.shape[0]
-    dt = time.perf_counter() - t0
+        n_rows += rows
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            break
     return {
         "value": round(n_rows / dt, 2),
         "unit": "rows/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n_rows} rows of the {w.name} batch ({w.vocab} vocab), sampler.zig restated in C "
-                  f"(oracle/llz_oracle.c), rows split over {threads} threads, {dt:.2f} s wall",
+        "cpu_model": cpu_model(),
+        "nproc": os.cpu_count(),
+        "sample": f"{n_rows} rows ({rows} distinct) of the {w.name} workload ({w.vocab} vocab), "
+                  f"sampler.zig restated in C (oracle/llz_oracle.c, std stable sort in place of Zig's "
+                  f"block sort), rows split over {threads} thread(s), {dt:.2f} s wall",
     }
 
 
@@ -63,16 +87,179 @@ def calibrate_copy(mib: int) -> int:
     return 0
 
 
+def c1_latency(w, x_host, u_host, reps: int) -> dict:
+    """Configuration 1 is one row per decode step (main.zig:667): its latency
+    per call, for the device-resident batched entry point and for the host
+    Sampler that takes host logits (H2D copy, sampling, D2H, synchronisation)."""
+    import numpy as np
+    import torch
+
+    import llz
+
+    dev = torch.device("cuda:0")
+    cfg = llz.SamplerConfig.of(w.params)
+    x = torch.from_numpy(x_host[:1]).to(dev)
+    u = torch.from_numpy(u_host[:1].copy()).to(dev)
+    ws = torch.empty(llz.workspace_bytes(1, w.vocab, cfg), dtype=torch.uint8, device=dev)
+    tok = torch.empty(1, dtype=torch.int32, device=dev)
+    con = torch.empty(1, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    for _ in range(20):
+        llz.sample_rows(x, cfg, u, workspace=ws, stream=stream, out=(tok, con))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        llz.sample_rows(x, cfg, u, workspace=ws, stream=stream, out=(tok, con))
+        torch.cuda.synchronize()
+    dev_us = (time.perf_counter() - t0) * 1e6 / reps
+
+    s = llz.Sampler(llz.SamplerConfig.of(w.params, seed=0))
+    row = np.ascontiguousarray(x_host[0])
+    for _ in range(20):
+        s.sample(row)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        s.sample(row)
+    host_us = (time.perf_counter() - t0) * 1e6 / reps
+    s.close()
+    return {"device_rows_us_per_call": round(dev_us, 2), "host_sampler_us_per_call": round(host_us, 2),
+            "reps": reps,
+            "note": "one row per call, each call synchronised: llz_sample_rows on device logits, and "
+                    "llz_sampler_sample on host logits (513 KB H2D copy + sampling + token D2H)"}
+
+
+def run_workload(name: str, steps: int, warmup: int, args) -> dict:
+    import numpy as np
+    import torch
+
+    import llz
+    import oracle_lib as O
+    from llz.workloads import WORKLOADS, algorithmic_bytes
+
+    w = WORKLOADS[name]
+    dev = torch.device("cuda:0")
+    rows, vocab = w.rows, w.vocab
+    batch_bytes = rows * vocab * 4
+    cfg = llz.SamplerConfig.of(w.params)
+
+    # one batch generated on the host; the other buffers hold its rows rotated
+    # (same data, other addresses: each step reads memory the previous steps
+    # did not leave in the Infinity Cache)
+    nbuf = max(2, -(-2 * MALL_BYTES // batch_bytes) + 1)
+    x_host = w.logits(rows)
+    u_host = llz.rng_uniforms(w.uniform_seed, rows)
+    x0 = torch.from_numpy(x_host).to(dev)
+    u0 = torch.from_numpy(u_host).to(dev)
+    xs = [torch.roll(x0, shifts=b * max(1, rows // nbuf), dims=0).contiguous() for b in range(nbuf)]
+    us = [torch.roll(u0, shifts=b * max(1, rows // nbuf), dims=0).contiguous() for b in range(nbuf)]
+    del x0
+    ws = torch.empty(llz.workspace_bytes(rows, vocab, cfg), dtype=torch.uint8, device=dev)
+    tokens = torch.empty(rows, dtype=torch.int32, device=dev)
+    consumed = torch.empty(rows, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        b = i % nbuf
+        llz.sample_rows(xs[b], cfg, us[b], workspace=ws, stream=stream, out=(tokens, consumed))
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # parity spot check of the timed configuration against the oracle, and
+    # the path each row of every buffer takes
+    res = llz.sample_rows(xs[0], cfg, us[0], path=True, workspace=ws, stream=stream)
+    torch.cuda.synchronize()
+    tok0 = res.tokens.cpu().numpy().view(np.uint32)
+    con0 = res.consumed.cpu().numpy()
+    nchk = min(8, rows)
+    o_tok, o_con, _ = O.sample_rows(x_host[:nchk], w.params, u_host[:nchk], threads=HOST_THREADS)
+    parity_ok = bool(np.array_equal(tok0[:nchk], o_tok) and np.array_equal(con0[:nchk], o_con))
+    paths = res.row_path.cpu().numpy().view(np.uint32)
+    frac = lambda bit: round(float(np.mean((paths & bit) != 0)), 4)  # noqa: E731
+    path_fracs = {"stream_norm": frac(llz.PATH_STREAM_NORM), "full_sort": frac(llz.PATH_FULL_SORT),
+                  "entropy": frac(llz.PATH_ENTROPY), "sum_le0": frac(llz.PATH_SUM_LE0),
+                  "single_pass": round(float(np.mean((paths & (llz.PATH_STREAM_NORM | llz.PATH_FULL_SORT)) == 0)), 4)}
+
+    # The timed region: K steps back to back on one stream, bracketed by HIP
+    # events on that stream.  k_stats is the only kernel of a step, so the
+    # events' interval over K is its average launch duration (the host
+    # enqueues faster than the GPU runs, so launches follow each other with
+    # no idle gap).
+    cb = torch.cuda.Event(enable_timing=True)
+    ce = torch.cuda.Event(enable_timing=True)
+    for ev in (cb, ce):  # materialise the underlying HIP events
+        ev.record(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    cb.record(stream)
+    for i in range(steps):
+        step(warmup + i)
+    ce.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+
+    ms_per_step = (t1 - t0) * 1e3 / steps
+    ms_events = cb.elapsed_time(ce) / steps
+    alg = algorithmic_bytes(rows, vocab)
+    achieved = alg / (ms_events * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"k_stats_{name}_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    out = {
+        "metric": METRIC,
+        "value": round(rows / (ms_per_step * 1e-3), 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": f"synthetic ({w.text}); numpy default_rng per row; inputs resident in HBM, "
+                f"{nbuf} rotating buffers ({nbuf * batch_bytes / 2**20:.0f} MiB) to defeat the Infinity Cache",
+        "config": {"workload": w.name, "rows": rows, "vocab": vocab, "temperature": w.params.temperature,
+                   "top_k": w.params.top_k, "top_p": w.params.top_p, "min_p": w.params.min_p,
+                   "typical_p": w.params.typical_p, "parallelism": "none (1 GPU)"},
+        "gbps": round(alg / (ms_per_step * 1e-3) / 1e9, 1),
+        "ms_per_step_events": round(ms_events, 5),
+        "roofline": {"bound": "hbm", "kernel": "k_stats", "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
+                     "traffic": traffic, "kernel_ms": round(ms_events, 5),
+                     "algorithmic_bytes": alg},
+        "paths": path_fracs,
+        "parity_spot_check": {"rows": nchk, "ok": parity_ok},
+    }
+    if name == "c1":
+        out["latency"] = c1_latency(w, x_host, u_host, reps=200)
+    del xs, us, ws
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        # 64 rows (a batch of fewer rows is repeated), so that every thread has rows
+        reps = -(-64 // min(rows, 64))
+        sample = np.ascontiguousarray(np.tile(x_host[: min(rows, 64)], (reps, 1))[:64])
+        usample = np.ascontiguousarray(np.tile(u_host[: min(rows, 64)], reps)[:64])
+        out["cpu_baseline"] = cpu_baseline(w, sample, usample, HOST_THREADS, args.cpu_seconds)
+        out["cpu_baseline_1core"] = cpu_baseline(w, sample[: min(16, sample.shape[0])],
+                                                 usample[: min(16, sample.shape[0])], 1, args.cpu_seconds)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--workload", default="headline")
-    ap.add_argument("--cpu-rows", type=int, default=2048)
+    ap.add_argument("--workload", default="headline",
+                    help="headline (default), c1 .. c5, or all (one JSON line each)")
+    ap.add_argument("--cpu-seconds", type=float, default=5.0,
+                    help="wall-clock budget of each CPU baseline mode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "k_stats_headline_traffic.json"),
-                    help="HBM traffic per launch measured with rocprofv3 --pmc (JSON), if present")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark: launch a plain device copy of MIB MiB a few times, "
                          "the known-size reference for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
@@ -87,107 +274,22 @@ def main() -> int:
                           "n_gpus": args.gpus}))
         return 2
 
-    import numpy as np
-    import torch
+    from llz.workloads import WORKLOADS
 
-    import llz
-    from llz.workloads import WORKLOADS, algorithmic_bytes
-
-    w = WORKLOADS[args.workload]
-    dev = torch.device("cuda:0")
-    rows, vocab = w.rows, w.vocab
-    batch_bytes = rows * vocab * 4
-    nbuf = max(3, -(-2 * MALL_BYTES // batch_bytes) + 1)
-    cfg = llz.SamplerConfig.of(w.params)
-
-    x_host = [w.logits(rows, first_row=b * rows) for b in range(nbuf)]
-    u_all = llz.rng_uniforms(w.uniform_seed, rows * nbuf)
-    xs = [torch.from_numpy(x).to(dev) for x in x_host]
-    us = [torch.from_numpy(u_all[b * rows:(b + 1) * rows].copy()).to(dev) for b in range(nbuf)]
-    ws = torch.empty(llz.workspace_bytes(rows, vocab, cfg), dtype=torch.uint8, device=dev)
-    tokens = torch.empty(rows, dtype=torch.int32, device=dev)
-    consumed = torch.empty(rows, dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream()
-
-    def step(i):
-        b = i % nbuf
-        llz.sample_rows(xs[b], cfg, us[b], workspace=ws, stream=stream, out=(tokens, consumed))
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # parity spot check of the timed configuration against the oracle
-    import oracle_lib as O
-
-    step(0)
-    torch.cuda.synchronize()
-    tok0 = tokens.cpu().numpy().view(np.uint32)
-    nchk = min(8, rows)
-    o_tok, o_con, _ = O.sample_rows(x_host[0][:nchk], w.params, u_all[:nchk])
-    parity_ok = bool(np.array_equal(tok0[:nchk], o_tok) and
-                     np.array_equal(consumed.cpu().numpy()[:nchk], o_con))
-
-    # The timed region: K steps back to back on one stream, bracketed by HIP
-    # events on that stream.  k_stats is the only kernel of a step, so the
-    # events' interval over K is its average launch duration (the host
-    # enqueues faster than the GPU runs, so launches follow each other with
-    # no idle gap).  Events around every launch would add about 7 us a step
-    # to the stream, so the per-launch hook (llz.set_kernel_events) is not
-    # used here.
-    cb = torch.cuda.Event(enable_timing=True)
-    ce = torch.cuda.Event(enable_timing=True)
-    for ev in (cb, ce):  # materialise the underlying HIP events
-        ev.record(stream)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    cb.record(stream)
-    for i in range(args.steps):
-        step(args.warmup + i)
-    ce.record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
-    ms_events = cb.elapsed_time(ce) / args.steps
-    k_avg = ms_events
-    alg = algorithmic_bytes(rows, vocab)
-    achieved = alg / (k_avg * 1e-3) / 1e9
-    traffic = None
-    if os.path.exists(args.traffic):
-        with open(args.traffic) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-
-    out = {
-        "metric": "sampled rows/sec + achieved HBM GB/s, batch 256 x vocab 128256 fp32",
-        "value": round(rows / (ms_per_step * 1e-3), 1),
-        "unit": "rows/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (numpy default_rng, configuration 2 family); inputs resident in HBM, "
-                f"{nbuf} rotating batches ({nbuf * batch_bytes / 2**20:.0f} MiB) to defeat the Infinity Cache",
-        "config": {"workload": w.name, "rows": rows, "vocab": vocab, "temperature": w.params.temperature,
-                   "top_k": w.params.top_k, "top_p": w.params.top_p, "min_p": w.params.min_p,
-                   "typical_p": w.params.typical_p, "parallelism": "none (1 GPU)"},
-        "gbps": round(alg / (ms_per_step * 1e-3) / 1e9, 1),
-        "ms_per_step_events": round(ms_events, 5),
-        "roofline": {"bound": "hbm", "kernel": "k_stats", "achieved": round(achieved, 1),
-                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
-                     "traffic": traffic, "kernel_ms": round(k_avg, 5),
-                     "algorithmic_bytes": alg},
-        "parity_spot_check": {"rows": nchk, "ok": parity_ok},
-    }
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(w, x_host[0], u_all[:rows], args.cpu_rows,
-                                           threads=min(16, os.cpu_count() or 1))
-    print(json.dumps(out), flush=True)
-    return 0 if parity_ok else 1
+    names = ["headline", "c1", "c2", "c3", "c4", "c5"] if args.workload == "all" else [args.workload]
+    head_rows = WORKLOADS["headline"].rows * WORKLOADS["headline"].vocab
+    ok = True
+    for name in names:
+        w = WORKLOADS[name]
+        # the headline takes the given K; the others scale K by their batch size
+        # (at least 10 steps), so each line times a comparable amount of work
+        steps = args.steps if name == "headline" else max(10, args.steps * head_rows // (w.rows * w.vocab))
+        steps = min(steps, args.steps) if name != "c1" else min(args.steps, 200)
+        warmup = min(args.warmup, max(2, steps // 4))
+        out = run_workload(name, steps, warmup, args)
+        ok = ok and out["parity_spot_check"]["ok"]
+        print(json.dumps(out), flush=True)
+    return 0 if ok else 1
 
 
 if __name__ == "__main__":

@@ -55,11 +55,12 @@ typedef struct llz_sampler_config {
     float top_p;
     float min_p;
     float typical_p;
+    uint32_t reserved;          /* padding before the u64 (an extern struct of the same
+                                   fields in the same order has it too); must be 0 */
+    uint64_t seed;
     uint32_t repetition_window;
     float repetition_penalty;
-    uint32_t reserved;          /* must be 0 */
-    uint64_t seed;
-} llz_sampler_config;
+} llz_sampler_config;           /* 40 bytes, fields in sampler.zig:4-13's order */
 
 /* Fills `cfg` with SamplerConfig's defaults (sampler.zig:4-13). */
 void llz_sampler_config_default(llz_sampler_config *cfg);
@@ -72,7 +73,17 @@ typedef struct llz_sample_extras {
     int32_t kept_cap;           /* capacity per row of the two arrays above                 */
     int32_t reserved;
     float *d_row_stats;         /* [rows][4]: max logit, normaliser, entropy, total kept     */
+    uint32_t *d_row_path;       /* [rows] the path each row took (LLZ_PATH_* bits)           */
 } llz_sample_extras;
+
+/* Bits of d_row_path (diagnostics; a row with none took the single-pass path). */
+enum {
+    LLZ_PATH_SUM_LE0 = 1,        /* sum <= 0 exit (sampler.zig:89)                         */
+    LLZ_PATH_ENTROPY = 2,        /* typical-p entropy pass ran (sampler.zig:128-154)       */
+    LLZ_PATH_FULL_SORT = 4,      /* kept set beyond the candidate list: full-row sort      */
+    LLZ_PATH_STREAM_NORM = 8,    /* normaliser not certified in one pass: streaming pass   */
+    LLZ_PATH_ERROR = (int)0x80000000u
+};
 
 /* Bytes of device workspace llz_sample_rows needs for this shape and
  * configuration (0 on invalid input).  n_prev is the repetition window
@@ -133,6 +144,17 @@ void llz_sampler_destroy(llz_sampler *s);
  * sampler.zig:162. */
 int llz_sampler_sample(llz_sampler *s, const float *logits, int32_t n,
                        const uint32_t *prev_tokens, int32_t n_prev, uint32_t *token);
+
+/* Sampler.sample for one row with the uniform supplied by the caller: for a
+ * caller that keeps the reference's PRNG itself (the Zig binding keeps
+ * std.Random.DefaultPrng and draws random.float(f32) before the call).
+ * *consumed is 1 when the row reached the draw (sampler.zig:162) and so used
+ * u, 0 when it left the chain before it (temperature <= 0, sum <= 0, empty
+ * kept set): the caller then undoes its draw.  The sampler's own PRNG is
+ * neither used nor advanced.  Synchronous. */
+int llz_sampler_sample_uniform(llz_sampler *s, const float *logits, int32_t n,
+                               const uint32_t *prev_tokens, int32_t n_prev, float u,
+                               uint32_t *token, uint8_t *consumed);
 
 /* PRNG state snapshot / restore (checkpointing a generation). */
 void llz_sampler_get_state(const llz_sampler *s, uint64_t state[4]);

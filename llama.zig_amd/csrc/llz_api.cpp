@@ -1,6 +1,7 @@
 // llz_api.cpp -- C ABI of libllzsample.so (declared in include/llz_sampler.h).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -104,7 +105,7 @@ int llz_argmax_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   int rc = check_common(d_logits, row_stride, rows, vocab);
   if (rc) return rc;
   if (!d_tokens) return LLZ_E_INVALID_ARG;
-  hipError_t e = launch_argmax(d_logits, row_stride, rows, vocab, d_tokens, nullptr, nullptr,
+  hipError_t e = launch_argmax(d_logits, row_stride, rows, vocab, d_tokens, nullptr, nullptr, nullptr,
                                (hipStream_t)stream);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }
@@ -126,7 +127,8 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   // sampler.zig:50 -- greedy rows never draw
   if (cfg->temperature <= 0.0f) {
     hipError_t e = launch_argmax(d_logits, row_stride, rows, vocab, d_tokens, d_consumed,
-                                 extras ? extras->d_kept_count : nullptr, st);
+                                 extras ? extras->d_kept_count : nullptr, extras ? extras->d_row_path : nullptr,
+                                 st);
     return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
   }
   if (!d_uniforms) return LLZ_E_INVALID_ARG;
@@ -141,8 +143,11 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   int64_t src_stride = row_stride;
   if (L.has_penal) {
     float* pen = (float*)(ws + L.penal);
+    // sampler.zig:60: window = min(len, repetition_window), taken before any
+    // narrowing (a u32 window of 2^31 or more means the whole history)
+    const int window = (int)std::min<uint64_t>((uint64_t)cfg->repetition_window, (uint64_t)n_prev);
     hipError_t e = launch_penalty(d_logits, row_stride, rows, vocab, d_prev_tokens, n_prev, prev_stride,
-                                  (int)cfg->repetition_window, cfg->repetition_penalty, pen, st);
+                                  window, cfg->repetition_penalty, pen, st);
     if (e != hipSuccess) return LLZ_E_HIP;
     src = pen;
     src_stride = vocab;
@@ -183,7 +188,7 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
     Q.kept_probs = extras->d_kept_probs;
     Q.row_stats = extras->d_row_stats;
   }
-  Q.status = (uint32_t*)(ws + L.status);
+  Q.status = (extras && extras->d_row_path) ? extras->d_row_path : (uint32_t*)(ws + L.status);
   Q.cand = (uint64_t*)(ws + L.cand);
   Q.fb = (uint32_t*)(ws + L.fb);
   Q.fb_mask = (uint8_t*)(ws + L.fb_mask);
@@ -331,8 +336,10 @@ static bool is_device_ptr(const void* p) {
   return a.type == hipMemoryTypeDevice;
 }
 
-int llz_sampler_sample(llz_sampler* s, const float* logits, int32_t n, const uint32_t* prev_tokens,
-                       int32_t n_prev, uint32_t* token) {
+// One row through llz_sample_rows with the caller's uniform: token and the
+// consumed-draw flag (sampler.zig:162 reached).  Synchronous.
+static int sampler_run(llz_sampler* s, const float* logits, int32_t n, const uint32_t* prev_tokens,
+                       int32_t n_prev, float u, uint32_t* token, uint8_t* consumed) {
   if (!s || !logits || n <= 0 || !token || n_prev < 0 || (n_prev > 0 && !prev_tokens))
     return LLZ_E_INVALID_ARG;
   if (hipSetDevice(s->device) != hipSuccess) return LLZ_E_HIP;
@@ -353,11 +360,6 @@ int llz_sampler_sample(llz_sampler* s, const float* logits, int32_t n, const uin
     s->cap_prev = cp;
     s->ws_bytes = need_ws;
   }
-  // draw as if the row reached sampler.zig:162; undo below if it did not
-  uint64_t snap[4];
-  std::memcpy(snap, s->prng, sizeof(snap));
-  const float u = llz_rng_float(s->prng);
-
   const float* d_in = logits;
   if (!is_device_ptr(logits)) {
     if (hipMemcpyAsync(s->d_logits, logits, (size_t)n * sizeof(float), hipMemcpyHostToDevice,
@@ -373,21 +375,36 @@ int llz_sampler_sample(llz_sampler* s, const float* logits, int32_t n, const uin
   int rc = llz_sample_rows(d_in, n, 1, n, &s->cfg, n_prev > 0 ? s->d_prev : nullptr, n_prev, 0,
                            s->d_u, s->d_token, s->d_consumed, nullptr, s->d_ws, s->ws_bytes,
                            s->stream);
-  if (rc != LLZ_OK) {
-    std::memcpy(s->prng, snap, sizeof(snap));
-    return rc;
-  }
+  if (rc != LLZ_OK) return rc;
   uint32_t tok = 0;
-  uint8_t consumed = 0;
+  uint8_t con = 0;
   if (hipMemcpyAsync(&tok, s->d_token, sizeof(tok), hipMemcpyDeviceToHost, s->stream) != hipSuccess ||
-      hipMemcpyAsync(&consumed, s->d_consumed, 1, hipMemcpyDeviceToHost, s->stream) != hipSuccess ||
-      hipStreamSynchronize(s->stream) != hipSuccess) {
-    std::memcpy(s->prng, snap, sizeof(snap));
+      hipMemcpyAsync(&con, s->d_consumed, 1, hipMemcpyDeviceToHost, s->stream) != hipSuccess ||
+      hipStreamSynchronize(s->stream) != hipSuccess)
     return LLZ_E_HIP;
-  }
-  if (!consumed || s->cfg.temperature <= 0.0f) std::memcpy(s->prng, snap, sizeof(snap));
   *token = tok;
+  *consumed = (con != 0 && s->cfg.temperature > 0.0f) ? 1 : 0;
   return LLZ_OK;
+}
+
+int llz_sampler_sample(llz_sampler* s, const float* logits, int32_t n, const uint32_t* prev_tokens,
+                       int32_t n_prev, uint32_t* token) {
+  if (!s) return LLZ_E_INVALID_ARG;
+  // draw as if the row reached sampler.zig:162; undo it if it did not
+  uint64_t snap[4];
+  std::memcpy(snap, s->prng, sizeof(snap));
+  const float u = llz_rng_float(s->prng);
+  uint8_t consumed = 0;
+  const int rc = sampler_run(s, logits, n, prev_tokens, n_prev, u, token, &consumed);
+  if (rc != LLZ_OK || !consumed) std::memcpy(s->prng, snap, sizeof(snap));
+  return rc;
+}
+
+int llz_sampler_sample_uniform(llz_sampler* s, const float* logits, int32_t n, const uint32_t* prev_tokens,
+                               int32_t n_prev, float u, uint32_t* token, uint8_t* consumed) {
+  if (!consumed) return LLZ_E_INVALID_ARG;
+  *consumed = 0;
+  return sampler_run(s, logits, n, prev_tokens, n_prev, u, token, consumed);
 }
 
 }  // extern "C"

@@ -57,7 +57,7 @@ hipError_t launch_penalty(const float* logits, int64_t stride, int rows, int n, 
                           int n_prev, int64_t prev_stride, int window, float penalty, float* out,
                           hipStream_t st);
 hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t* tokens,
-                         uint8_t* consumed, uint32_t* kept_count, hipStream_t st);
+                         uint8_t* consumed, uint32_t* kept_count, uint32_t* path, hipStream_t st);
 hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_begin, hipEvent_t ev_end,
                          hipStream_t st);
 hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, int64_t n, hipStream_t st);

@@ -51,7 +51,8 @@ __global__ __launch_bounds__(kMaxNT) void k_penalty(const float* __restrict__ lo
 __global__ __launch_bounds__(kNT) void k_argmax(const float* __restrict__ logits, int64_t stride,
                                                 int n, uint32_t* __restrict__ tokens,
                                                 uint8_t* __restrict__ consumed,
-                                                uint32_t* __restrict__ kept_count) {
+                                                uint32_t* __restrict__ kept_count,
+                                                uint32_t* __restrict__ path) {
   __shared__ WgScratch<kNT> sh;
   int bank = 0;
   const int row = blockIdx.x;
@@ -60,6 +61,7 @@ __global__ __launch_bounds__(kNT) void k_argmax(const float* __restrict__ logits
     tokens[row] = tok;
     if (consumed) consumed[row] = 0;
     if (kept_count) kept_count[row] = 0;
+    if (path) path[row] = 0;
   }
 }
 
@@ -95,9 +97,9 @@ hipError_t launch_penalty(const float* logits, int64_t stride, int rows, int n, 
 }
 
 hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t* tokens,
-                         uint8_t* consumed, uint32_t* kept_count, hipStream_t st) {
+                         uint8_t* consumed, uint32_t* kept_count, uint32_t* path, hipStream_t st) {
   hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(kNT), 0, st, logits, stride, n, tokens, consumed,
-                     kept_count);
+                     kept_count, path);
   return hipGetLastError();
 }
 

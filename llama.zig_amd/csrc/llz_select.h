@@ -245,7 +245,7 @@ __device__ float row_normaliser(const float* xr, int n, const RowParams& P, Samp
   constexpr int NC = W * kSub;      // sub-chunks per group
   static_assert(NC <= kWave, "one wave scans a group's sub-chunk sums");
   NormShared<kNT>& ns = sh.u.norm;
-  const int t = (int)threadIdx.x, lane = lane_id(), w = wave_id();
+  const int lane = lane_id(), w = wave_id();
   const bool t1 = (P.flags & kFlagTIsOne) != 0;
   const bool vec = (P.flags & kFlagVecSrc) != 0;
   const int p0 = min(n, kPrologue);

@@ -36,7 +36,8 @@ LLZ_E_NO_DEVICE = -5
 EXPORTED = (
     "llz_sampler_config_default", "llz_sample_workspace_bytes", "llz_sample_rows",
     "llz_argmax_rows", "llz_rng_seed", "llz_rng_next", "llz_rng_float", "llz_rng_uniforms",
-    "llz_sampler_create", "llz_sampler_destroy", "llz_sampler_sample", "llz_sampler_get_state",
+    "llz_sampler_create", "llz_sampler_destroy", "llz_sampler_sample", "llz_sampler_sample_uniform",
+    "llz_sampler_get_state",
     "llz_sampler_set_state", "llz_debug_math", "llz_debug_kernel_events", "llz_strerror",
 )
 
@@ -51,8 +52,8 @@ class LlzError(RuntimeError):
 class CConfig(C.Structure):
     _fields_ = [
         ("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
-        ("min_p", C.c_float), ("typical_p", C.c_float), ("repetition_window", C.c_uint32),
-        ("repetition_penalty", C.c_float), ("reserved", C.c_uint32), ("seed", C.c_uint64),
+        ("min_p", C.c_float), ("typical_p", C.c_float), ("reserved", C.c_uint32),
+        ("seed", C.c_uint64), ("repetition_window", C.c_uint32), ("repetition_penalty", C.c_float),
     ]
 
 
@@ -60,6 +61,7 @@ class CExtras(C.Structure):
     _fields_ = [
         ("d_kept_count", C.c_void_p), ("d_kept_ids", C.c_void_p), ("d_kept_probs", C.c_void_p),
         ("kept_cap", C.c_int32), ("reserved", C.c_int32), ("d_row_stats", C.c_void_p),
+        ("d_row_path", C.c_void_p),
     ]
 
 
@@ -78,8 +80,8 @@ class SamplerConfig:
 
     def to_c(self) -> CConfig:
         return CConfig(float(self.temperature), int(self.top_k), float(self.top_p),
-                       float(self.min_p), float(self.typical_p), int(self.repetition_window),
-                       float(self.repetition_penalty), 0, int(self.seed))
+                       float(self.min_p), float(self.typical_p), 0, int(self.seed),
+                       int(self.repetition_window), float(self.repetition_penalty))
 
     @classmethod
     def of(cls, params, seed: int = 0) -> "SamplerConfig":
@@ -121,6 +123,9 @@ def _lib():
         L.llz_sampler_sample.argtypes = [vp, vp, i32, C.POINTER(C.c_uint32), i32,
                                          C.POINTER(C.c_uint32)]
         L.llz_sampler_sample.restype = C.c_int
+        L.llz_sampler_sample_uniform.argtypes = [vp, vp, i32, C.POINTER(C.c_uint32), i32, C.c_float,
+                                                 C.POINTER(C.c_uint32), C.POINTER(C.c_uint8)]
+        L.llz_sampler_sample_uniform.restype = C.c_int
         L.llz_sampler_get_state.argtypes = [vp, C.POINTER(u64)]
         L.llz_sampler_get_state.restype = None
         L.llz_sampler_set_state.argtypes = [vp, C.POINTER(u64)]
@@ -199,10 +204,15 @@ class SampleResult:
     kept_ids: Optional[object] = None
     kept_probs: Optional[object] = None
     row_stats: Optional[object] = None
+    row_path: Optional[object] = None  # torch.int32 [rows], LLZ_PATH_* bits
+
+
+PATH_SUM_LE0, PATH_ENTROPY, PATH_FULL_SORT, PATH_STREAM_NORM = 1, 2, 4, 8
 
 
 def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, kept_cap: int = 0,
-                stats: bool = False, workspace=None, stream=None, out=None) -> SampleResult:
+                stats: bool = False, path: bool = False, workspace=None, stream=None,
+                out=None) -> SampleResult:
     """Batched Sampler.sample over device rows.
 
     logits: float32 CUDA tensor [rows, vocab] (rows may be strided);
@@ -217,13 +227,21 @@ def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, kept_
         raise ValueError("logits rows must be contiguous")
     rows, vocab = logits.shape
     dev = logits.device
-    if uniforms.dtype != torch.float32 or not uniforms.is_cuda or uniforms.numel() < rows:
-        raise ValueError("uniforms must be a float32 CUDA tensor with one value per row")
+    if (uniforms.dtype != torch.float32 or not uniforms.is_cuda or uniforms.numel() < rows
+            or not uniforms.is_contiguous()):
+        raise ValueError("uniforms must be a contiguous float32 CUDA tensor with one value per row")
     n_prev, prev_stride, prev_ptr = 0, 0, None
     if prev_tokens is not None and prev_tokens.numel() > 0:
+        # token ids are u32 (tokenizer.zig:5): int32 / uint32 storage, on the device
+        if not prev_tokens.is_cuda or prev_tokens.dtype not in (torch.int32, getattr(torch, "uint32", torch.int32)):
+            raise ValueError("prev_tokens must be an int32 or uint32 CUDA tensor")
+        if prev_tokens.dim() not in (1, 2) or prev_tokens.stride(-1) != 1:
+            raise ValueError("prev_tokens must be 1-D or 2-D with contiguous rows")
         if prev_tokens.dim() == 1:
             n_prev, prev_stride = prev_tokens.shape[0], 0
         else:
+            if prev_tokens.shape[0] != rows:
+                raise ValueError("2-D prev_tokens needs one history row per logit row")
             n_prev, prev_stride = prev_tokens.shape[1], prev_tokens.stride(0)
         prev_ptr = prev_tokens.data_ptr()
     if out is None:
@@ -233,8 +251,11 @@ def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, kept_
         tokens, consumed = out
     res = SampleResult(tokens, consumed)
     ex = None
-    if kept_cap > 0 or stats:
+    if kept_cap > 0 or stats or path:
         ex = CExtras()
+        if path:
+            res.row_path = torch.empty(rows, dtype=torch.int32, device=dev)
+            ex.d_row_path = res.row_path.data_ptr()
         res.kept_count = torch.empty(rows, dtype=torch.int32, device=dev)
         ex.d_kept_count = res.kept_count.data_ptr()
         if kept_cap > 0:
@@ -310,6 +331,20 @@ class Sampler:
                                        prev.shape[0], C.byref(tok))
         _check(rc, "llz_sampler_sample")
         return int(tok.value)
+
+    def sample_uniform(self, logits, u: float, prev_tokens=()) -> Tuple[int, bool]:
+        """One row with the caller's uniform: (token, consumed-draw flag)."""
+        prev = np.ascontiguousarray(np.asarray(prev_tokens, dtype=np.uint32))
+        if isinstance(logits, np.ndarray):
+            x = np.ascontiguousarray(logits, dtype=np.float32)
+            ptr, n = x.ctypes.data, x.shape[0]
+        else:
+            ptr, n = logits.data_ptr(), logits.numel()
+        tok, con = C.c_uint32(), C.c_uint8()
+        rc = _lib().llz_sampler_sample_uniform(self._h, ptr, n, prev.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                               prev.shape[0], C.c_float(u), C.byref(tok), C.byref(con))
+        _check(rc, "llz_sampler_sample_uniform")
+        return int(tok.value), bool(con.value)
 
     @property
     def state(self) -> Tuple[int, int, int, int]:

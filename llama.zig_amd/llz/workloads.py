@@ -96,7 +96,9 @@ WORKLOADS: Dict[str, Workload] = {
     "c1": Workload(
         "c1", 1, 128256,
         Params(temperature=0.8, top_k=0, top_p=0.9, min_p=0.0, typical_p=1.0, **_NO_REP),
-        data_seed=0, uniform_seed=0, gen_row=_c1_row,
+        # sampler seed 0: Sampler.init seeds DefaultPrng with 0xDEADBEEF
+        # instead (sampler.zig:22)
+        data_seed=0, uniform_seed=0xDEADBEEF, gen_row=_c1_row,
         text="1 x 128256, N(0,2) + 8 tokens at +12; T 0.8, top-p 0.9 (sampler.zig defaults)"),
     "c2": Workload(
         "c2", 64, 128256,
