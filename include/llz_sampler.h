@@ -65,6 +65,19 @@ typedef struct llz_sampler_config {
 /* Fills `cfg` with SamplerConfig's defaults (sampler.zig:4-13). */
 void llz_sampler_config_default(llz_sampler_config *cfg);
 
+/* The decode loop's post-processing of the final logits before the sampler
+ * sees them (main.zig:653-666), applied by the kernels as they read each
+ * logit (the caller's rows are not written):
+ *   final_logit_softcapping > 0:          v = tanh(v / s) * s   (f32 std.math.tanh)
+ *   logit_scale != 1 and logit_scale != 0: v = v * RN(1 / logit_scale)
+ * A NULL pointer, or {0, 1}, leaves the logits as they are.  Mirrors the
+ * model config fields main.zig reads (cfg.final_logit_softcapping,
+ * cfg.logit_scale). */
+typedef struct llz_logit_post {
+    float final_logit_softcapping;
+    float logit_scale;
+} llz_logit_post;
+
 /* Optional per-row outputs of llz_sample_rows.  Any pointer may be NULL. */
 typedef struct llz_sample_extras {
     uint32_t *d_kept_count;     /* [rows] size of the final kept set                        */
@@ -93,7 +106,11 @@ size_t llz_sample_workspace_bytes(int32_t rows, int32_t vocab, const llz_sampler
 
 /* Samples one token per row from `rows` fp32 logit rows of length `vocab`
  * (row r at d_logits + r * row_stride), replacing Sampler.sample /
- * sampleWithRandom (sampler.zig:26-28, :43-169) for a batch.
+ * sampleWithRandom (sampler.zig:26-28, :43-169) for a batch, after the
+ * decode loop's post-processing (main.zig:653-666) given by `post` (may be
+ * NULL).  The repetition penalty (sampler.zig:54-75) is applied as the rows
+ * are read when the window (min(n_prev, repetition_window)) holds at most 64
+ * tokens, else to a penalised copy in the workspace.
  *   d_prev_tokens: repetition history, n_prev ids per row, rows prev_stride
  *                  apart (prev_stride 0 = one history shared by all rows);
  *                  may be NULL when n_prev == 0.
@@ -105,17 +122,21 @@ size_t llz_sample_workspace_bytes(int32_t rows, int32_t vocab, const llz_sampler
  *                  (temperature <= 0, sum <= 0, empty kept set).  May be NULL.
  * The call is asynchronous on `stream`. */
 int llz_sample_rows(const float *d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
-                    const llz_sampler_config *cfg, const uint32_t *d_prev_tokens, int32_t n_prev,
+                    const llz_sampler_config *cfg, const llz_logit_post *post,
+                    const uint32_t *d_prev_tokens, int32_t n_prev,
                     int64_t prev_stride, const float *d_uniforms, uint32_t *d_tokens,
                     uint8_t *d_consumed, const llz_sample_extras *extras, void *d_workspace,
                     size_t workspace_bytes, void *stream);
 
-/* sampleArgmax (sampler.zig:31-41) per row: the first index of the
+/* sampleArgmax (sampler.zig:31-41) per row of the post-processed logits
+ * (`post` as for llz_sample_rows; may be NULL): the first index of the
  * strict maximum, scanning from index 0.  Replaces the greedy GPU path
- * executeTopK / topk_bda.glsl (compute_graph.zig:948-984), keeping the
- * reference sampler's tie-break.  Asynchronous on `stream`. */
+ * executeTopK / topk_bda.glsl (compute_graph.zig:948-984, which scales by
+ * 1 / logit_scale at topk_bda.glsl:38-40), keeping the reference sampler's
+ * tie-break: values that become equal after the scale keep the first index.
+ * Asynchronous on `stream`. */
 int llz_argmax_rows(const float *d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
-                    uint32_t *d_tokens, void *stream);
+                    const llz_logit_post *post, uint32_t *d_tokens, void *stream);
 
 /* ---- the reference's PRNG (std.Random.DefaultPrng, sampler.zig:17,22,162) ---- */
 
@@ -161,10 +182,12 @@ void llz_sampler_get_state(const llz_sampler *s, uint64_t state[4]);
 void llz_sampler_set_state(llz_sampler *s, const uint64_t state[4]);
 
 /* Test hook (no counterpart in the reference): evaluates the device's f32
- * exp and log -- the functions the kernels use in place of std.math.exp and
- * @log (sampler.zig:85,131,136) -- on n inputs.  d_exp / d_log may be NULL.
- * Used by the parity tests to compare the GPU math with the CPU oracle. */
-int llz_debug_math(const float *d_in, float *d_exp, float *d_log, int64_t n, void *stream);
+ * exp, log, expm1 and tanh -- the functions the kernels use in place of
+ * std.math.exp, @log (sampler.zig:85,131,136) and std.math.tanh
+ * (main.zig:656) -- on n inputs.  Any output may be NULL.  Used by the
+ * parity tests to compare the GPU math with the CPU oracle. */
+int llz_debug_math(const float *d_in, float *d_exp, float *d_log, float *d_expm1, float *d_tanh,
+                   int64_t n, void *stream);
 
 /* Measurement hook (no counterpart in the reference): while set, every
  * llz_sample_rows call records `begin_event` right before and `end_event`

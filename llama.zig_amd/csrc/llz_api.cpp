@@ -25,6 +25,26 @@ bool penalty_active(const llz_sampler_config* cfg, int32_t n_prev) {
   return cfg->repetition_penalty != 1.0f && n_prev > 0 && cfg->repetition_window > 0;
 }
 
+// sampler.zig:60: window = min(len, repetition_window), taken before any
+// narrowing (a u32 window of 2^31 or more means the whole history)
+int penalty_window(const llz_sampler_config* cfg, int32_t n_prev) {
+  return (int)std::min<uint64_t>((uint64_t)cfg->repetition_window, (uint64_t)n_prev);
+}
+
+// The penalty goes to a penalised copy when its window is too long to fuse.
+bool penalty_copy(const llz_sampler_config* cfg, int32_t n_prev) {
+  return penalty_active(cfg, n_prev) && penalty_window(cfg, n_prev) > kPenMax;
+}
+
+// kXf bits of main.zig:653-666's post-processing.
+uint32_t post_bits(const llz_logit_post* post) {
+  if (!post) return 0u;
+  uint32_t b = 0u;
+  if (post->final_logit_softcapping > 0.0f) b |= kXfCap;
+  if (post->logit_scale != 1.0f && post->logit_scale != 0.0f) b |= kXfScale;
+  return b;
+}
+
 // Workspace layout of one llz_sample_rows call.
 struct Layout {
   size_t status, cand, penal, fb, fb_mask, total;
@@ -37,7 +57,7 @@ Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int
   size_t off = 0;
   L.status = off;  off = align_up(off + r * sizeof(uint32_t));
   L.cand = off;    off = align_up(off + r * (size_t)kCandCap * sizeof(uint64_t));
-  L.has_penal = penalty_active(cfg, n_prev);
+  L.has_penal = penalty_copy(cfg, n_prev);
   L.penal = off;   if (L.has_penal) off = align_up(off + r * n * sizeof(float));
   L.fb = off;      off = align_up(off + 6 * r * n * sizeof(uint32_t));
   L.fb_mask = off; off = align_up(off + r * n);
@@ -101,17 +121,21 @@ size_t llz_sample_workspace_bytes(int32_t rows, int32_t vocab, const llz_sampler
 }
 
 int llz_argmax_rows(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
-                    uint32_t* d_tokens, void* stream) {
+                    const llz_logit_post* post, uint32_t* d_tokens, void* stream) {
   int rc = check_common(d_logits, row_stride, rows, vocab);
   if (rc) return rc;
   if (!d_tokens) return LLZ_E_INVALID_ARG;
-  hipError_t e = launch_argmax(d_logits, row_stride, rows, vocab, d_tokens, nullptr, nullptr, nullptr,
-                               (hipStream_t)stream);
+  const uint32_t xb = post_bits(post);
+  // main.zig:664: the inverse is one f32 division
+  const float inv = (xb & kXfScale) ? 1.0f / post->logit_scale : 1.0f;
+  hipError_t e = launch_argmax(d_logits, row_stride, rows, vocab, xb, post ? post->final_logit_softcapping : 0.0f,
+                               inv, d_tokens, nullptr, nullptr, nullptr, (hipStream_t)stream);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }
 
 int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
-                    const llz_sampler_config* cfg, const uint32_t* d_prev_tokens, int32_t n_prev,
+                    const llz_sampler_config* cfg, const llz_logit_post* post,
+                    const uint32_t* d_prev_tokens, int32_t n_prev,
                     int64_t prev_stride, const float* d_uniforms, uint32_t* d_tokens,
                     uint8_t* d_consumed, const llz_sample_extras* extras, void* d_workspace,
                     size_t workspace_bytes, void* stream) {
@@ -123,10 +147,13 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   if (extras && (extras->d_kept_ids || extras->d_kept_probs) && extras->kept_cap <= 0)
     return LLZ_E_INVALID_ARG;
   hipStream_t st = (hipStream_t)stream;
+  const uint32_t xb = post_bits(post);
+  const float cap = (xb & kXfCap) ? post->final_logit_softcapping : 0.0f;
+  const float inv = (xb & kXfScale) ? 1.0f / post->logit_scale : 1.0f;  // main.zig:664
 
   // sampler.zig:50 -- greedy rows never draw
   if (cfg->temperature <= 0.0f) {
-    hipError_t e = launch_argmax(d_logits, row_stride, rows, vocab, d_tokens, d_consumed,
+    hipError_t e = launch_argmax(d_logits, row_stride, rows, vocab, xb, cap, inv, d_tokens, d_consumed,
                                  extras ? extras->d_kept_count : nullptr, extras ? extras->d_row_path : nullptr,
                                  st);
     return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
@@ -141,16 +168,20 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
 
   const float* src = d_logits;
   int64_t src_stride = row_stride;
+  uint32_t xf_src = xb;
+  const bool pen_on = penalty_active(cfg, n_prev);
+  const int window = pen_on ? penalty_window(cfg, n_prev) : 0;
   if (L.has_penal) {
+    // a window too long to fuse: the penalised, post-processed copy
     float* pen = (float*)(ws + L.penal);
-    // sampler.zig:60: window = min(len, repetition_window), taken before any
-    // narrowing (a u32 window of 2^31 or more means the whole history)
-    const int window = (int)std::min<uint64_t>((uint64_t)cfg->repetition_window, (uint64_t)n_prev);
     hipError_t e = launch_penalty(d_logits, row_stride, rows, vocab, d_prev_tokens, n_prev, prev_stride,
-                                  window, cfg->repetition_penalty, pen, st);
+                                  window, cfg->repetition_penalty, xb, cap, inv, pen, st);
     if (e != hipSuccess) return LLZ_E_HIP;
     src = pen;
     src_stride = vocab;
+    xf_src = 0u;
+  } else if (pen_on) {
+    xf_src |= kXfPen;  // fused: applied as each row is read
   }
   const bool vec = ((uintptr_t)src % 16 == 0) && (src_stride % 4 == 0);
   hipError_t e = hipSuccess;
@@ -169,6 +200,13 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   P.src_stride = src_stride;
   P.orig_stride = row_stride;
   P.flags = (cfg->temperature == 1.0f ? kFlagTIsOne : 0u) | (vec ? kFlagVecSrc : 0u) | kFlagFallback;
+  P.xf_src = xf_src;
+  P.xf_orig = xb;
+  P.cap = cap;
+  P.inv_scale = inv;
+  P.rpen = cfg->repetition_penalty;
+  P.pen_w = (xf_src & kXfPen) ? window : 0;
+  P.prev_stride = prev_stride;
   // LLZ_TEST_QUEUE_CAP: a smaller special-queue chunk, so that tests reach
   // the chunked queue on ordinary rows (the kernel clamps it to its own)
   {
@@ -192,6 +230,7 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   Q.cand = (uint64_t*)(ws + L.cand);
   Q.fb = (uint32_t*)(ws + L.fb);
   Q.fb_mask = (uint8_t*)(ws + L.fb_mask);
+  Q.prev_win = (xf_src & kXfPen) ? d_prev_tokens + (n_prev - window) : nullptr;
   e = launch_sample(P, Q, g_ev_begin, g_ev_end, st);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }
@@ -202,10 +241,11 @@ int llz_debug_kernel_events(void* begin_event, void* end_event) {
   return LLZ_OK;
 }
 
-int llz_debug_math(const float* d_in, float* d_exp, float* d_log, int64_t n, void* stream) {
+int llz_debug_math(const float* d_in, float* d_exp, float* d_log, float* d_expm1, float* d_tanh, int64_t n,
+                   void* stream) {
   if (!d_in || n < 0 || n > ((int64_t)1 << 40)) return LLZ_E_INVALID_ARG;
   if (n == 0) return LLZ_OK;
-  hipError_t e = launch_math_probe(d_in, d_exp, d_log, n, (hipStream_t)stream);
+  hipError_t e = launch_math_probe(d_in, d_exp, d_log, d_expm1, d_tanh, n, (hipStream_t)stream);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }
 
@@ -372,7 +412,7 @@ static int sampler_run(llz_sampler* s, const float* logits, int32_t n, const uin
     return LLZ_E_HIP;
   if (hipMemcpyAsync(s->d_u, &u, sizeof(float), hipMemcpyHostToDevice, s->stream) != hipSuccess)
     return LLZ_E_HIP;
-  int rc = llz_sample_rows(d_in, n, 1, n, &s->cfg, n_prev > 0 ? s->d_prev : nullptr, n_prev, 0,
+  int rc = llz_sample_rows(d_in, n, 1, n, &s->cfg, nullptr, n_prev > 0 ? s->d_prev : nullptr, n_prev, 0,
                            s->d_u, s->d_token, s->d_consumed, nullptr, s->d_ws, s->ws_bytes,
                            s->stream);
   if (rc != LLZ_OK) return rc;

@@ -7,11 +7,17 @@
 namespace llz {
 
 constexpr int kCandCap = 2048;  // candidate list capacity per row (power of two)
+constexpr int kPenMax = 64;     // fused repetition penalty: window entries at most (one per lane)
 
 // RowParams.flags
 constexpr uint32_t kFlagTIsOne = 1u;    // temperature == 1.0f exactly: (v - m) / T == v - m
 constexpr uint32_t kFlagVecSrc = 2u;    // 16-byte loads are legal on the rows the chain reads
 constexpr uint32_t kFlagFallback = 4u;  // the full-row fallback buffers are present
+
+// RowParams.xf_src / xf_orig: transforms applied as a row is read
+constexpr uint32_t kXfCap = 1u;    // v = tanh(v / cap) * cap   (main.zig:653-658)
+constexpr uint32_t kXfScale = 2u;  // v *= inv_scale            (main.zig:663-666)
+constexpr uint32_t kXfPen = 4u;    // repetition penalty        (sampler.zig:54-75)
 
 // per-row status bits (diagnostics)
 constexpr uint32_t kPathSumLe0 = 1u;
@@ -35,6 +41,13 @@ struct RowParams {
   int64_t orig_stride;
   uint32_t flags;
   uint32_t qcap;  // special-queue chunk size override for tests (0: the kernel's own)
+  uint32_t xf_src;   // kXf* bits applied to reads of src (the chain's input)
+  uint32_t xf_orig;  // kXf* bits applied to reads of orig (sampleArgmax's input)
+  float cap;         // final-logit soft-cap s (kXfCap)
+  float inv_scale;   // RN(1 / logit_scale) (kXfScale)
+  float rpen;        // repetition penalty (kXfPen)
+  int32_t pen_w;     // kXfPen: window length (<= kPenMax)
+  int64_t prev_stride;
 };
 
 struct RowPtrs {
@@ -51,15 +64,18 @@ struct RowPtrs {
   uint64_t* cand;         // [rows][kCandCap] candidate list
   uint32_t* fb;           // 6 x [rows][n] u32 (fallback sort buffers)
   uint8_t* fb_mask;       // [rows][n]
+  const uint32_t* prev_win;  // kXfPen: row 0's window (its last pen_w history tokens)
 };
 
 hipError_t launch_penalty(const float* logits, int64_t stride, int rows, int n, const uint32_t* prev,
-                          int n_prev, int64_t prev_stride, int window, float penalty, float* out,
-                          hipStream_t st);
-hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t* tokens,
-                         uint8_t* consumed, uint32_t* kept_count, uint32_t* path, hipStream_t st);
+                          int n_prev, int64_t prev_stride, int window, float penalty, uint32_t xf, float cap,
+                          float inv_scale, float* out, hipStream_t st);
+hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t xf, float cap,
+                         float inv_scale, uint32_t* tokens, uint8_t* consumed, uint32_t* kept_count,
+                         uint32_t* path, hipStream_t st);
 hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_begin, hipEvent_t ev_end,
                          hipStream_t st);
-hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, int64_t n, hipStream_t st);
+hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, float* out_expm1, float* out_tanh,
+                             int64_t n, hipStream_t st);
 
 }  // namespace llz

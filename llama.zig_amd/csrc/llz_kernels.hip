@@ -1,8 +1,8 @@
 // llz_kernels.hip -- MI355X (gfx950) kernels around the fused sampling kernel
 // (llz_stats.hip):
 //   k_penalty     (optional) penalised copy of the rows   sampler.zig:54-75
+//   k_math_probe  the device exp/log/expm1/tanh (parity tests)
 //   k_argmax      greedy rows (temperature <= 0)          sampler.zig:31-41,50
-//   k_math_probe  the device exp/log (parity tests)
 #include <hip/hip_runtime.h>
 
 #include "llz_internal.h"
@@ -14,20 +14,22 @@ constexpr int kMaxNT = 256;        // threads of the k_penalty workgroups
 constexpr int kMaxPerThread = 16;  // logits per thread in k_penalty
 
 // ---------------------------------------------------------------------------
-// k_penalty: penalised copy (sampler.zig:54-75).  Each index is penalised at
-// most once even when it repeats in the window (the reference breaks out of
-// the window scan at the first match).
+// k_penalty: penalised copy (sampler.zig:54-75) of the post-processed rows
+// (main.zig:653-666), for windows longer than the fused penalty takes.
+// Each index is penalised at most once even when it repeats in the window
+// (the reference breaks out of the window scan at the first match).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kMaxNT) void k_penalty(const float* __restrict__ logits, int64_t stride,
                                                     int n, const uint32_t* __restrict__ prev,
                                                     int n_prev, int64_t prev_stride, int window,
-                                                    float penalty, float* __restrict__ out) {
+                                                    float penalty, uint32_t xf, float cap, float inv_scale,
+                                                    float* __restrict__ out) {
   const int row = blockIdx.y;
   const int seg0 = blockIdx.x * (kMaxNT * kMaxPerThread);
   const int seg1 = min(n, seg0 + kMaxNT * kMaxPerThread);
   const float* x = logits + (int64_t)row * stride;
   float* y = out + (int64_t)row * n;
-  for (int i = seg0 + (int)threadIdx.x; i < seg1; i += kMaxNT) y[i] = x[i];
+  for (int i = seg0 + (int)threadIdx.x; i < seg1; i += kMaxNT) y[i] = logit_post(x[i], xf, cap, inv_scale);
   __syncthreads();
   const uint32_t* pv = prev + (int64_t)row * prev_stride;
   const int w = min(n_prev, window);
@@ -38,8 +40,7 @@ __global__ __launch_bounds__(kMaxNT) void k_penalty(const float* __restrict__ lo
       bool first = true;
       for (int b = start; b < a; ++b) first = first && (pv[b] != tok);
       if (first) {
-        const float v = x[tok];
-        y[tok] = v > 0.0f ? v / penalty : v * penalty;
+        y[tok] = penalise(logit_post(x[tok], xf, cap, inv_scale), penalty);
       }
     }
   }
@@ -49,14 +50,16 @@ __global__ __launch_bounds__(kMaxNT) void k_penalty(const float* __restrict__ lo
 // k_argmax: one workgroup per row.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kNT) void k_argmax(const float* __restrict__ logits, int64_t stride,
-                                                int n, uint32_t* __restrict__ tokens,
+                                                int n, uint32_t xf, float cap, float inv_scale,
+                                                uint32_t* __restrict__ tokens,
                                                 uint8_t* __restrict__ consumed,
                                                 uint32_t* __restrict__ kept_count,
                                                 uint32_t* __restrict__ path) {
   __shared__ WgScratch<kNT> sh;
   int bank = 0;
   const int row = blockIdx.x;
-  const uint32_t tok = wg_argmax_row<kNT>(logits + (int64_t)row * stride, n, sh, bank);
+  const RowSrc x{logits + (int64_t)row * stride, xf & ~kXfPen, cap, inv_scale, 1.0f, nullptr};
+  const uint32_t tok = wg_argmax_row<kNT>(x, n, sh, bank);
   if (threadIdx.x == 0) {
     tokens[row] = tok;
     if (consumed) consumed[row] = 0;
@@ -66,40 +69,47 @@ __global__ __launch_bounds__(kNT) void k_argmax(const float* __restrict__ logits
 }
 
 // ---------------------------------------------------------------------------
-// k_math_probe: the device exp/log on an array (parity tests of the math).
+// k_math_probe: the device exp/log/expm1/tanh on an array (parity tests of
+// the math).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_math_probe(const float* __restrict__ in, float* __restrict__ out_exp,
-                                                   float* __restrict__ out_log, int64_t n) {
+                                                   float* __restrict__ out_log, float* __restrict__ out_expm1,
+                                                   float* __restrict__ out_tanh, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) {
     const float x = in[i];
     if (out_exp) out_exp[i] = exp_f32(x);
     if (out_log) out_log[i] = log_f32(x);
+    if (out_expm1) out_expm1[i] = expm1_f32(x);
+    if (out_tanh) out_tanh[i] = tanh_f32(x);
   }
 }
 
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, int64_t n, hipStream_t st) {
+hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, float* out_expm1, float* out_tanh,
+                             int64_t n, hipStream_t st) {
   const int64_t blocks = (n + 255) / 256;
-  hipLaunchKernelGGL(k_math_probe, dim3((unsigned)blocks), dim3(256), 0, st, in, out_exp, out_log, n);
+  hipLaunchKernelGGL(k_math_probe, dim3((unsigned)blocks), dim3(256), 0, st, in, out_exp, out_log, out_expm1,
+                     out_tanh, n);
   return hipGetLastError();
 }
 
 hipError_t launch_penalty(const float* logits, int64_t stride, int rows, int n, const uint32_t* prev,
-                          int n_prev, int64_t prev_stride, int window, float penalty, float* out,
-                          hipStream_t st) {
+                          int n_prev, int64_t prev_stride, int window, float penalty, uint32_t xf, float cap,
+                          float inv_scale, float* out, hipStream_t st) {
   dim3 grid((n + kMaxNT * kMaxPerThread - 1) / (kMaxNT * kMaxPerThread), rows);
   hipLaunchKernelGGL(k_penalty, grid, dim3(kMaxNT), 0, st, logits, stride, n, prev, n_prev,
-                     prev_stride, window, penalty, out);
+                     prev_stride, window, penalty, xf, cap, inv_scale, out);
   return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t* tokens,
-                         uint8_t* consumed, uint32_t* kept_count, uint32_t* path, hipStream_t st) {
-  hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(kNT), 0, st, logits, stride, n, tokens, consumed,
-                     kept_count, path);
+hipError_t launch_argmax(const float* logits, int64_t stride, int rows, int n, uint32_t xf, float cap,
+                         float inv_scale, uint32_t* tokens, uint8_t* consumed, uint32_t* kept_count,
+                         uint32_t* path, hipStream_t st) {
+  hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(kNT), 0, st, logits, stride, n, xf, cap, inv_scale, tokens,
+                     consumed, kept_count, path);
   return hipGetLastError();
 }
 

@@ -8,6 +8,22 @@
 // operation.  Each f32 operation must round exactly once, so every file that
 // includes this header is compiled with -ffp-contract=off, f32 denormals on,
 // and IEEE (correctly rounded) division.
+//
+// The final logits may be soft-capped with std.math.tanh before sampling
+// (main.zig:653-658); Zig's f32 tanh / expm1 are ports of musl's tanhf.c /
+// expm1f.c, restated below as tanh_f32 / expm1_f32.
+//
+// Notices of the third-party algorithms restated here:
+//   expf, logf, expm1f (FreeBSD msun e_expf.c, e_logf.c, s_expm1f.c):
+//     Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//     Developed at SunPro, a Sun Microsystems, Inc. business.
+//     Permission to use, copy, modify, and distribute this software is
+//     freely granted, provided that this notice is preserved.
+//     (Float versions by Ian Lance Taylor, Cygnus Support.)
+//   tanhf (musl src/math/tanhf.c): musl libc, Copyright (c) 2005-2020 Rich
+//     Felker, et al., MIT license ("The above copyright notice and this
+//     permission notice shall be included in all copies or substantial
+//     portions of the Software").
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -109,6 +125,107 @@ __device__ __forceinline__ float log_f32(float x) {
   const float hfsq = 0.5f * f * f;
   const float dk = (float)k;
   return s * (hfsq + R) + dk * ln2_lo - hfsq + f + dk * ln2_hi;
+}
+
+}  // namespace llz
+
+namespace llz {
+
+// expm1(x) for f32, the s_expm1f.c algorithm as musl carries it (FreeBSD
+// msun lineage, two-coefficient rational approximation): reduce x = k ln2 +
+// r with a two-part ln2 and its rounding correction c, evaluate the
+// approximation on r, rebuild 2^k (r - e + 1) - 1 by k's range.  Every
+// operation rounds once (the file's compile flags).
+__device__ __forceinline__ float expm1_f32(float x) {
+  const float o_threshold = 8.8721679688e+01f;  // 0x42b17180
+  const float ln2_hi = 6.9313812256e-01f;       // 0x3f317180
+  const float ln2_lo = 9.0580006145e-06f;       // 0x3717f7d1
+  const float invln2 = 1.4426950216e+00f;       // 0x3fb8aa3b
+  const float Q1 = -3.3333212137e-2f;           // -0x888868.0p-28
+  const float Q2 = 1.5807170421e-3f;            //  0xcf3010.0p-33
+  const uint32_t ux = fbits(x);
+  const uint32_t hx = ux & 0x7fffffffu;
+  const int sign = (int)(ux >> 31);
+  if (hx >= 0x4195b844u) {  // |x| >= 27 ln2, or not finite
+    if (hx > 0x7f800000u) return x;
+    if (sign) return -1.0f;
+    if (x > o_threshold) return x * 0x1p127f;
+  }
+  float hi, lo, c = 0.0f;
+  int k;
+  if (hx > 0x3eb17218u) {    // |x| > ln2 / 2
+    if (hx < 0x3f851592u) {  // and < 1.5 ln2
+      if (!sign) {
+        hi = x - ln2_hi;
+        lo = ln2_lo;
+        k = 1;
+      } else {
+        hi = x + ln2_hi;
+        lo = -ln2_lo;
+        k = -1;
+      }
+    } else {
+      k = (int)(invln2 * x + (sign ? -0.5f : 0.5f));
+      const float t = (float)k;
+      hi = x - t * ln2_hi;
+      lo = t * ln2_lo;
+    }
+    x = hi - lo;
+    c = (hi - x) - lo;
+  } else if (hx < 0x33000000u) {  // |x| < 2^-25
+    return x;
+  } else {
+    k = 0;
+  }
+  const float hfx = 0.5f * x;
+  const float hxs = x * hfx;
+  const float r1 = 1.0f + hxs * (Q1 + hxs * Q2);
+  const float t = 3.0f - r1 * hfx;
+  float e = hxs * ((r1 - t) / (6.0f - x * t));
+  if (k == 0) return x - (x * e - hxs);
+  e = x * (e - c) - c;
+  e -= hxs;
+  if (k == -1) return 0.5f * (x - e) - 0.5f;
+  if (k == 1) {
+    if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+    return 1.0f + 2.0f * (x - e);
+  }
+  const float twopk = bitsf((uint32_t)(0x7f + k) << 23);
+  if (k < 0 || k > 56) {
+    float y = x - e + 1.0f;
+    y = k == 128 ? y * 2.0f * 0x1p127f : y * twopk;
+    return y - 1.0f;
+  }
+  const float tmk = bitsf((uint32_t)(0x7f - k) << 23);  // 2^-k
+  return k < 23 ? (x - e + (1.0f - tmk)) * twopk : (x - (e + tmk) + 1.0f) * twopk;
+}
+
+// tanh(x) for f32, the tanhf.c algorithm as musl carries it: by |x|,
+// 1 - 2 / (expm1(2|x|) + 2), expm1(2|x|) / (expm1(2|x|) + 2) or
+// -expm1(-2|x|) / (expm1(-2|x|) + 2), with the sign put back.
+__device__ __forceinline__ float tanh_f32(float x) {
+  const uint32_t ux = fbits(x);
+  const uint32_t w = ux & 0x7fffffffu;
+  const bool sign = (ux >> 31) != 0;
+  const float ax = bitsf(w);
+  float t;
+  if (w > 0x3f0c9f54u) {    // |x| > log(3) / 2, or NaN
+    if (w > 0x41200000u) {  // |x| > 10
+      t = 1.0f + 0.0f / ax;
+    } else {
+      t = expm1_f32(2.0f * ax);
+      t = 1.0f - 2.0f / (t + 2.0f);
+    }
+  } else if (w > 0x3e82c578u) {  // |x| > log(5/3) / 2
+    t = expm1_f32(2.0f * ax);
+    t = t / (t + 2.0f);
+  } else if (w >= 0x00800000u) {  // normal
+    t = expm1_f32(-2.0f * ax);
+    t = -t / (t + 2.0f);
+  } else {  // subnormal or zero
+    t = ax;
+  }
+  return sign ? -t : t;
 }
 
 }  // namespace llz

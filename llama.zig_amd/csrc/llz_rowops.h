@@ -8,6 +8,7 @@
 #include "llz_math.h"
 #include "llz_norm.h"
 #include "llz_wg.h"
+#include "llz_xform.h"
 
 namespace llz {
 
@@ -50,12 +51,12 @@ __device__ __forceinline__ bool amax_better(float v, uint32_t i, float bv, uint3
 // sampleArgmax over one row with the whole workgroup.  A NaN at index 0
 // is never replaced by the reference's loop, so the answer is then 0.
 template <int NT>
-__device__ uint32_t wg_argmax_row(const float* x, int n, WgScratch<NT>& sh, int& bank) {
+__device__ uint32_t wg_argmax_row(const RowSrc& x, int n, WgScratch<NT>& sh, int& bank) {
   const int t = (int)threadIdx.x;
   float bv = __builtin_nanf("");
   uint32_t bi = 0xffffffffu;
   for (int i = t; i < n; i += NT) {
-    const float v = x[i];
+    const float v = x.at(i);
     if (amax_better(v, (uint32_t)i, bv, bi)) { bv = v; bi = (uint32_t)i; }
   }
 #pragma unroll
@@ -77,20 +78,9 @@ __device__ uint32_t wg_argmax_row(const float* x, int n, WgScratch<NT>& sh, int&
     if (amax_better(v, i, rv, ri)) { rv = v; ri = i; }
   }
   lds_barrier();  // both banks were used
-  const float x0 = x[0];
+  const float x0 = x.at(0);
   if (x0 != x0 || ri == 0xffffffffu) ri = 0;
   return ri;
-}
-
-// Load kV consecutive logits starting at pos (positions >= n read as 0).
-__device__ __forceinline__ void load4(const float* row, int pos, int n, bool vec, float (&v)[kV]) {
-  if (vec && pos + kV <= n) {
-    const float4 q = *reinterpret_cast<const float4*>(row + pos);
-    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
-  } else {
-#pragma unroll
-    for (int k = 0; k < kV; ++k) v[k] = pos + k < n ? row[pos + k] : 0.0f;
-  }
 }
 
 // e_i = exp((v_i - max) / T) as sampler.zig:85 evaluates it.

@@ -238,7 +238,7 @@ __device__ __forceinline__ bool wave_resolve(float& s, int& done, const SliceSta
 
 // sampler.zig:83-88: the exact sequential f32 normaliser of one row, plus the
 // candidate list (every element with e >= cand_theta).
-__device__ float row_normaliser(const float* xr, int n, const RowParams& P, SampleShared& sh, int& bank,
+__device__ float row_normaliser(const RowSrc& X, int n, const RowParams& P, SampleShared& sh, int& bank,
                                 float& m_out, float m_known) {
   constexpr int W = kNT / kWave;
   constexpr int GE = W * kSlice;    // elements per group
@@ -253,10 +253,10 @@ __device__ float row_normaliser(const float* xr, int n, const RowParams& P, Samp
   // independent loads first: the max partials, the prologue's logits and the
   // first group
   const float mp = m_known;
-  const float vp = (w == 0 && lane < p0) ? xr[lane] : 0.0f;
+  const float vp = (w == 0 && lane < p0) ? X.at(lane) : 0.0f;
   float vcur[kSub][kV], vnext[kSub][kV];
 #pragma unroll
-  for (int c = 0; c < kSub; ++c) load4(xr, p0 + w * kSlice + c * (kWave * kV) + lane * kV, n, vec, vcur[c]);
+  for (int c = 0; c < kSub; ++c) X.load4(p0 + w * kSlice + c * (kWave * kV) + lane * kV, n, vec, vcur[c]);
   const float m = wg_fmax<kNT>(mp, sh.wg, bank);
   m_out = m;
 
@@ -281,7 +281,7 @@ __device__ float row_normaliser(const float* xr, int n, const RowParams& P, Samp
     if (gb + GE < n) {
 #pragma unroll
       for (int c = 0; c < kSub; ++c)
-        load4(xr, gb + GE + w * kSlice + c * (kWave * kV) + lane * kV, n, vec, vnext[c]);
+        X.load4(gb + GE + w * kSlice + c * (kWave * kV) + lane * kV, n, vec, vnext[c]);
     }
     uint32_t* part = ns.part[pb];
     const int sb = gb + w * kSlice;
@@ -469,7 +469,7 @@ __device__ int prefix_filters(const List& L, int M, float p_nc, int n, const Row
 }
 
 // Entropy sum over the whole row in index order (sampler.zig:129-132).
-__device__ float entropy_pass(const float* xr, int n, float m, float S, const RowParams& P,
+__device__ float entropy_pass(const RowSrc& X, int n, float m, float S, const RowParams& P,
                               SampleShared& sh, int& bank) {
   const bool t1 = (P.flags & kFlagTIsOne) != 0;
   const bool vec = (P.flags & kFlagVecSrc) != 0;
@@ -477,7 +477,7 @@ __device__ float entropy_pass(const float* xr, int n, float m, float S, const Ro
   const int t = (int)threadIdx.x;
   for (int base = 0; base < n; base += kTile) {
     float v[kV], term[kV];
-    load4(xr, base + t * kV, n, vec, v);
+    X.load4(base + t * kV, n, vec, v);
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
       const float p = row_exp(v[k], m, P.temperature, t1) / S;
@@ -520,17 +520,17 @@ struct NormResult {
 
 // The streaming normaliser (sampler.zig:83-88) for a row k_stats could not
 // certify; fills the candidate list in LDS.
-__device__ __noinline__ NormResult select_norm_fallback(const RowParams P, const float* xr, SampleShared& sh,
+__device__ __noinline__ NormResult select_norm_fallback(const RowParams P, const RowSrc X, SampleShared& sh,
                                                         int bank, float m_known) {
   if (threadIdx.x == 0) sh.cand_count = 0;
   NormResult r;
-  r.S = row_normaliser(xr, P.n, P, sh, bank, r.m, m_known);
+  r.S = row_normaliser(X, P.n, P, sh, bank, r.m, m_known);
   r.bank = bank;
   return r;
 }
 
 __device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q, SampleShared& sh, int bank,
-                                             float m, float S, uint32_t path);
+                                             float m, float S, uint32_t path, const PenShared* pen);
 
 constexpr int kShortMax = 256;  // longest candidate list of the short path
 
@@ -679,16 +679,16 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
 // cc_in <= 448 (the later ones are read here).
 __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q, SampleShared& sh, float m,
                                            float S, uint32_t cc_in, bool uncertified, float u_row, bool pre_ok,
-                                           uint64_t cand_pre, uint32_t cand_n0) {
+                                           uint64_t cand_pre, uint32_t cand_n0, const RowSrc& X,
+                                           const PenShared* pen) {
   int bank = 0;
   const int row = blockIdx.x;
   const int t = (int)threadIdx.x;
   const int n = P.n;
-  const float* xr = Q.src + (int64_t)row * P.src_stride;
   uint32_t path = 0;
   if (uncertified) {
     // the streaming normaliser (sampler.zig:83-88) fills the candidate list in LDS
-    const NormResult r = select_norm_fallback(P, xr, sh, bank, m);
+    const NormResult r = select_norm_fallback(P, X, sh, bank, m);
     S = r.S;
     m = r.m;
     bank = r.bank;
@@ -710,7 +710,10 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
 
   // ---- 3. sum <= 0 exit: sampleArgmax of the caller's logits (:89)
   if (S <= 0.0f) {
-    token = wg_argmax_row<kNT>(Q.orig + (int64_t)row * P.orig_stride, n, sh.wg, bank);
+    // (pen is null exactly when the kernel reads rows untransformed)
+    const RowSrc O = pen ? row_orig(P, Q, row)
+                         : RowSrc{Q.orig + (int64_t)row * P.orig_stride, 0u, 1.0f, 1.0f, 1.0f, nullptr};
+    token = wg_argmax_row<kNT>(O, n, sh.wg, bank);
     path = kPathSumLe0;
     if (t == 0) {
       Q.tokens[row] = token;
@@ -757,7 +760,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   const bool ovf = cc > (uint32_t)kCap;
   const int c = ovf ? kCap : (int)cc;
   if (!ovf && c <= kShortMax && !(P.typical_p > 0.0f && P.typical_p < 1.0f)) {
-    if (!select_short(P, Q, sh, c, m, S, path, u_row)) select_full_row(P, Q, sh, bank, m, S, path);
+    if (!select_short(P, Q, sh, c, m, S, path, u_row)) select_full_row(P, Q, sh, bank, m, S, path, pen);
     return;
   }
   const int csort = next_pow2(c);
@@ -803,7 +806,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
       lds_barrier();
     } else if (typical && K >= 2) {
       path |= kPathEntropy;
-      H = entropy_pass(xr, n, m, S, P, sh, bank);
+      H = entropy_pass(X, n, m, S, P, sh, bank);
       const int ksort = next_pow2(K);
       for (int q = t; q < ksort; q += kNT) {
         if (q < K) {
@@ -861,19 +864,19 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   }
 
   // ---- full-row fallback: every probability, stable radix sort, filters
-  select_full_row(P, Q, sh, bank, m, S, path);
+  select_full_row(P, Q, sh, bank, m, S, path, pen);
 }
 
 // The full-row fallback of k_select: every probability, stable radix sort of
 // the whole row in the workspace, the filters and the draw over it.
 __device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q, SampleShared& sh, int bank,
-                                             float m, float S, uint32_t path) {
+                                             float m, float S, uint32_t path, const PenShared* pen) {
   const int row = blockIdx.x;
   const int t = (int)threadIdx.x;
   const int n = P.n;
   const bool t1 = (P.flags & kFlagTIsOne) != 0;
   const bool vec = (P.flags & kFlagVecSrc) != 0;
-  const float* xr = Q.src + (int64_t)row * P.src_stride;
+  const RowSrc X = row_src(P, Q, row, pen);
   const bool typical = P.typical_p > 0.0f && P.typical_p < 1.0f;
   const float u = Q.uniforms[row];
   int K = 0;
@@ -899,7 +902,7 @@ __device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q,
   for (int base = 0; base < n; base += kTile) {
     float v[kV];
     const int pos = base + t * kV;
-    load4(xr, pos, n, vec, v);
+    X.load4(pos, n, vec, v);
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
       if (pos + k < n) {
@@ -919,7 +922,7 @@ __device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q,
   if (K < 0) K = 0;
   if (typical && K >= 2) {
     path |= kPathEntropy;
-    H = entropy_pass(xr, n, m, S, P, sh, bank);
+    H = entropy_pass(X, n, m, S, P, sh, bank);
     for (int i = t; i < n; i += kNT) mask[i] = 0;
     __threadfence();
     __syncthreads();
@@ -933,7 +936,7 @@ __device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q,
       const bool sel = i < n && mask[i] == 1;
       const uint32_t before = wg_excl_scan_sat<kNT>(sel ? 1u : 0u, 0x7fffffffu, sh.wg, bank);
       if (sel) {
-        const float p = row_exp(xr[i], m, P.temperature, t1) / S;
+        const float p = row_exp(X.at(i), m, P.temperature, t1) / S;
         const float surprise = p > 0.0f ? -log_f32(p) : kInf;
         Bk[written + before] = __float_as_uint(fabsf(surprise - H));
         Bv[written + before] = (uint32_t)i;
@@ -948,7 +951,7 @@ __device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q,
     int st;
     list_accumulate<kNT, 2, false>(
         0.0f, written, P.typical_p, st,
-        [&](int d) { return row_exp(xr[Bv[d]], m, P.temperature, t1) / S; }, sh.wg, bank);
+        [&](int d) { return row_exp(X.at((int)Bv[d]), m, P.temperature, t1) / S; }, sh.wg, bank);
     const int keep_n = st >= 0 ? st : written;
     for (int d = t; d < keep_n; d += kNT) mask[Bv[d]] = 2;
     __threadfence();

@@ -115,14 +115,14 @@ __device__ __forceinline__ float4 exact_terms4(float4 v, float m, float T, bool 
 
 // The exact terms of EXACT slot `slot` (loaded and waited for) into its dump
 // area, and its candidates (once per segment).
-__device__ __forceinline__ void slot_terms(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int slot,
-                                           int n, float m, float theta, bool t1) {
+__device__ __forceinline__ void slot_terms(FastShared& F, const RowPtrs& Q, const RowParams& P, const RowSrc& X,
+                                           int row, int slot, int n, float m, float theta, bool t1) {
   const int lane = lane_id();
   const int seg = F.slotseg[slot];
   const bool pred = F.sflag[seg] == EXACT_PRED;
   float4* p = reinterpret_cast<float4*>(&F.u.x.dump[slot][lane * 4]);
   const int pos = seg * SEG + lane * 4;
-  float4 e = exact_terms4(*p, m, P.temperature, t1);
+  float4 e = exact_terms4(X.fix4(pos, *p, n), m, P.temperature, t1);
   e.x = pos + 0 < n ? e.x : 0.0f;
   e.y = pos + 1 < n ? e.y : 0.0f;
   e.z = pos + 2 < n ? e.z : 0.0f;
@@ -188,10 +188,10 @@ __device__ __forceinline__ void slot_tables(FastShared& F, int slot) {
 
 // Rounds after the first: the terms and tables of this wave's slots (slot s
 // on wave s % W, all loaded by this wave and waited for).
-__device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
-                                               int nslot, int n, float m, float theta, bool t1) {
+__device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, const RowSrc& X,
+                                               int row, int w, int nslot, int n, float m, float theta, bool t1) {
   for (int slot = w; slot < nslot; slot += W) {
-    slot_terms(F, Q, P, row, slot, n, m, theta, t1);
+    slot_terms(F, Q, P, X, row, slot, n, m, theta, t1);
     slot_tables(F, slot);
   }
 }
@@ -484,13 +484,16 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
 }
 
 // FASTLD: 16-byte aligned rows with n % 4 == 0 (one float4 per lane per
-// segment through buffer loads); otherwise element loads.
-template <bool FASTLD>
+// segment through buffer loads); otherwise element loads.  XF: the rows are
+// read through post-processing and/or the fused repetition penalty
+// (llz_xform.h); otherwise as they are.
+template <bool FASTLD, bool XF>
 __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   __shared__ union {
     FastShared fast;      // phases L .. C
     SampleShared select;  // then the selection stage
   } U;
+  __shared__ PenShared pen_sh;  // kXfPen: the row's penalised positions
   FastShared& F = U.fast;
   const int row = blockIdx.x;
   const int t = (int)threadIdx.x, lane = lane_id();
@@ -498,6 +501,28 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   const int n = P.n;
   const bool t1 = (P.flags & kFlagTIsOne) != 0;
   const float* xr = Q.src + (int64_t)row * P.src_stride;
+  // reads of the row through the caller's post-processing and the penalty
+  // (the identity when !XF)
+  const RowSrc X{xr, XF ? P.xf_src : 0u, P.cap, P.inv_scale, P.rpen, &pen_sh};
+  uint64_t pen_wm = 0;  // segments of this wave holding a penalised position
+  if constexpr (XF) {
+    if (P.xf_src & kXfPen) {
+      pen_build(pen_sh, P, Q, row);
+      lds_barrier();
+      pen_wm = uni_u64(pen_sh.wmask[w]);
+    }
+  }
+  // one landed segment's logits (k: the wave's segment index) through the
+  // transforms: post-processing on every element, the penalty only in the
+  // segments that hold a penalised position
+  auto seg_fix = [&](int k, float4 v) {
+    if constexpr (XF) {
+      const int pos = (w + W * k) * SEG + lane * 4;
+      v = X.pre4(pos, v, n);
+      if ((pen_wm >> (k & 63)) & 1ull) v = X.pen4(pos, v, n);
+    }
+    return v;
+  };
   const float l2e_t = P.l2e_t;
   const int G = (n + SEG - 1) / SEG;
   const int SPW = (G + W - 1) / W;
@@ -577,7 +602,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         if (k < nseg_w) {
           lds_dma_wait<kLoadWindow - 1>();  // the window's loads behind it (the register ones come later)
           float4* p = reinterpret_cast<float4*>(&F.u.data[w][i][lane * 4]);
-          const float4 v = *p;
+          const float4 v = seg_fix(k, *p);
           if (i == 0) set_cw(wave_max_f32(lane4 < seg_lim(k) ? max4(v) : -kInfS));  // the first segment processed
           const float4 q = seg_q(k, v);
           *p = q;
@@ -585,6 +610,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         }
       } else {
         const int k = i - KL;
+        d[k] = seg_fix(k, d[k]);
         if (k == 0 && nseg_w <= KV) set_cw(wave_max_f32(lane4 < seg_lim(0) ? max4(d[0]) : -kInfS));
         float4 q = seg_q(k, d[k]);  // a NaN logit makes its segment sum NaN
         // materialise q here, while the loads land (not sunk into phase S)
@@ -603,9 +629,11 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     for (int k = 0; k < KV; ++k) d[k] = ld1x4(xr, base_w + k * (W * SEG), k < nseg_w ? n : 0);
     for (int k = KV; k < nseg_w; ++k) seg_to_lds(xr, w + W * k, n, false, &F.u.data[w][k - KV][0]);
     __builtin_amdgcn_sched_barrier(0);
+    d[0] = seg_fix(0, d[0]);
     set_cw(wave_max_f32(lane4 < seg_lim(0) ? max4(d[0]) : -kInfS));
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
+      if (k > 0) d[k] = seg_fix(k, d[k]);
       float4 q = seg_q(k, d[k]);
       asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
       d[k] = q;
@@ -614,7 +642,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     }
     for (int k = KV; k < nseg_w; ++k) {
       float4* p = reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]);
-      const float4 q = seg_q(k, *p);
+      const float4 q = seg_q(k, seg_fix(k, *p));
       *p = q;
       seg_sum(k, q);
     }
@@ -622,7 +650,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   if (lane < nseg_w) F.v.aseg[w + W * lane] = my_a;
   if (!fits) {  // rows the fast path does not take: maximum and NaN scan only
     for (int i = t; i < n; i += NT) {
-      const float v = xr[i];
+      const float v = X.at(i);
       mx = fmaxf(mx, v);
       nanf |= (uint32_t)(v != v);
     }
@@ -674,7 +702,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       // row's maximum is taken again (sampler.zig:80-81: NaNs are skipped)
       nanrow = true;
       float mm = -kInfS;
-      for (int i = t; i < n; i += NT) mm = fmaxf(mm, xr[i]);
+      for (int i = t; i < n; i += NT) mm = fmaxf(mm, X.at(i));
       mm = wave_max_f32(mm);
       __syncthreads();  // every wave has read F.mw
       if (lane == 0) F.mw[w] = mm;
@@ -774,7 +802,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       for (int h = 0; h < 2; ++h) {
         const int i = h * kWave + lane;
         const int pos = i < cnt ? (int)(F.qpos[w][i] & 0x7fffffffu) : 0;
-        v4q[h] = FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n);
+        v4q[h] = X.fix4(pos, FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n), n);
       }
     };
     auto settle = [&](int cnt) { settle_specials(F, Q, P, row, w, cnt, v4q, Rw, cw, m, theta, t1); };
@@ -931,7 +959,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
       // while the re-reads land; slot 0, the row's first segment, needs no
       // tables: wave 0 sums it term by term
       for (int slot = w; slot < min(F.nslot, DCAP); slot += W) {
-        slot_terms(F, Q, P, row, slot, n, m, theta, t1);
+        slot_terms(F, Q, P, X, row, slot, n, m, theta, t1);
         if (slot != 0) slot_tables(F, slot);
       }
       if (w == 0) {
@@ -1038,7 +1066,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
         const int nslot = F.nslot;
         exact_loads<FASTLD>(F, xr, w, nslot, n);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        exact_segments(F, Q, P, row, w, nslot, n, m, theta, t1);
+        exact_segments(F, Q, P, X, row, w, nslot, n, m, theta, t1);
         __syncthreads();
       }
       if (w == 0) {
@@ -1185,7 +1213,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   // walk's results, lie past F.u): no barrier here
   static_assert(sizeof(SampleShared) <= sizeof(F.u), "the selection's memory must lie inside F.u");
   select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified, u_row, certified && pre_ok,
-             cand_pre, cand_n0);
+             cand_pre, cand_n0, X, XF ? &pen_sh : nullptr);
 }
 
 }  // namespace
@@ -1194,10 +1222,16 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
 hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_begin, hipEvent_t ev_end,
                          hipStream_t st) {
   if (ev_begin && hipEventRecord(ev_begin, st) != hipSuccess) return hipErrorUnknown;
-  if ((P.flags & kFlagVecSrc) != 0 && (P.n % 4) == 0)
-    hipLaunchKernelGGL(k_stats<true>, dim3(P.rows), dim3(NT), 0, st, P, Q);
+  const bool fastld = (P.flags & kFlagVecSrc) != 0 && (P.n % 4) == 0;
+  const bool xf = P.xf_src != 0u || P.xf_orig != 0u;
+  if (fastld && !xf)
+    hipLaunchKernelGGL((k_stats<true, false>), dim3(P.rows), dim3(NT), 0, st, P, Q);
+  else if (fastld)
+    hipLaunchKernelGGL((k_stats<true, true>), dim3(P.rows), dim3(NT), 0, st, P, Q);
+  else if (!xf)
+    hipLaunchKernelGGL((k_stats<false, false>), dim3(P.rows), dim3(NT), 0, st, P, Q);
   else
-    hipLaunchKernelGGL(k_stats<false>, dim3(P.rows), dim3(NT), 0, st, P, Q);
+    hipLaunchKernelGGL((k_stats<false, true>), dim3(P.rows), dim3(NT), 0, st, P, Q);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (ev_end && hipEventRecord(ev_end, st) != hipSuccess) return hipErrorUnknown;

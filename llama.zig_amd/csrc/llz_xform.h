@@ -1,0 +1,158 @@
+// llz_xform.h -- the logits as the sampler sees them.
+//
+// The reference's decode loop post-processes the final logits before
+// Sampler.sample (main.zig:653-666): soft-capping v = tanh(v / s) * s when
+// s > 0, then the logit scale v *= 1 / scale when scale is neither 1 nor 0.
+// sampleWithRandom then applies the repetition penalty to a copy
+// (sampler.zig:54-75).  RowSrc applies all three to a caller's row at every
+// read, so the kernels read each logit from HBM as the caller wrote it and
+// see the values the reference computes with:
+//   at(i) / load4  -- penalised post-processed logits (the chain's input);
+//   pre(v)         -- post-processing only (sampleArgmax's input at
+//                     sampler.zig:50,89 is `logits`, not `penalized`).
+// The penalised positions of a row (the distinct ids < n among the last
+// min(len, window) history tokens, at most kPenMax of them) are collected
+// once per row into LDS (pen_build), sorted; a read checks membership there.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "llz_internal.h"
+#include "llz_math.h"
+#include "llz_norm.h"
+#include "llz_wg.h"
+
+namespace llz {
+
+// main.zig:653-666 on one logit.
+__device__ __forceinline__ float logit_post(float v, uint32_t xf, float cap, float inv_scale) {
+  if (xf & kXfCap) v = tanh_f32(v / cap) * cap;
+  if (xf & kXfScale) v = v * inv_scale;
+  return v;
+}
+
+// sampler.zig:65-69 on a logit of a penalised position.
+__device__ __forceinline__ float penalise(float v, float rp) { return v > 0.0f ? v / rp : v * rp; }
+
+// The penalised positions of one row, ascending, and for each of the
+// single-pass kernel's eight waves the segments (256 logits; wave w owns
+// segments w, w + 8, ...) holding one: bit k of wmask[w] for segment w + 8k.
+struct PenShared {
+  uint32_t pos[kPenMax];
+  uint64_t wmask[8];
+  int n;
+};
+
+// Wave 0 collects the row's penalised positions (the window is read from the
+// history row; ids >= n never match, sampler.zig:64).  The caller
+// synchronises the workgroup before any read uses them.
+__device__ __forceinline__ void pen_build(PenShared& ps, const RowParams& P, const RowPtrs& Q, int row) {
+  if (wave_id() != 0) return;
+  const int lane = lane_id();
+  const int w = P.pen_w;  // <= kPenMax, the window's length
+  const uint32_t* win = Q.prev_win + (int64_t)row * P.prev_stride;
+  const uint32_t id = lane < w ? win[lane] : 0xffffffffu;
+  // keep the first occurrence of each id < n
+  bool keep = lane < w && id < (uint32_t)P.n;
+  for (int j = 0; j < w; ++j) {
+    const uint32_t o = readlane_u32(id, j);
+    keep = keep && !(j < lane && o == id);
+  }
+  // rank among the kept ids (distinct), then scatter in ascending order
+  const uint64_t km = bal64(keep);
+  uint32_t rank = 0;
+  for (int j = 0; j < w; ++j) {
+    const uint32_t o = readlane_u32(id, j);
+    rank += (((km >> j) & 1ull) != 0ull && o < id) ? 1u : 0u;
+  }
+  if (keep) ps.pos[rank] = id;
+  if (lane == 0) ps.n = __popcll(km);
+  if (lane < 8) {
+    uint64_t wm = 0;
+    for (int j = 0; j < w; ++j) {
+      const uint32_t g = readlane_u32(id, j) >> 8;  // its segment
+      if (((km >> j) & 1ull) != 0ull && (int)(g & 7u) == lane && (g >> 3) < 64u) wm |= 1ull << (g >> 3);
+    }
+    ps.wmask[lane] = wm;
+  }
+}
+
+// A row of logits as the chain reads it (see the file comment).
+struct RowSrc {
+  const float* x;       // the row as the caller passed it
+  uint32_t xf;          // kXf* bits applied on reads through at() / load4()
+  float cap, inv_scale, rp;
+  const PenShared* pen; // penalised positions (kXfPen)
+
+  __device__ __forceinline__ float pre(float v) const { return logit_post(v, xf, cap, inv_scale); }
+
+  __device__ __forceinline__ bool penalised(int i) const {
+    const int np = pen->n;
+    // lower bound of i in the sorted list
+    int lo = 0, hi = np;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (pen->pos[mid] < (uint32_t)i) lo = mid + 1; else hi = mid;
+    }
+    return lo < np && pen->pos[lo] == (uint32_t)i;
+  }
+
+  // One read value v of position i through the row's transforms.
+  __device__ __forceinline__ float fix(int i, float v) const {
+    if (xf == 0u) return v;
+    v = pre(v);
+    if ((xf & kXfPen) && penalised(i)) v = penalise(v, rp);
+    return v;
+  }
+
+  __device__ __forceinline__ float at(int i) const { return fix(i, x[i]); }
+
+  // Four consecutive read values from position pos; positions >= n are left
+  // as they are (callers fill them with their own neutral value).  pre4:
+  // post-processing only; pen4: the penalty only; fix4: both.
+  __device__ __forceinline__ float4 pre4(int pos, float4 v, int n) const {
+    if ((xf & (kXfCap | kXfScale)) == 0u) return v;
+    v.x = pos + 0 < n ? pre(v.x) : v.x;
+    v.y = pos + 1 < n ? pre(v.y) : v.y;
+    v.z = pos + 2 < n ? pre(v.z) : v.z;
+    v.w = pos + 3 < n ? pre(v.w) : v.w;
+    return v;
+  }
+  __device__ __forceinline__ float4 pen4(int pos, float4 v, int n) const {
+    if ((xf & kXfPen) == 0u) return v;
+    v.x = pos + 0 < n && penalised(pos + 0) ? penalise(v.x, rp) : v.x;
+    v.y = pos + 1 < n && penalised(pos + 1) ? penalise(v.y, rp) : v.y;
+    v.z = pos + 2 < n && penalised(pos + 2) ? penalise(v.z, rp) : v.z;
+    v.w = pos + 3 < n && penalised(pos + 3) ? penalise(v.w, rp) : v.w;
+    return v;
+  }
+  __device__ __forceinline__ float4 fix4(int pos, float4 v, int n) const { return pen4(pos, pre4(pos, v, n), n); }
+
+  // kLaneV consecutive logits from pos (positions >= n read as 0).
+  __device__ __forceinline__ void load4(int pos, int n, bool vec, float (&v)[kLaneV]) const {
+    if (vec && pos + kLaneV <= n) {
+      const float4 q = *reinterpret_cast<const float4*>(x + pos);
+      v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+#pragma unroll
+      for (int k = 0; k < kLaneV; ++k) v[k] = pos + k < n ? x[pos + k] : 0.0f;
+    }
+    if (xf != 0u) {
+#pragma unroll
+      for (int k = 0; k < kLaneV; ++k)
+        if (pos + k < n) v[k] = fix(pos + k, v[k]);
+    }
+  }
+};
+
+// The chain's view of row `row` (src: the caller's rows, or the penalised
+// copy) and sampleArgmax's view (the caller's rows, post-processing only).
+__device__ __forceinline__ RowSrc row_src(const RowParams& P, const RowPtrs& Q, int row, const PenShared* pen) {
+  return RowSrc{Q.src + (int64_t)row * P.src_stride, P.xf_src, P.cap, P.inv_scale, P.rpen, pen};
+}
+__device__ __forceinline__ RowSrc row_orig(const RowParams& P, const RowPtrs& Q, int row) {
+  return RowSrc{Q.orig + (int64_t)row * P.orig_stride, P.xf_orig & ~kXfPen, P.cap, P.inv_scale, 1.0f, nullptr};
+}
+
+}  // namespace llz

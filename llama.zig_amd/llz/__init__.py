@@ -57,6 +57,27 @@ class CConfig(C.Structure):
     ]
 
 
+class CPost(C.Structure):
+    _fields_ = [("final_logit_softcapping", C.c_float), ("logit_scale", C.c_float)]
+
+
+@dataclasses.dataclass
+class LogitPost:
+    """The decode loop's final-logit post-processing (main.zig:653-666):
+    soft-capping when final_logit_softcapping > 0, then v *= 1 / logit_scale
+    when logit_scale is neither 1 nor 0."""
+
+    final_logit_softcapping: float = 0.0
+    logit_scale: float = 1.0
+
+    def to_c(self) -> CPost:
+        return CPost(float(self.final_logit_softcapping), float(self.logit_scale))
+
+
+def _post_ref(post: Optional[LogitPost]):
+    return C.byref(post.to_c()) if post is not None else None
+
+
 class CExtras(C.Structure):
     _fields_ = [
         ("d_kept_count", C.c_void_p), ("d_kept_ids", C.c_void_p), ("d_kept_probs", C.c_void_p),
@@ -103,10 +124,10 @@ def _lib():
         L.llz_sampler_config_default.restype = None
         L.llz_sample_workspace_bytes.argtypes = [i32, i32, C.POINTER(CConfig), i32]
         L.llz_sample_workspace_bytes.restype = C.c_size_t
-        L.llz_sample_rows.argtypes = [vp, i64, i32, i32, C.POINTER(CConfig), vp, i32, i64, vp, vp,
-                                      vp, C.POINTER(CExtras), vp, C.c_size_t, vp]
+        L.llz_sample_rows.argtypes = [vp, i64, i32, i32, C.POINTER(CConfig), C.POINTER(CPost), vp, i32, i64,
+                                      vp, vp, vp, C.POINTER(CExtras), vp, C.c_size_t, vp]
         L.llz_sample_rows.restype = C.c_int
-        L.llz_argmax_rows.argtypes = [vp, i64, i32, i32, vp, vp]
+        L.llz_argmax_rows.argtypes = [vp, i64, i32, i32, C.POINTER(CPost), vp, vp]
         L.llz_argmax_rows.restype = C.c_int
         L.llz_rng_seed.argtypes = [C.POINTER(u64), u64]
         L.llz_rng_seed.restype = None
@@ -130,7 +151,7 @@ def _lib():
         L.llz_sampler_get_state.restype = None
         L.llz_sampler_set_state.argtypes = [vp, C.POINTER(u64)]
         L.llz_sampler_set_state.restype = None
-        L.llz_debug_math.argtypes = [vp, vp, vp, i64, vp]
+        L.llz_debug_math.argtypes = [vp, vp, vp, vp, vp, i64, vp]
         L.llz_debug_math.restype = C.c_int
         L.llz_debug_kernel_events.argtypes = [vp, vp]
         L.llz_debug_kernel_events.restype = C.c_int
@@ -210,8 +231,8 @@ class SampleResult:
 PATH_SUM_LE0, PATH_ENTROPY, PATH_FULL_SORT, PATH_STREAM_NORM = 1, 2, 4, 8
 
 
-def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, kept_cap: int = 0,
-                stats: bool = False, path: bool = False, workspace=None, stream=None,
+def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, post: Optional[LogitPost] = None,
+                kept_cap: int = 0, stats: bool = False, path: bool = False, workspace=None, stream=None,
                 out=None) -> SampleResult:
     """Batched Sampler.sample over device rows.
 
@@ -272,7 +293,8 @@ def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, kept_
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
     rc = _lib().llz_sample_rows(
-        logits.data_ptr(), logits.stride(0), rows, vocab, C.byref(c), prev_ptr, n_prev, prev_stride,
+        logits.data_ptr(), logits.stride(0), rows, vocab, C.byref(c), _post_ref(post), prev_ptr, n_prev,
+        prev_stride,
         uniforms.data_ptr(), tokens.data_ptr(), consumed.data_ptr(),
         C.byref(ex) if ex is not None else None, workspace.data_ptr(), workspace.numel(),
         _stream_ptr(stream))
@@ -280,25 +302,33 @@ def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, kept_
     return res
 
 
-def argmax_rows(logits, stream=None):
-    """sampleArgmax per row (sampler.zig:31-41) on a 2-D float32 CUDA tensor."""
+def argmax_rows(logits, post: Optional[LogitPost] = None, stream=None):
+    """sampleArgmax per row (sampler.zig:31-41) of the post-processed logits
+    (main.zig:653-666) on a 2-D float32 CUDA tensor."""
     torch = _torch()
+    if not (logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1):
+        raise ValueError("logits must be a 2-D float32 CUDA tensor with contiguous rows")
     rows, vocab = logits.shape
     tokens = torch.empty(rows, dtype=torch.int32, device=logits.device)
-    rc = _lib().llz_argmax_rows(logits.data_ptr(), logits.stride(0), rows, vocab, tokens.data_ptr(),
-                                _stream_ptr(stream))
+    rc = _lib().llz_argmax_rows(logits.data_ptr(), logits.stride(0), rows, vocab, _post_ref(post),
+                                tokens.data_ptr(), _stream_ptr(stream))
     _check(rc, "llz_argmax_rows")
     return tokens
 
 
-def debug_math(x):
-    """Device exp/log of a float32 CUDA tensor (parity tests of the math)."""
+def debug_math(x, extra: bool = False):
+    """Device exp/log (and with extra, expm1/tanh) of a float32 CUDA tensor
+    (parity tests of the math)."""
     torch = _torch()
     e = torch.empty_like(x)
     lg = torch.empty_like(x)
-    rc = _lib().llz_debug_math(x.data_ptr(), e.data_ptr(), lg.data_ptr(), x.numel(), _stream_ptr(None))
+    em1 = torch.empty_like(x) if extra else None
+    th = torch.empty_like(x) if extra else None
+    rc = _lib().llz_debug_math(x.data_ptr(), e.data_ptr(), lg.data_ptr(),
+                               em1.data_ptr() if extra else None, th.data_ptr() if extra else None,
+                               x.numel(), _stream_ptr(None))
     _check(rc, "llz_debug_math")
-    return e, lg
+    return (e, lg, em1, th) if extra else (e, lg)
 
 
 def set_kernel_events(begin=None, end=None) -> None:

@@ -2,6 +2,19 @@
  * llz_oracle.c -- CPU restatement of llama.zig's token sampler (TEST
  * INFRASTRUCTURE ONLY: the shipped library never links or calls it).
  *
+ * Third-party algorithms restated below, with the notices their authors ask
+ * to be kept:
+ *   expf, logf, expm1f (FreeBSD msun e_expf.c, e_logf.c, s_expm1f.c):
+ *     Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+ *     Developed at SunPro, a Sun Microsystems, Inc. business.
+ *     Permission to use, copy, modify, and distribute this software is
+ *     freely granted, provided that this notice is preserved.
+ *     (Float versions by Ian Lance Taylor, Cygnus Support.)
+ *   tanhf (musl src/math/tanhf.c): musl libc, Copyright (c) 2005-2020 Rich
+ *     Felker, et al., MIT license ("The above copyright notice and this
+ *     permission notice shall be included in all copies or substantial
+ *     portions of the Software").
+ *
  * Every function cites the reference line it follows.  The restatement is
  * deliberately literal: sequential f32 loops in the reference's order, a
  * stable sort with the reference's comparator, the same early exits.  Build
@@ -148,6 +161,128 @@ void llz_oracle_expf_array(const float *in, float *out, int64_t n)
 void llz_oracle_logf_array(const float *in, float *out, int64_t n)
 {
     for (int64_t i = 0; i < n; ++i) out[i] = llz_oracle_logf(in[i]);
+}
+
+/* ------------------------------------------------------------------------
+ * expm1 / tanh for f32.  The reference's decode loop soft-caps the final
+ * logits with std.math.tanh (main.zig:653-658) before the sampler sees them.
+ * Zig's std.math.tanh / expm1 for f32 are ports of musl's tanhf.c /
+ * expm1f.c (musl 1.2.x; expm1f.c derives from FreeBSD msun s_expm1f.c).
+ * This is a fresh restatement of those published algorithms.
+ * ---------------------------------------------------------------------- */
+float llz_oracle_expm1f(float x)
+{
+    const float o_threshold = 8.8721679688e+01f; /* 0x42b17180 */
+    const float ln2_hi = 6.9313812256e-01f;      /* 0x3f317180 */
+    const float ln2_lo = 9.0580006145e-06f;      /* 0x3717f7d1 */
+    const float invln2 = 1.4426950216e+00f;      /* 0x3fb8aa3b */
+    const float Q1 = -3.3333212137e-2f;          /* -0x888868.0p-28 */
+    const float Q2 = 1.5807170421e-3f;           /*  0xcf3010.0p-33 */
+    const uint32_t ux = f2u(x);
+    const uint32_t hx = ux & 0x7fffffffu;
+    const int sign = (int)(ux >> 31);
+    float hi, lo, c = 0.0f, t, e, hfx, hxs, r1, twopk, y;
+    int k;
+
+    if (hx >= 0x4195b844u) {          /* |x| >= 27 ln2, or not finite */
+        if (hx > 0x7f800000u) return x; /* NaN */
+        if (sign) return -1.0f;
+        if (x > o_threshold) return x * 0x1p127f;
+    }
+    if (hx > 0x3eb17218u) {           /* |x| > ln2 / 2 */
+        if (hx < 0x3f851592u) {       /* and |x| < 1.5 ln2 */
+            if (!sign) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+            else { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+        } else {
+            k = (int)(invln2 * x + (sign ? -0.5f : 0.5f));
+            t = (float)k;
+            hi = x - t * ln2_hi;
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000u) {    /* |x| < 2^-25 */
+        return x;
+    } else {
+        k = 0;
+    }
+    hfx = 0.5f * x;
+    hxs = x * hfx;
+    r1 = 1.0f + hxs * (Q1 + hxs * Q2);
+    t = 3.0f - r1 * hfx;
+    e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = x * (e - c) - c;
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) {
+        if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+        return 1.0f + 2.0f * (x - e);
+    }
+    twopk = u2f((uint32_t)(0x7f + k) << 23);
+    if (k < 0 || k > 56) {
+        y = x - e + 1.0f;
+        if (k == 128) y = y * 2.0f * 0x1p127f;
+        else y = y * twopk;
+        return y - 1.0f;
+    }
+    {
+        const float tmk = u2f((uint32_t)(0x7f - k) << 23); /* 2^-k */
+        if (k < 23) y = (x - e + (1.0f - tmk)) * twopk;
+        else y = (x - (e + tmk) + 1.0f) * twopk;
+    }
+    return y;
+}
+
+float llz_oracle_tanhf(float x)
+{
+    const uint32_t ux = f2u(x);
+    const uint32_t w = ux & 0x7fffffffu;
+    const int sign = (int)(ux >> 31);
+    const float ax = u2f(w);
+    float t;
+
+    if (w > 0x3f0c9f54u) {            /* |x| > log(3) / 2, or NaN */
+        if (w > 0x41200000u) {        /* |x| > 10 */
+            t = 1.0f + 0.0f / ax;
+        } else {
+            t = llz_oracle_expm1f(2.0f * ax);
+            t = 1.0f - 2.0f / (t + 2.0f);
+        }
+    } else if (w > 0x3e82c578u) {     /* |x| > log(5/3) / 2 */
+        t = llz_oracle_expm1f(2.0f * ax);
+        t = t / (t + 2.0f);
+    } else if (w >= 0x00800000u) {    /* normal */
+        t = llz_oracle_expm1f(-2.0f * ax);
+        t = -t / (t + 2.0f);
+    } else {                          /* subnormal or zero */
+        t = ax;
+    }
+    return sign ? -t : t;
+}
+
+void llz_oracle_expm1f_array(const float *in, float *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = llz_oracle_expm1f(in[i]);
+}
+
+void llz_oracle_tanhf_array(const float *in, float *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = llz_oracle_tanhf(in[i]);
+}
+
+/* main.zig:653-666: the decode loop's post-processing of the final logits
+ * before Sampler.sample: soft-capping v = tanh(v / s) * s when s > 0, then
+ * the logit scale v *= 1 / scale when scale is neither 1 nor 0 (the inverse
+ * is one f32 division, main.zig:664).  In place. */
+void llz_oracle_logit_post(float *x, int64_t n, float softcap, float logit_scale)
+{
+    if (softcap > 0.0f)
+        for (int64_t i = 0; i < n; ++i) x[i] = llz_oracle_tanhf(x[i] / softcap) * softcap;
+    if (logit_scale != 1.0f && logit_scale != 0.0f) {
+        const float inv = 1.0f / logit_scale;
+        for (int64_t i = 0; i < n; ++i) x[i] *= inv;
+    }
 }
 
 /* ------------------------------------------------------------------------

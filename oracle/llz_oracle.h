@@ -78,9 +78,19 @@ enum {
 /* Zig std restatements. */
 float llz_oracle_expf(float x);
 float llz_oracle_logf(float x);
+/* std.math.expm1 / std.math.tanh for f32 (musl expm1f.c / tanhf.c). */
+float llz_oracle_expm1f(float x);
+float llz_oracle_tanhf(float x);
 /* Element-wise over arrays (parity tests of the device math). */
 void llz_oracle_expf_array(const float *in, float *out, int64_t n);
 void llz_oracle_logf_array(const float *in, float *out, int64_t n);
+void llz_oracle_expm1f_array(const float *in, float *out, int64_t n);
+void llz_oracle_tanhf_array(const float *in, float *out, int64_t n);
+
+/* main.zig:653-666, the decode loop's final-logit post-processing before
+ * Sampler.sample, in place: v = tanh(v / softcap) * softcap when softcap > 0,
+ * then v *= 1 / logit_scale when logit_scale is neither 1 nor 0. */
+void llz_oracle_logit_post(float *x, int64_t n, float softcap, float logit_scale);
 uint64_t llz_oracle_splitmix64_next(uint64_t *state);
 void llz_oracle_xoshiro_seed(uint64_t s[4], uint64_t seed);
 uint64_t llz_oracle_xoshiro_next(uint64_t s[4]);

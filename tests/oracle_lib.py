@@ -77,6 +77,14 @@ def lib():
         L.llz_oracle_expf_array.restype = None
         L.llz_oracle_logf_array.argtypes = [fp, fp, i64]
         L.llz_oracle_logf_array.restype = None
+        for name in ("llz_oracle_expm1f", "llz_oracle_tanhf"):
+            getattr(L, name).restype = C.c_float
+            getattr(L, name).argtypes = [C.c_float]
+        for name in ("llz_oracle_expm1f_array", "llz_oracle_tanhf_array"):
+            getattr(L, name).restype = None
+            getattr(L, name).argtypes = [fp, fp, i64]
+        L.llz_oracle_logit_post.restype = None
+        L.llz_oracle_logit_post.argtypes = [fp, i64, C.c_float, C.c_float]
         L.llz_oracle_splitmix64_next.restype = u64
         L.llz_oracle_splitmix64_next.argtypes = [C.POINTER(u64)]
         L.llz_oracle_xoshiro_seed.argtypes = [C.POINTER(u64), u64]
@@ -211,6 +219,27 @@ def logf_array(x: np.ndarray) -> np.ndarray:
     out = np.empty_like(x)
     lib().llz_oracle_logf_array(_fptr(x), _fptr(out), x.size)
     return out
+
+
+def expm1f_array(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().llz_oracle_expm1f_array(_fptr(x), _fptr(out), x.size)
+    return out
+
+
+def tanhf_array(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().llz_oracle_tanhf_array(_fptr(x), _fptr(out), x.size)
+    return out
+
+
+def logit_post(x: np.ndarray, softcap: float = 0.0, logit_scale: float = 1.0) -> np.ndarray:
+    """main.zig:653-666 on a copy of the logits (any shape)."""
+    y = np.array(x, dtype=np.float32, order="C", copy=True)
+    lib().llz_oracle_logit_post(_fptr(y), y.size, C.c_float(softcap), C.c_float(logit_scale))
+    return y
 
 
 def uniforms(seed: int, count: int) -> np.ndarray:

@@ -87,8 +87,8 @@ def test_argument_validation_without_gpu():
 
     def call(logits=fake, stride=16, rows=1, vocab=16, c=C.byref(cfg), prev=None, n_prev=0, pstride=0,
              u=fake, tok=fake, con=None, ws=fake, wsb=1 << 30):
-        return L.llz_sample_rows(logits, stride, rows, vocab, c, prev, n_prev, pstride, u, tok, con, None,
-                                 ws, wsb, None)
+        return L.llz_sample_rows(logits, stride, rows, vocab, c, None, prev, n_prev, pstride, u, tok, con,
+                                 None, ws, wsb, None)
 
     assert call(logits=None) == llz.LLZ_E_INVALID_ARG
     assert call(rows=0) == llz.LLZ_E_INVALID_ARG
@@ -103,9 +103,9 @@ def test_argument_validation_without_gpu():
     assert call(c=C.byref(nan_cfg)) == llz.LLZ_E_INVALID_ARG
     assert call(ws=None) == llz.LLZ_E_WORKSPACE
     assert call(wsb=16) == llz.LLZ_E_WORKSPACE
-    assert L.llz_argmax_rows(None, 16, 1, 16, fake, None) == llz.LLZ_E_INVALID_ARG
-    assert L.llz_argmax_rows(fake, 16, 1, 16, None, None) == llz.LLZ_E_INVALID_ARG
-    assert L.llz_debug_math(None, None, None, 4, None) == llz.LLZ_E_INVALID_ARG
+    assert L.llz_argmax_rows(None, 16, 1, 16, None, fake, None) == llz.LLZ_E_INVALID_ARG
+    assert L.llz_argmax_rows(fake, 16, 1, 16, None, None, None) == llz.LLZ_E_INVALID_ARG
+    assert L.llz_debug_math(None, None, None, None, None, 4, None) == llz.LLZ_E_INVALID_ARG
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert L.llz_strerror(code)
 

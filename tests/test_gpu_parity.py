@@ -21,7 +21,7 @@ def _f32bits(a) -> np.ndarray:
     return np.asarray(a, dtype=np.float32).view(np.uint32)
 
 
-def run_gpu(x: np.ndarray, params, u: np.ndarray, cuda, prev=None, kept_cap: int = 0):
+def run_gpu(x: np.ndarray, params, u: np.ndarray, cuda, prev=None, kept_cap: int = 0, post=None):
     import torch
 
     cfg = llz.SamplerConfig.of(params)
@@ -31,7 +31,7 @@ def run_gpu(x: np.ndarray, params, u: np.ndarray, cuda, prev=None, kept_cap: int
     if prev is not None:
         pt = torch.from_numpy(np.ascontiguousarray(prev, dtype=np.int32)).to(cuda)
     cap = kept_cap or 64
-    res = llz.sample_rows(xt, cfg, ut, pt, kept_cap=cap, stats=True)
+    res = llz.sample_rows(xt, cfg, ut, pt, post=post, kept_cap=cap, stats=True)
     torch.cuda.synchronize()
     return dict(
         tokens=res.tokens.cpu().numpy().view(np.uint32),

@@ -384,3 +384,94 @@ def test_planted_oracle_mistake_is_caught():
     o = O.sample_row(x, w.params, 0.5)
     assert f32bits(o.sum) == f32bits(seq)
     assert f32bits(pairwise) != f32bits(seq)
+
+
+# ---------------------------------------------------------------------------
+# expm1f / tanhf (musl expm1f.c / tanhf.c, the functions behind Zig's f32
+# std.math.expm1 / tanh) and main.zig:653-666's post-processing.  The bit
+# patterns Zig produces cannot be compared here (no Zig toolchain); what
+# pins the restatement: musl's documented accuracy (< 1 ulp for expm1f,
+# measured <= 2.05 ulp for tanhf over the sweeps), the branch structure
+# (odd symmetry, saturation, the small-|x| identity), and a planted mistake
+# that the accuracy check catches.
+# ---------------------------------------------------------------------------
+def _sweep(lo, hi, step):
+    return np.arange(lo, hi, step, dtype=np.uint64).astype(np.uint32).view(np.float32)
+
+
+def test_expm1f_within_one_ulp():
+    x = np.concatenate([_sweep(0x80000000, 0xC18AA123, 89),    # -0 .. -17.3 (below: -1)
+                        _sweep(0x00000000, 0x42B17180, 89)])    # 0 .. 88.72 (above: overflow)
+    got = O.expm1f_array(x)
+    want = np.expm1(x.astype(np.float64))
+    ok = np.abs(want) >= np.finfo(np.float32).tiny
+    err = _ulp_err(got[ok], want[ok])
+    assert err.max() < 1.0, f"max error {err.max():.3f} ulp"
+
+
+def test_expm1f_special_values():
+    L = O.lib()
+    assert L.llz_oracle_expm1f(0.0) == 0.0
+    assert math.copysign(1.0, L.llz_oracle_expm1f(-0.0)) == -1.0
+    assert L.llz_oracle_expm1f(-np.inf) == -1.0 and L.llz_oracle_expm1f(-30.0) == -1.0
+    assert L.llz_oracle_expm1f(np.inf) == np.inf and L.llz_oracle_expm1f(89.0) == np.inf
+    assert np.isnan(L.llz_oracle_expm1f(np.nan))
+    t = np.float32(2.0 ** -26)  # |x| < 2^-25 returns x
+    assert L.llz_oracle_expm1f(float(t)) == t
+
+
+def test_tanhf_accuracy_and_structure():
+    x = np.concatenate([_sweep(0x00800000, 0x41300000, 53),    # normal .. 11
+                        _sweep(0x3E700000, 0x3F200000, 3)])    # the two branch edges, dense
+    got = O.tanhf_array(x)
+    want = np.tanh(x.astype(np.float64))
+    err = _ulp_err(got, want)
+    assert err.max() <= 2.5, f"max error {err.max():.3f} ulp"
+    assert np.mean(err <= 0.5) > 0.85          # mostly correctly rounded
+    # odd: tanh(-x) == -tanh(x) bit for bit
+    assert np.array_equal(O.tanhf_array(-x).view(np.uint32), (-got).view(np.uint32))
+    # saturation: exactly 1 for |x| > 10 and where tanh rounds to 1
+    big = _sweep(0x41200001, 0x7F800001, 997)
+    assert np.all(O.tanhf_array(big) == 1.0) and np.all(O.tanhf_array(-big) == -1.0)
+    assert O.tanhf_array(np.float32([9.5]))[0] == 1.0
+    # tiny arguments: tanh(x) == x (subnormals returned as they are)
+    tiny = np.float32([1e-40, 2.0 ** -126, 1e-10, -3e-9])
+    assert np.array_equal(O.tanhf_array(tiny), tiny)
+    assert O.tanhf_array(np.float32([0.0]))[0] == 0.0
+    assert np.isnan(O.tanhf_array(np.float32([np.nan]))[0])
+
+
+def test_tanhf_planted_mistake_is_caught():
+    """A tanh built on an expm1 with a wrong coefficient (Q1 off by 10%)
+    violates the accuracy bound the test above enforces."""
+    x = _sweep(0x3E900000, 0x3F800000, 101).astype(np.float64)
+    q1, q2 = -3.3333212137e-2 * 1.1, 1.5807170421e-3
+
+    def expm1_bad(v):  # k == 0 branch of the algorithm, in float64
+        hfx = 0.5 * v
+        hxs = v * hfx
+        r1 = 1.0 + hxs * (q1 + hxs * q2)
+        t = 3.0 - r1 * hfx
+        e = hxs * ((r1 - t) / (6.0 - v * t))
+        return v - (v * e - hxs)
+
+    bad = np.array([expm1_bad(2 * v) / (expm1_bad(2 * v) + 2) for v in x], np.float32)
+    assert _ulp_err(bad, np.tanh(x)).max() > 2.5
+
+
+def test_logit_post_closed_forms():
+    x = np.float32([-3.0, -0.5, 0.0, 0.25, 7.0, 100.0])
+    # the scale: v * RN(1/scale); 1/0.5 == 2 exactly
+    assert np.array_equal(O.logit_post(x, 0.0, 0.5), x * np.float32(2.0))
+    # scale 1 and 0 (and a non-positive cap) leave the logits alone
+    for s in (1.0, 0.0):
+        assert np.array_equal(O.logit_post(x, -2.0, s), x)
+    # the soft-cap: tanh(v / s) * s with f32 operations; bounded by s, odd, monotone
+    y = O.logit_post(x, 30.0, 1.0)
+    want = O.tanhf_array(x / np.float32(30.0)) * np.float32(30.0)
+    assert np.array_equal(y, want)
+    assert np.all(np.abs(y) <= 30.0) and np.all(np.diff(y) >= 0)
+    assert np.array_equal(O.logit_post(-x, 30.0, 1.0), -y)
+    # both: cap first, then the scale (main.zig:653-666's order)
+    both = O.logit_post(x, 30.0, 0.5)
+    assert np.array_equal(both, y * np.float32(2.0))
