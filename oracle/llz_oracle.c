@@ -153,6 +153,17 @@ float llz_oracle_logf(float x)
     return s * (hfsq + R) + dk * ln2_lo - hfsq + f + dk * ln2_hi;
 }
 
+/* Sensitivity study only (oracle/libm_sensitivity.py): when set, the chain
+ * evaluates its exp and log with the C library's expf / logf instead of the
+ * msun restatement above, to measure how much an ulp-level difference in
+ * Zig's std.math.exp / @log could change kept sets and tokens. */
+static int g_use_libm = 0;
+
+void llz_oracle_use_libm(int on) { g_use_libm = on; }
+
+static inline float chain_expf(float x) { return g_use_libm ? expf(x) : llz_oracle_expf(x); }
+static inline float chain_logf(float x) { return g_use_libm ? logf(x) : llz_oracle_logf(x); }
+
 void llz_oracle_expf_array(const float *in, float *out, int64_t n)
 {
     for (int64_t i = 0; i < n; ++i) out[i] = llz_oracle_expf(in[i]);
@@ -466,7 +477,7 @@ static int sample_row_impl(const float *logits, int64_t n, const llz_oracle_cfg 
     /* :83-88 sequential f32 sum in index order */
     float sum = 0.0f;
     for (int64_t i = 0; i < n; ++i) {
-        float p = llz_oracle_expf((penalized[i] - max_logit) / cfg->temperature);
+        float p = chain_expf((penalized[i] - max_logit) / cfg->temperature);
         probs[i] = p;
         sum += p;
     }
@@ -519,7 +530,7 @@ static int sample_row_impl(const float *logits, int64_t n, const llz_oracle_cfg 
         float entropy = 0.0f;
         for (int64_t i = 0; i < n; ++i) {
             float p = probs[i];
-            if (p > 0.0f) entropy -= p * llz_oracle_logf(p);
+            if (p > 0.0f) entropy -= p * chain_logf(p);
         }
         out->entropy = entropy;
         dev = (float *)malloc((size_t)n * sizeof(float));
@@ -527,7 +538,7 @@ static int sample_row_impl(const float *logits, int64_t n, const llz_oracle_cfg 
         if (!dev || !typical_order) { rc = -1; goto done; }
         for (int64_t i = 0; i < n; ++i) {
             float p = probs[i];
-            float surprise = p > 0.0f ? -llz_oracle_logf(p) : INFINITY;
+            float surprise = p > 0.0f ? -chain_logf(p) : INFINITY;
             dev[i] = fabsf(surprise - entropy);
         }
         for (int64_t i = 0; i < n; ++i) typical_order[i] = (uint32_t)i;

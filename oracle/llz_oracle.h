@@ -98,6 +98,11 @@ float llz_oracle_random_f32(uint64_t s[4]);
 /* Fill `out[0..count)` with successive Random.float(f32) draws. */
 void llz_oracle_uniforms(uint64_t s[4], float *out, int64_t count);
 
+/* Sensitivity study only: 1 = the chain uses the C library's expf / logf
+ * in place of the msun restatement; 0 (default) = the restatement.
+ * Process-wide; set it before sampling. */
+void llz_oracle_use_libm(int on);
+
 /* sampler.zig:31-41 */
 uint32_t llz_oracle_argmax(const float *logits, int64_t n);
 

@@ -83,6 +83,8 @@ def lib():
         for name in ("llz_oracle_expm1f_array", "llz_oracle_tanhf_array"):
             getattr(L, name).restype = None
             getattr(L, name).argtypes = [fp, fp, i64]
+        L.llz_oracle_use_libm.restype = None
+        L.llz_oracle_use_libm.argtypes = [C.c_int]
         L.llz_oracle_logit_post.restype = None
         L.llz_oracle_logit_post.argtypes = [fp, i64, C.c_float, C.c_float]
         L.llz_oracle_splitmix64_next.restype = u64

@@ -88,6 +88,72 @@ def test_uniform_stream_properties():
     assert np.array_equal(u, O.uniforms(0xDEADBEEF, 200000))
 
 
+def _gof_checks(u: np.ndarray):
+    """Goodness of fit of a Random.float(f32) stream (raises AssertionError).
+    The construction: exponent 126 - clz(draw), mantissa = the draw's low 23
+    bits, so (1) u is uniform on (0, 1); (2) the binade [2^-(k+1), 2^-k)
+    holds a fraction 2^-(k+1) of the draws; (3) within a binade the mantissa
+    is uniform and independent of the binade."""
+    from scipy import stats
+
+    n = u.size
+    assert np.all((u > 0) & (u < 1)), "u outside (0, 1)"
+    # (1) chi-square over 4096 equal bins
+    counts = np.bincount(np.minimum((u.astype(np.float64) * 4096).astype(np.int64), 4095), minlength=4096)
+    p1 = stats.chisquare(counts).pvalue
+    assert p1 > 1e-6, f"bins: p = {p1:.3g}"
+    # (2) binade frequencies 2^-(k+1), k = 0 .. 15 (and the rest pooled)
+    e = (u.view(np.uint32) >> 23).astype(np.int64)
+    k = np.minimum(126 - e, 16)
+    obs = np.bincount(k, minlength=17)
+    exp = np.array([2.0 ** -(i + 1) for i in range(16)] + [2.0 ** -16]) * n
+    p2 = stats.chisquare(obs, exp).pvalue
+    assert p2 > 1e-6, f"binades: p = {p2:.3g}"
+    # (3) the top 6 mantissa bits are uniform within each of the first four binades
+    m6 = (u.view(np.uint32) >> 17) & 63
+    table = np.stack([np.bincount(m6[k == i], minlength=64) for i in range(4)])
+    p3 = stats.chi2_contingency(table).pvalue
+    assert p3 > 1e-6, f"mantissa vs binade: p = {p3:.3g}"
+    for i in range(4):
+        pi = stats.chisquare(table[i]).pvalue
+        assert pi > 1e-6, f"mantissa in binade {i}: p = {pi:.3g}"
+    # (4) the low mantissa bits stay random in smaller binades (a fixed-point
+    # uniform has fewer random bits there: its lowest k bits are 0 in binade k)
+    low2 = u.view(np.uint32) & 3
+    for i in range(1, 7):
+        c = np.bincount(low2[k == i], minlength=4)
+        pi = stats.chisquare(c).pvalue
+        assert pi > 1e-6, f"low mantissa bits in binade {i}: p = {pi:.3g}"
+
+
+def test_random_float_goodness_of_fit():
+    """Random.float(f32) (sampler.zig:162) over a long stream: the
+    construction's three distributional properties hold."""
+    _gof_checks(O.uniforms(0xDEADBEEF, 1 << 21))
+
+
+def test_random_float_goodness_of_fit_catches_construction_mistakes():
+    """Plausible restatement mistakes fail the same checks: an exponent off
+    by one (127 - clz), the mantissa from the draw's top bits, and a plain
+    24-bit uniform (no clz exponent)."""
+    L = O.lib()
+    st = (C.c_uint64 * 4)()
+    L.llz_oracle_xoshiro_seed(st, 99)
+    raw = np.array([L.llz_oracle_xoshiro_next(st) for _ in range(1 << 19)], dtype=np.uint64)
+    lz = np.array([64 - int(r).bit_length() for r in raw.tolist()], dtype=np.int64)
+    good = (((126 - lz) << 23) | (raw & 0x7FFFFF).astype(np.int64)).astype(np.uint32).view(np.float32)
+    _gof_checks(good)  # the correct construction from the same draws passes
+    off_by_one = (((127 - lz) << 23) | (raw & 0x7FFFFF).astype(np.int64)).astype(np.uint32).view(np.float32)
+    top_bits = (((126 - lz) << 23) | ((raw >> 41) & 0x7FFFFF).astype(np.int64)).astype(np.uint32).view(np.float32)
+    plain24 = ((raw >> 40).astype(np.float64) * 2.0 ** -24).astype(np.float32)
+    plain24 = plain24[plain24 > 0]
+    for name, bad in (("exponent off by one", off_by_one), ("mantissa from the top bits", top_bits),
+                      ("plain 24-bit uniform", plain24)):
+        with pytest.raises(AssertionError):
+            _gof_checks(bad)
+            raise RuntimeError(f"{name} passed the goodness-of-fit checks")
+
+
 # ---------------------------------------------------------------------------
 # exp / log (sampler.zig:85 std.math.exp, :131,136 @log) -- msun algorithms
 # ---------------------------------------------------------------------------
@@ -475,3 +541,21 @@ def test_logit_post_closed_forms():
     # both: cap first, then the scale (main.zig:653-666's order)
     both = O.logit_post(x, 30.0, 0.5)
     assert np.array_equal(both, y * np.float32(2.0))
+
+
+def test_libm_switch_changes_results_and_restores():
+    """The sensitivity switch (oracle/libm_sensitivity.py): with the C
+    library's expf/logf some probabilities of a headline row change, and the
+    default (the msun restatement) comes back bit for bit."""
+    w = WORKLOADS["headline"]
+    x = w.logits(4)
+    u = O.uniforms(w.uniform_seed, 4)
+    base = [O.sample_row(x[r], w.params, u[r]).probs.copy() for r in range(4)]
+    O.lib().llz_oracle_use_libm(1)
+    try:
+        alt = [O.sample_row(x[r], w.params, u[r]).probs.copy() for r in range(4)]
+    finally:
+        O.lib().llz_oracle_use_libm(0)
+    again = [O.sample_row(x[r], w.params, u[r]).probs.copy() for r in range(4)]
+    assert any(not np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(base, alt))
+    assert all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(base, again))
