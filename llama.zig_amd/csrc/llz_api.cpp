@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -45,25 +46,40 @@ uint32_t post_bits(const llz_logit_post* post) {
   return b;
 }
 
-// Workspace layout of one llz_sample_rows call.
+// Workspace layout of one llz_sample_rows call: per row, its status word,
+// candidate list and special-queue overflow (32 KB); per call, a pool of
+// min(rows, kFbSlots) full-row fallback buffer sets (25 B per logit each)
+// with their owner words; the penalised copy only for windows too long to
+// fuse.
 struct Layout {
-  size_t status, cand, penal, fb, fb_mask, total;
+  size_t status, cand, qovf, owner, fb, fb_mask, penal, total;
+  int fb_slots;
   bool has_penal;
 };
 
 Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int32_t n_prev) {
   Layout L{};
   const size_t r = (size_t)rows, n = (size_t)vocab;
+  L.fb_slots = rows < kFbSlots ? rows : kFbSlots;
+  const size_t ns = (size_t)L.fb_slots;
   size_t off = 0;
   L.status = off;  off = align_up(off + r * sizeof(uint32_t));
   L.cand = off;    off = align_up(off + r * (size_t)kCandCap * sizeof(uint64_t));
+  L.qovf = off;    off = align_up(off + r * (size_t)kQovfRow * sizeof(uint32_t));
+  L.owner = off;   off = align_up(off + ns * sizeof(uint64_t));
+  L.fb = off;      off = align_up(off + 6 * ns * n * sizeof(uint32_t));
+  L.fb_mask = off; off = align_up(off + ns * n);
   L.has_penal = penalty_copy(cfg, n_prev);
   L.penal = off;   if (L.has_penal) off = align_up(off + r * n * sizeof(float));
-  L.fb = off;      off = align_up(off + 6 * r * n * sizeof(uint32_t));
-  L.fb_mask = off; off = align_up(off + r * n);
   L.total = off;
   return L;
 }
+
+// Per-call epochs tag the fallback slots a call holds (llz_select.h).  Any
+// owner word but the current epoch means free, so a workspace needs no
+// clearing; the counter starts at an arbitrary 62-bit value so that stale
+// memory is unlikely to hold a live epoch.
+std::atomic<uint64_t> g_epoch{0x2d5f7a19c3e4b681ull};
 
 // Candidate threshold on e = exp((v - max) / T).  Every element that can be
 // kept must satisfy e >= theta, or the row takes the full fallback.
@@ -207,6 +223,8 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   P.rpen = cfg->repetition_penalty;
   P.pen_w = (xf_src & kXfPen) ? window : 0;
   P.prev_stride = prev_stride;
+  P.fb_slots = L.fb_slots;
+  P.epoch = g_epoch.fetch_add(1, std::memory_order_relaxed) & ((1ull << 62) - 1);
   // LLZ_TEST_QUEUE_CAP: a smaller special-queue chunk, so that tests reach
   // the chunked queue on ordinary rows (the kernel clamps it to its own)
   {
@@ -230,6 +248,8 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   Q.cand = (uint64_t*)(ws + L.cand);
   Q.fb = (uint32_t*)(ws + L.fb);
   Q.fb_mask = (uint8_t*)(ws + L.fb_mask);
+  Q.fb_owner = (unsigned long long*)(ws + L.owner);
+  Q.qovf = (uint32_t*)(ws + L.qovf);
   Q.prev_win = (xf_src & kXfPen) ? d_prev_tokens + (n_prev - window) : nullptr;
   e = launch_sample(P, Q, g_ev_begin, g_ev_end, st);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;

@@ -8,6 +8,9 @@ namespace llz {
 
 constexpr int kCandCap = 2048;  // candidate list capacity per row (power of two)
 constexpr int kPenMax = 64;     // fused repetition penalty: window entries at most (one per lane)
+constexpr int kQovfWave = 512;  // k_stats special-queue overflow entries per wave (four chunks)
+constexpr int kQovfRow = 8 * kQovfWave;  // ... per row (eight waves)
+constexpr int kFbSlots = 64;    // full-row fallback buffers per call at most (rows beyond wait for one)
 
 // RowParams.flags
 constexpr uint32_t kFlagTIsOne = 1u;    // temperature == 1.0f exactly: (v - m) / T == v - m
@@ -48,6 +51,8 @@ struct RowParams {
   float rpen;        // repetition penalty (kXfPen)
   int32_t pen_w;     // kXfPen: window length (<= kPenMax)
   int64_t prev_stride;
+  int32_t fb_slots;  // full-row fallback buffers in the workspace
+  uint64_t epoch;    // this call's tag: a fallback slot whose owner word holds it is in use
 };
 
 struct RowPtrs {
@@ -62,9 +67,17 @@ struct RowPtrs {
   float* row_stats;
   uint32_t* status;
   uint64_t* cand;         // [rows][kCandCap] candidate list
-  uint32_t* fb;           // 6 x [rows][n] u32 (fallback sort buffers)
-  uint8_t* fb_mask;       // [rows][n]
+  uint32_t* fb;           // 6 x [fb_slots][n] u32 (full-row fallback sort buffers)
+  uint8_t* fb_mask;       // [fb_slots][n]
+  unsigned long long* fb_owner;  // [fb_slots] epoch of the row using each slot
+  uint32_t* qovf;         // [rows][kQovfRow] k_stats special-queue overflow
   const uint32_t* prev_win;  // kXfPen: row 0's window (its last pen_w history tokens)
+};
+
+// k_stats's one kernel argument.
+struct KArgs {
+  RowParams P;
+  RowPtrs Q;
 };
 
 hipError_t launch_penalty(const float* logits, int64_t stride, int rows, int n, const uint32_t* prev,

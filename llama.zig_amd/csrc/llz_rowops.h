@@ -50,8 +50,8 @@ __device__ __forceinline__ bool amax_better(float v, uint32_t i, float bv, uint3
 
 // sampleArgmax over one row with the whole workgroup.  A NaN at index 0
 // is never replaced by the reference's loop, so the answer is then 0.
-template <int NT>
-__device__ uint32_t wg_argmax_row(const RowSrc& x, int n, WgScratch<NT>& sh, int& bank) {
+template <int NT, class Src>
+__device__ uint32_t wg_argmax_row(const Src& x, int n, WgScratch<NT>& sh, int& bank) {
   const int t = (int)threadIdx.x;
   float bv = __builtin_nanf("");
   uint32_t bi = 0xffffffffu;

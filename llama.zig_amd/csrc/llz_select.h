@@ -238,7 +238,8 @@ __device__ __forceinline__ bool wave_resolve(float& s, int& done, const SliceSta
 
 // sampler.zig:83-88: the exact sequential f32 normaliser of one row, plus the
 // candidate list (every element with e >= cand_theta).
-__device__ float row_normaliser(const RowSrc& X, int n, const RowParams& P, SampleShared& sh, int& bank,
+template <class Src>
+__device__ float row_normaliser(const Src& X, int n, const RowParams& P, SampleShared& sh, int& bank,
                                 float& m_out, float m_known) {
   constexpr int W = kNT / kWave;
   constexpr int GE = W * kSlice;    // elements per group
@@ -469,7 +470,8 @@ __device__ int prefix_filters(const List& L, int M, float p_nc, int n, const Row
 }
 
 // Entropy sum over the whole row in index order (sampler.zig:129-132).
-__device__ float entropy_pass(const RowSrc& X, int n, float m, float S, const RowParams& P,
+template <class Src>
+__device__ float entropy_pass(const Src& X, int n, float m, float S, const RowParams& P,
                               SampleShared& sh, int& bank) {
   const bool t1 = (P.flags & kFlagTIsOne) != 0;
   const bool vec = (P.flags & kFlagVecSrc) != 0;
@@ -518,10 +520,32 @@ struct NormResult {
   int bank;
 };
 
+// k_stats's argument (KArgs) where the kernel received it, in its argument
+// segment: the out-of-line fallbacks read it through this pointer instead of
+// from a copy in their stack frame (a copy the compiler stores in every
+// launch's prologue).  The segment pointer exists in the kernel only (a
+// callee's builtin yields null), so the kernel takes it and passes it down.
+__device__ __forceinline__ const KArgs* kernel_args_ptr() {
+  return (const KArgs*)__builtin_amdgcn_kernarg_segment_ptr();  // address-space cast to a generic pointer
+}
+
+// The chain's reader of row `row` for a reader type.
+template <class Src>
+__device__ __forceinline__ Src make_src(const RowParams& P, const RowPtrs& Q, int row, const PenShared* pen) {
+  if constexpr (std::is_same<Src, RowSrc>::value) {
+    return row_src(P, Q, row, pen);
+  } else {
+    return PlainSrc{Q.src + (int64_t)row * P.src_stride};
+  }
+}
+
 // The streaming normaliser (sampler.zig:83-88) for a row k_stats could not
 // certify; fills the candidate list in LDS.
-__device__ __noinline__ NormResult select_norm_fallback(const RowParams P, const RowSrc X, SampleShared& sh,
+template <class Src>
+__device__ __noinline__ NormResult select_norm_fallback(const KArgs* A, const PenShared* pen, SampleShared& sh,
                                                         int bank, float m_known) {
+  const RowParams& P = A->P;
+  const Src X = make_src<Src>(P, A->Q, blockIdx.x, pen);
   if (threadIdx.x == 0) sh.cand_count = 0;
   NormResult r;
   r.S = row_normaliser(X, P.n, P, sh, bank, r.m, m_known);
@@ -529,8 +553,9 @@ __device__ __noinline__ NormResult select_norm_fallback(const RowParams P, const
   return r;
 }
 
-__device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q, SampleShared& sh, int bank,
-                                             float m, float S, uint32_t path, const PenShared* pen);
+template <class Src>
+__device__ __noinline__ void select_full_row(const KArgs* A, const PenShared* pen, SampleShared& sh, int bank,
+                                             float m, float S, uint32_t path);
 
 constexpr int kShortMax = 256;  // longest candidate list of the short path
 
@@ -677,10 +702,11 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
 // calls it; `sh` may alias the caller's shared memory once all of it is read.
 // pre_ok: thread 64 + i holds candidate i in cand_pre for i < cand_n0, and
 // cc_in <= 448 (the later ones are read here).
+template <class Src>
 __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q, SampleShared& sh, float m,
                                            float S, uint32_t cc_in, bool uncertified, float u_row, bool pre_ok,
-                                           uint64_t cand_pre, uint32_t cand_n0, const RowSrc& X,
-                                           const PenShared* pen) {
+                                           uint64_t cand_pre, uint32_t cand_n0, const Src& X, const Src& O,
+                                           const PenShared* pen, const KArgs* A) {
   int bank = 0;
   const int row = blockIdx.x;
   const int t = (int)threadIdx.x;
@@ -688,7 +714,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   uint32_t path = 0;
   if (uncertified) {
     // the streaming normaliser (sampler.zig:83-88) fills the candidate list in LDS
-    const NormResult r = select_norm_fallback(P, X, sh, bank, m);
+    const NormResult r = select_norm_fallback<Src>(A, pen, sh, bank, m);
     S = r.S;
     m = r.m;
     bank = r.bank;
@@ -710,9 +736,6 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
 
   // ---- 3. sum <= 0 exit: sampleArgmax of the caller's logits (:89)
   if (S <= 0.0f) {
-    // (pen is null exactly when the kernel reads rows untransformed)
-    const RowSrc O = pen ? row_orig(P, Q, row)
-                         : RowSrc{Q.orig + (int64_t)row * P.orig_stride, 0u, 1.0f, 1.0f, 1.0f, nullptr};
     token = wg_argmax_row<kNT>(O, n, sh.wg, bank);
     path = kPathSumLe0;
     if (t == 0) {
@@ -760,7 +783,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   const bool ovf = cc > (uint32_t)kCap;
   const int c = ovf ? kCap : (int)cc;
   if (!ovf && c <= kShortMax && !(P.typical_p > 0.0f && P.typical_p < 1.0f)) {
-    if (!select_short(P, Q, sh, c, m, S, path, u_row)) select_full_row(P, Q, sh, bank, m, S, path, pen);
+    if (!select_short(P, Q, sh, c, m, S, path, u_row)) select_full_row<Src>(A, pen, sh, bank, m, S, path);
     return;
   }
   const int csort = next_pow2(c);
@@ -864,19 +887,22 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   }
 
   // ---- full-row fallback: every probability, stable radix sort, filters
-  select_full_row(P, Q, sh, bank, m, S, path, pen);
+  select_full_row<Src>(A, pen, sh, bank, m, S, path);
 }
 
 // The full-row fallback of k_select: every probability, stable radix sort of
 // the whole row in the workspace, the filters and the draw over it.
-__device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q, SampleShared& sh, int bank,
-                                             float m, float S, uint32_t path, const PenShared* pen) {
+template <class Src>
+__device__ __noinline__ void select_full_row(const KArgs* A, const PenShared* pen, SampleShared& sh, int bank,
+                                             float m, float S, uint32_t path) {
+  const RowParams& P = A->P;
+  const RowPtrs& Q = A->Q;
   const int row = blockIdx.x;
+  const Src X = make_src<Src>(P, Q, row, pen);
   const int t = (int)threadIdx.x;
   const int n = P.n;
   const bool t1 = (P.flags & kFlagTIsOne) != 0;
   const bool vec = (P.flags & kFlagVecSrc) != 0;
-  const RowSrc X = row_src(P, Q, row, pen);
   const bool typical = P.typical_p > 0.0f && P.typical_p < 1.0f;
   const float u = Q.uniforms[row];
   int K = 0;
@@ -891,13 +917,44 @@ __device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q,
     }
     return;
   }
-  const int64_t fo = (int64_t)row * n;
-  uint32_t* Ak = Q.fb + 0 * (int64_t)P.rows * n + fo;
-  uint32_t* Av = Q.fb + 1 * (int64_t)P.rows * n + fo;
-  uint32_t* Bk = Q.fb + 2 * (int64_t)P.rows * n + fo;
-  uint32_t* Bv = Q.fb + 3 * (int64_t)P.rows * n + fo;
-  uint32_t* Ck = Q.fb + 4 * (int64_t)P.rows * n + fo;
-  uint32_t* Cv = Q.fb + 5 * (int64_t)P.rows * n + fo;
+  // one of the call's fb_slots buffer sets, claimed for this row: a slot is
+  // free for this call when its owner word holds anything but this call's
+  // epoch.  At most fb_slots rows hold one at a time; a row that finds none
+  // waits for a holder (a running workgroup that needs nothing else) to
+  // release one.  The fences make the previous holder's writes, possibly
+  // from another XCD's L2, land before this row touches the buffers.
+  if (t == 0) {
+    const unsigned long long E = P.epoch;
+    int got = -1;
+    for (uint32_t spin = 0; got < 0 && spin < (1u << 20); ++spin) {
+      for (int k = 0; k < P.fb_slots && got < 0; ++k) {
+        const int s = (row + k) % P.fb_slots;
+        const unsigned long long old = __hip_atomic_load(&Q.fb_owner[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old != E && atomicCAS(&Q.fb_owner[s], old, E) == old) got = s;
+      }
+      if (got < 0) __builtin_amdgcn_s_sleep(127);
+    }
+    __threadfence();
+    sh.misc[1] = (uint32_t)got;
+  }
+  __syncthreads();
+  const int slot = (int)sh.misc[1];
+  if (slot < 0 || slot >= P.fb_slots) {  // no slot within the wait bound
+    if (t == 0) {
+      Q.tokens[row] = 0xffffffffu;
+      if (Q.consumed) Q.consumed[row] = 0;
+      if (Q.status) Q.status[row] = path | kPathError;
+    }
+    return;
+  }
+  const int64_t fo = (int64_t)slot * n;
+  const int64_t fs = (int64_t)P.fb_slots * n;
+  uint32_t* Ak = Q.fb + 0 * fs + fo;
+  uint32_t* Av = Q.fb + 1 * fs + fo;
+  uint32_t* Bk = Q.fb + 2 * fs + fo;
+  uint32_t* Bv = Q.fb + 3 * fs + fo;
+  uint32_t* Ck = Q.fb + 4 * fs + fo;
+  uint32_t* Cv = Q.fb + 5 * fs + fo;
   uint8_t* mask = Q.fb_mask + fo;
   for (int base = 0; base < n; base += kTile) {
     float v[kV];
@@ -992,6 +1049,11 @@ __device__ __noinline__ void select_full_row(const RowParams P, const RowPtrs Q,
     }
     if (Q.status) Q.status[row] = path;
   }
+  // release the slot once every thread is done with it (a value no later
+  // call's epoch takes)
+  __threadfence();
+  __syncthreads();
+  if (t == 0) atomicExch(&Q.fb_owner[slot], P.epoch ^ (1ull << 63));
 }
 
 }  // namespace llz

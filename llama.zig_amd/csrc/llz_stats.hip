@@ -6,6 +6,8 @@
 // cannot certify takes the streaming normaliser there instead.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "llz_exact.h"
 #include "llz_fast.h"
 #include "llz_internal.h"
@@ -115,7 +117,8 @@ __device__ __forceinline__ float4 exact_terms4(float4 v, float m, float T, bool 
 
 // The exact terms of EXACT slot `slot` (loaded and waited for) into its dump
 // area, and its candidates (once per segment).
-__device__ __forceinline__ void slot_terms(FastShared& F, const RowPtrs& Q, const RowParams& P, const RowSrc& X,
+template <class Src>
+__device__ __forceinline__ void slot_terms(FastShared& F, const RowPtrs& Q, const RowParams& P, const Src& X,
                                            int row, int slot, int n, float m, float theta, bool t1) {
   const int lane = lane_id();
   const int seg = F.slotseg[slot];
@@ -188,7 +191,8 @@ __device__ __forceinline__ void slot_tables(FastShared& F, int slot) {
 
 // Rounds after the first: the terms and tables of this wave's slots (slot s
 // on wave s % W, all loaded by this wave and waited for).
-__device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, const RowSrc& X,
+template <class Src>
+__device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, const Src& X,
                                                int row, int w, int nslot, int n, float m, float theta, bool t1) {
   for (int slot = w; slot < nslot; slot += W) {
     slot_terms(F, Q, P, X, row, slot, n, m, theta, t1);
@@ -488,7 +492,9 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
 // read through post-processing and/or the fused repetition penalty
 // (llz_xform.h); otherwise as they are.
 template <bool FASTLD, bool XF>
-__global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
+__global__ __launch_bounds__(NT) void k_stats(KArgs A) {
+  const RowParams P = A.P;
+  const RowPtrs Q = A.Q;
   __shared__ union {
     FastShared fast;      // phases L .. C
     SampleShared select;  // then the selection stage
@@ -502,8 +508,16 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   const bool t1 = (P.flags & kFlagTIsOne) != 0;
   const float* xr = Q.src + (int64_t)row * P.src_stride;
   // reads of the row through the caller's post-processing and the penalty
-  // (the identity when !XF)
-  const RowSrc X{xr, XF ? P.xf_src : 0u, P.cap, P.inv_scale, P.rpen, &pen_sh};
+  // (plain reads when !XF)
+  using Src = typename std::conditional<XF, RowSrc, PlainSrc>::type;
+  Src X, O;  // the chain's input; sampleArgmax's input (sampler.zig:89)
+  if constexpr (XF) {
+    X = row_src(P, Q, row, &pen_sh);
+    O = row_orig(P, Q, row);
+  } else {
+    X = PlainSrc{xr};
+    O = PlainSrc{Q.orig + (int64_t)row * P.orig_stride};
+  }
   uint64_t pen_wm = 0;  // segments of this wave holding a penalised position
   if constexpr (XF) {
     if (P.xf_src & kXfPen) {
@@ -808,11 +822,11 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
     auto settle = [&](int cnt) { settle_specials(F, Q, P, row, w, cnt, v4q, Rw, cw, m, theta, t1); };
     // The queue is filled in chunks of at most qcap <= QCAP entries, each holding
     // whole batches (a segment's lanes are settled together): chunk 0 in LDS,
-    // chunks 1.. in this row's part of fallback buffer 0, SPW * 64 entries per
-    // wave (a wave queues each of its lanes at most once per segment).  All
-    // are settled in phase F+X: phase S never settles.  qch: current chunk,
+    // chunks 1.. in this row's overflow area of the workspace, kQovfWave
+    // entries per wave.  All are settled in phase F+X: phase S never
+    // settles.  qch: current chunk,
     // qn: its entries, lane c of ccnt: the entries of an earlier chunk c.
-    uint32_t* const ovp = Q.fb + (int64_t)row * n + (int64_t)w * SPW * kWave;
+    uint32_t* const ovp = Q.qovf + (int64_t)row * kQovfRow + (int64_t)w * kQovfWave;
     const int qcap = (P.qcap > 0u && P.qcap < (uint32_t)QCAP) ? (int)P.qcap : QCAP;  // entries per chunk
     int qch = 0;
     uint32_t ccnt = 0;
@@ -895,8 +909,8 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
               ++qch;
               qn = 0;
               // chunk qch occupies entries [(qch - 1) qcap, qch qcap) of the wave's
-              // SPW * 64 (always enough: a wave has at most SPW / 4 + 2 batches)
-              if (qch * qcap > SPW * kWave || qch >= kWave) qovf = true;
+              // kQovfWave; a wave that needs more fails the row (streaming normaliser)
+              if (qch * qcap > kQovfWave || qch >= kWave) qovf = true;
             }
             uint32_t* const op = ovp + (qch - 1) * qcap;
 #pragma unroll
@@ -1213,7 +1227,7 @@ __global__ __launch_bounds__(NT) void k_stats(RowParams P, RowPtrs Q) {
   // walk's results, lie past F.u): no barrier here
   static_assert(sizeof(SampleShared) <= sizeof(F.u), "the selection's memory must lie inside F.u");
   select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified, u_row, certified && pre_ok,
-             cand_pre, cand_n0, X, XF ? &pen_sh : nullptr);
+             cand_pre, cand_n0, X, O, XF ? &pen_sh : nullptr, kernel_args_ptr());
 }
 
 }  // namespace
@@ -1225,13 +1239,13 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
   const bool fastld = (P.flags & kFlagVecSrc) != 0 && (P.n % 4) == 0;
   const bool xf = P.xf_src != 0u || P.xf_orig != 0u;
   if (fastld && !xf)
-    hipLaunchKernelGGL((k_stats<true, false>), dim3(P.rows), dim3(NT), 0, st, P, Q);
+    hipLaunchKernelGGL((k_stats<true, false>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
   else if (fastld)
-    hipLaunchKernelGGL((k_stats<true, true>), dim3(P.rows), dim3(NT), 0, st, P, Q);
+    hipLaunchKernelGGL((k_stats<true, true>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
   else if (!xf)
-    hipLaunchKernelGGL((k_stats<false, false>), dim3(P.rows), dim3(NT), 0, st, P, Q);
+    hipLaunchKernelGGL((k_stats<false, false>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
   else
-    hipLaunchKernelGGL((k_stats<false, true>), dim3(P.rows), dim3(NT), 0, st, P, Q);
+    hipLaunchKernelGGL((k_stats<false, true>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (ev_end && hipEventRecord(ev_end, st) != hipSuccess) return hipErrorUnknown;

@@ -146,6 +146,28 @@ struct RowSrc {
   }
 };
 
+// A row read as it is (no post-processing, no fused penalty): the same
+// interface as RowSrc with no transform code, so kernels that do not
+// transform compile as if they read the pointer directly.
+struct PlainSrc {
+  const float* x;
+  __device__ __forceinline__ float pre(float v) const { return v; }
+  __device__ __forceinline__ float fix(int, float v) const { return v; }
+  __device__ __forceinline__ float at(int i) const { return x[i]; }
+  __device__ __forceinline__ float4 pre4(int, float4 v, int) const { return v; }
+  __device__ __forceinline__ float4 pen4(int, float4 v, int) const { return v; }
+  __device__ __forceinline__ float4 fix4(int, float4 v, int) const { return v; }
+  __device__ __forceinline__ void load4(int pos, int n, bool vec, float (&v)[kLaneV]) const {
+    if (vec && pos + kLaneV <= n) {
+      const float4 q = *reinterpret_cast<const float4*>(x + pos);
+      v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+#pragma unroll
+      for (int k = 0; k < kLaneV; ++k) v[k] = pos + k < n ? x[pos + k] : 0.0f;
+    }
+  }
+};
+
 // The chain's view of row `row` (src: the caller's rows, or the penalised
 // copy) and sampleArgmax's view (the caller's rows, post-processing only).
 __device__ __forceinline__ RowSrc row_src(const RowParams& P, const RowPtrs& Q, int row, const PenShared* pen) {
