@@ -40,7 +40,9 @@ enum {
     LLZ_E_WORKSPACE = -2,     /* workspace missing or smaller than required          */
     LLZ_E_HIP = -3,           /* a HIP runtime call failed                           */
     LLZ_E_OOM = -4,           /* host-side object could not allocate                 */
-    LLZ_E_NO_DEVICE = -5      /* no usable HIP device                                */
+    LLZ_E_NO_DEVICE = -5,     /* no usable HIP device                                */
+    LLZ_E_SCRATCH = -6        /* llz_sample_rows_noalloc: the call needs more than   */
+                              /* its static scratch (LLZ_NOALLOC_SCRATCH_BYTES)      */
 };
 
 /* Mirror of SamplerConfig (sampler.zig:4-13).  Field meanings and defaults
@@ -127,6 +129,24 @@ int llz_sample_rows(const float *d_logits, int64_t row_stride, int32_t rows, int
                     int64_t prev_stride, const float *d_uniforms, uint32_t *d_tokens,
                     uint8_t *d_consumed, const llz_sample_extras *extras, void *d_workspace,
                     size_t workspace_bytes, void *stream);
+
+/* llz_sample_rows without a workspace: the variant for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * The kernels' scratch is a static device array of LLZ_NOALLOC_SCRATCH_BYTES
+ * inside the library, one per GPU it runs on, held until the process ends;
+ * the call allocates and frees nothing.  A call whose layout does not fit it
+ * (llz_sample_workspace_bytes' layout with at most 8 rows' full-row fallback
+ * buffers at a time, and no penalised copy beyond the scratch) returns
+ * LLZ_E_SCRATCH before any work.  Every call on a GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (other streams, other threads) race
+ * and must not be issued.  Outputs and semantics are llz_sample_rows'. */
+#define LLZ_NOALLOC_SCRATCH_BYTES (96u << 20)
+int llz_sample_rows_noalloc(const float *d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                            const llz_sampler_config *cfg, const llz_logit_post *post,
+                            const uint32_t *d_prev_tokens, int32_t n_prev, int64_t prev_stride,
+                            const float *d_uniforms, uint32_t *d_tokens, uint8_t *d_consumed,
+                            const llz_sample_extras *extras, void *stream);
 
 /* sampleArgmax (sampler.zig:31-41) per row of the post-processed logits
  * (`post` as for llz_sample_rows; may be NULL): the first index of the

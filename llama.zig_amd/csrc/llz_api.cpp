@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 
 #include "../../include/llz_sampler.h"
@@ -57,10 +58,11 @@ struct Layout {
   bool has_penal;
 };
 
-Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int32_t n_prev) {
+Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int32_t n_prev,
+                 int max_slots = kFbSlots) {
   Layout L{};
   const size_t r = (size_t)rows, n = (size_t)vocab;
-  L.fb_slots = rows < kFbSlots ? rows : kFbSlots;
+  L.fb_slots = rows < max_slots ? rows : max_slots;
   const size_t ns = (size_t)L.fb_slots;
   size_t off = 0;
   L.status = off;  off = align_up(off + r * sizeof(uint32_t));
@@ -126,6 +128,7 @@ const char* llz_strerror(int code) {
     case LLZ_E_HIP: return "HIP runtime error";
     case LLZ_E_OOM: return "out of memory";
     case LLZ_E_NO_DEVICE: return "no HIP device";
+    case LLZ_E_SCRATCH: return "input too large for the static scratch of llz_sample_rows_noalloc";
     default: return "unknown error";
   }
 }
@@ -149,12 +152,17 @@ int llz_argmax_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }
 
-int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
-                    const llz_sampler_config* cfg, const llz_logit_post* post,
-                    const uint32_t* d_prev_tokens, int32_t n_prev,
-                    int64_t prev_stride, const float* d_uniforms, uint32_t* d_tokens,
-                    uint8_t* d_consumed, const llz_sample_extras* extras, void* d_workspace,
-                    size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// llz_sample_rows on a given workspace holding at most max_slots full-row
+// fallback buffer sets (llz_sample_rows: the caller's, kFbSlots;
+// llz_sample_rows_noalloc: the library's static scratch, kScratchSlots).
+static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                            const llz_sampler_config* cfg, const llz_logit_post* post,
+                            const uint32_t* d_prev_tokens, int32_t n_prev, int64_t prev_stride,
+                            const float* d_uniforms, uint32_t* d_tokens, uint8_t* d_consumed,
+                            const llz_sample_extras* extras, void* d_workspace, size_t workspace_bytes,
+                            int max_slots, int too_small_code, void* stream) {
   int rc = check_common(d_logits, row_stride, rows, vocab);
   if (rc) return rc;
   if (!cfg || !d_tokens || n_prev < 0 || prev_stride < 0) return LLZ_E_INVALID_ARG;
@@ -178,8 +186,8 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   if (penalty_active(cfg, n_prev) && cfg->repetition_penalty != cfg->repetition_penalty)
     return LLZ_E_INVALID_ARG;
 
-  const Layout L = layout_of(rows, vocab, cfg, n_prev);
-  if (!d_workspace || workspace_bytes < L.total) return LLZ_E_WORKSPACE;
+  const Layout L = layout_of(rows, vocab, cfg, n_prev, max_slots);
+  if (!d_workspace || workspace_bytes < L.total) return too_small_code;
   char* ws = (char*)d_workspace;
 
   const float* src = d_logits;
@@ -253,6 +261,82 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   Q.prev_win = (xf_src & kXfPen) ? d_prev_tokens + (n_prev - window) : nullptr;
   e = launch_sample(P, Q, g_ev_begin, g_ev_end, st);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
+}
+
+// ---------------------------------------------------------------------------
+// llz_sample_rows_noalloc: the same call on the library's static scratch.
+// `scratch` is a host-side stand-in for the device array: host code uses the
+// per-device address hipGetSymbolAddress returns for it, never the name.
+// Nothing in it needs clearing between calls: the status words, candidate
+// lists and queue overflow are written before they are read within a call,
+// and a fallback slot is free for a call whenever its owner word holds
+// anything but that call's epoch.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)LLZ_NOALLOC_SCRATCH_BYTES;
+constexpr int kScratchSlots = 8;  // full-row fallback buffer sets in the scratch
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // per device: the address of its copy of `scratch`
+
+// The scratch of device `dev`, looked up once per device with that device
+// current (each GPU holds its own copy of the array at its own address).
+int scratch_of(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxDevices) return LLZ_E_NO_DEVICE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return LLZ_E_HIP;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return LLZ_E_HIP;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return LLZ_E_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return LLZ_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int llz_sample_rows_noalloc(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                            const llz_sampler_config* cfg, const llz_logit_post* post,
+                            const uint32_t* d_prev_tokens, int32_t n_prev, int64_t prev_stride,
+                            const float* d_uniforms, uint32_t* d_tokens, uint8_t* d_consumed,
+                            const llz_sample_extras* extras, void* stream) {
+  int rc = check_common(d_logits, row_stride, rows, vocab);
+  if (rc) return rc;
+  // the device the call's stream runs on
+  int dev = 0;
+  if (stream) {
+    if (hipStreamGetDevice((hipStream_t)stream, &dev) != hipSuccess) return LLZ_E_HIP;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return LLZ_E_HIP;
+  }
+  void* ws = nullptr;
+  rc = scratch_of(dev, &ws);
+  if (rc) return rc;
+  return sample_rows_impl(d_logits, row_stride, rows, vocab, cfg, post, d_prev_tokens, n_prev, prev_stride,
+                          d_uniforms, d_tokens, d_consumed, extras, ws, kScratchBytes, kScratchSlots,
+                          LLZ_E_SCRATCH, stream);
+}
+
+int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                    const llz_sampler_config* cfg, const llz_logit_post* post,
+                    const uint32_t* d_prev_tokens, int32_t n_prev,
+                    int64_t prev_stride, const float* d_uniforms, uint32_t* d_tokens,
+                    uint8_t* d_consumed, const llz_sample_extras* extras, void* d_workspace,
+                    size_t workspace_bytes, void* stream) {
+  return sample_rows_impl(d_logits, row_stride, rows, vocab, cfg, post, d_prev_tokens, n_prev, prev_stride,
+                          d_uniforms, d_tokens, d_consumed, extras, d_workspace, workspace_bytes, kFbSlots,
+                          LLZ_E_WORKSPACE, stream);
 }
 
 int llz_debug_kernel_events(void* begin_event, void* end_event) {

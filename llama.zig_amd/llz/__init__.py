@@ -31,10 +31,11 @@ LLZ_E_WORKSPACE = -2
 LLZ_E_HIP = -3
 LLZ_E_OOM = -4
 LLZ_E_NO_DEVICE = -5
+LLZ_E_SCRATCH = -6
 
 # Public symbols of include/llz_sampler.h.
 EXPORTED = (
-    "llz_sampler_config_default", "llz_sample_workspace_bytes", "llz_sample_rows",
+    "llz_sampler_config_default", "llz_sample_workspace_bytes", "llz_sample_rows", "llz_sample_rows_noalloc",
     "llz_argmax_rows", "llz_rng_seed", "llz_rng_next", "llz_rng_float", "llz_rng_uniforms",
     "llz_sampler_create", "llz_sampler_destroy", "llz_sampler_sample", "llz_sampler_sample_uniform",
     "llz_sampler_get_state",
@@ -127,6 +128,9 @@ def _lib():
         L.llz_sample_rows.argtypes = [vp, i64, i32, i32, C.POINTER(CConfig), C.POINTER(CPost), vp, i32, i64,
                                       vp, vp, vp, C.POINTER(CExtras), vp, C.c_size_t, vp]
         L.llz_sample_rows.restype = C.c_int
+        L.llz_sample_rows_noalloc.argtypes = [vp, i64, i32, i32, C.POINTER(CConfig), C.POINTER(CPost), vp, i32,
+                                              i64, vp, vp, vp, C.POINTER(CExtras), vp]
+        L.llz_sample_rows_noalloc.restype = C.c_int
         L.llz_argmax_rows.argtypes = [vp, i64, i32, i32, C.POINTER(CPost), vp, vp]
         L.llz_argmax_rows.restype = C.c_int
         L.llz_rng_seed.argtypes = [C.POINTER(u64), u64]
