@@ -180,83 +180,184 @@ __device__ void lds_bitonic_sort_u64(uint64_t* a, int n) {
 }
 
 // Stable LSD radix sort (8-bit digits, ascending keys) of n pairs held in
-// global memory.  (k0, v0) is the input and, after the four passes, the
-// output; (k1, v1) is the ping-pong buffer.  Equal keys keep input order.
+// global memory, by one workgroup.  (k0, v0) is the input and the output;
+// (k1, v1) is the ping-pong buffer.  Equal keys keep input order.
+//
+// One read of the keys counts the digits of all four passes; a pass whose
+// digit is the same for every key moves nothing and is skipped (it would
+// keep the order).  A pass handles tiles of kRadixRounds * NT elements:
+// round r of a tile holds elements tile + r NT + t, so (round, wave, lane)
+// order is input order.  Each round ranks its elements within their wave
+// (lanes with the same digit found by eight ballots), the counts of every
+// (round, wave) go to LDS, and one scan per digit turns them into the
+// elements' places in the tile ordered by digit.  The tile is staged in LDS
+// in that order and written out in it: each digit's elements of the tile go
+// to consecutive global addresses, so the writes are runs, not scattered
+// words.
+constexpr int kRadixRounds = 8;
+
 struct RadixScratch {
-  uint32_t base[256];
-  uint32_t cnt[16][256];  // per-wave digit counts of one tile
+  uint32_t hist[4][256];                  // digit counts of the whole input, per pass
+  uint32_t base[256];                     // next output offset per digit
+  int32_t delta[256];                     // tile: output offset minus tile place, per digit
+  uint32_t wsum[4];                       // tile: digit-total scan, per wave of the scan
+  uint16_t cnt[kRadixRounds][8][256];     // per (round, wave): digit counts, then tile places (< 2^16)
+  uint32_t stage_k[kRadixRounds * 512];   // the tile ordered by digit
+  uint32_t stage_v[kRadixRounds * 512];
 };
 
 template <int NT>
 __device__ void wg_radix_sort_pairs(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, int n,
                                     RadixScratch& rs) {
-  static_assert(NT % kWave == 0 && NT / kWave <= 16 && NT >= 256, "radix sort layout");
+  static_assert(NT % kWave == 0 && NT / kWave <= 8 && NT >= 256 && NT <= 512, "radix sort layout");
+  static_assert(kRadixRounds * 512 <= 65536, "tile places fit 16 bits");
   constexpr int W = NT / kWave;
+  constexpr int R = kRadixRounds;
+  constexpr int TILE = R * NT;
   const int t = (int)threadIdx.x;
   const int w = wave_id();
-  const uint64_t lt_mask = (lane_id() == 0) ? 0ull : (~0ull >> (kWave - lane_id()));
+  const int lane = lane_id();
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+  if (n <= 1) return;
+
+  // digit counts of all four passes
+  for (int d = t; d < 4 * 256; d += NT) (&rs.hist[0][0])[d] = 0;
+  __syncthreads();
+  for (int i = t; i < n; i += NT) {
+    const uint32_t key = k0[i];
+    atomicAdd(&rs.hist[0][key & 255u], 1u);
+    atomicAdd(&rs.hist[1][(key >> 8) & 255u], 1u);
+    atomicAdd(&rs.hist[2][(key >> 16) & 255u], 1u);
+    atomicAdd(&rs.hist[3][key >> 24], 1u);
+  }
+  __syncthreads();
+
   uint32_t *src_k = k0, *src_v = v0, *dst_k = k1, *dst_v = v1;
-  for (int shift = 0; shift < 32; shift += 8) {
-    // 1. histogram
-    for (int d = t; d < 256; d += NT) rs.base[d] = 0;
-    __syncthreads();
-    for (int i = t; i < n; i += NT) atomicAdd(&rs.base[(src_k[i] >> shift) & 255u], 1u);
-    __syncthreads();
-    // 2. exclusive scan of the 256 counts (one wave, 4 per lane)
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 8 * pass;
+    // a digit shared by every key: nothing moves
+    bool constant = false;
+    for (int d = 0; d < 256; ++d) constant = constant || rs.hist[pass][d] == (uint32_t)n;
+    if (constant) continue;
+    // exclusive scan of the pass's counts (one wave, four digits per lane)
     if (w == 0) {
-      uint32_t c[4], s = 0;
+      uint32_t c[4], sum = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) { c[q] = rs.base[lane_id() * 4 + q]; s += c[q]; }
-      uint32_t incl = s;
+      for (int q = 0; q < 4; ++q) { c[q] = rs.hist[pass][lane * 4 + q]; sum += c[q]; }
+      uint32_t incl = sum;
 #pragma unroll
       for (int d = 1; d < kWave; d <<= 1) {
-        uint32_t o = __shfl_up(incl, d, kWave);
-        if (lane_id() >= d) incl += o;
+        const uint32_t o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
       }
-      uint32_t run = incl - s;
+      uint32_t run = incl - sum;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) { rs.base[lane_id() * 4 + q] = run; run += c[q]; }
+      for (int q = 0; q < 4; ++q) { rs.base[lane * 4 + q] = run; run += c[q]; }
     }
-    __syncthreads();
-    // 3. stable scatter, one element per thread per tile, tiles in order
-    for (int tile = 0; tile < n; tile += NT) {
-      for (int d = t; d < 256 * W; d += NT) (&rs.cnt[0][0])[d] = 0;
-      __syncthreads();
-      const int i = tile + t;
-      const bool valid = i < n;
-      uint32_t key = 0, val = 0, dig = 0;
-      if (valid) {
-        key = src_k[i];
-        val = src_v[i];
-        dig = (key >> shift) & 255u;
-      }
-      // lanes of this wave with the same digit
-      uint64_t peers = __ballot(valid);
+    // the tile's elements, loaded one tile ahead (the barriers inside the
+    // loop order LDS only, so these loads and the previous tile's writes
+    // stay in flight across them)
+    uint32_t nk[R], nv[R];
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const uint64_t bb = __ballot(valid && ((dig >> b) & 1u));
-        peers &= ((dig >> b) & 1u) ? bb : ~bb;
+    for (int r = 0; r < R; ++r) {
+      const int i = r * NT + t;
+      nk[r] = i < n ? src_k[i] : 0u;
+      nv[r] = i < n ? src_v[i] : 0u;
+    }
+    for (int tile = 0; tile < n; tile += TILE) {
+      const int tn = min(TILE, n - tile);
+      uint32_t key[R], val[R], dig[R], rank[R];
+      bool valid[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        valid[r] = tile + r * NT + t < n;
+        key[r] = nk[r];
+        val[r] = nv[r];
       }
-      const uint32_t rank_in_wave = (uint32_t)__popcll(peers & lt_mask);
-      if (valid && rank_in_wave == 0) rs.cnt[w][dig] = (uint32_t)__popcll(peers);
-      __syncthreads();
-      if (valid) {
-        uint32_t off = rs.base[dig] + rank_in_wave;
-        for (int ww = 0; ww < w; ++ww) off += rs.cnt[ww][dig];
-        dst_k[off] = key;
-        dst_v[off] = val;
+      if (tile + TILE < n) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int i = tile + TILE + r * NT + t;
+          nk[r] = i < n ? src_k[i] : 0u;
+          nv[r] = i < n ? src_v[i] : 0u;
+        }
       }
-      __syncthreads();
-      for (int d = t; d < 256; d += NT) {
-        uint32_t s = 0;
-        for (int ww = 0; ww < W; ++ww) s += rs.cnt[ww][d];
-        rs.base[d] += s;
+      // zero the tile's counts (the previous tile's last reads are done)
+      uint4* cz = reinterpret_cast<uint4*>(&rs.cnt[0][0][0]);
+      for (int d = t; d < R * 8 * 256 / 8; d += NT) cz[d] = make_uint4(0u, 0u, 0u, 0u);
+      lds_barrier();
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        dig[r] = (key[r] >> shift) & 255u;
+        // lanes of this wave with the same digit
+        uint64_t peers = bal64(valid[r]);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const uint64_t bb = bal64(((dig[r] >> b) & 1u) != 0u);
+          peers &= ((dig[r] >> b) & 1u) ? bb : ~bb;
+        }
+        rank[r] = (uint32_t)__popcll(peers & lt_mask);
+        if (valid[r] && rank[r] == 0) rs.cnt[r][w][dig[r]] = (uint16_t)__popcll(peers);
       }
-      __syncthreads();
+      lds_barrier();
+      // per digit (thread d < 256, waves 0 .. 3): its tile total, the tile
+      // place where its elements start (a scan over digits), then each
+      // (round, wave)'s place
+      uint32_t tot = 0, incl = 0;
+      if (t < 256) {
+#pragma unroll 8
+        for (int rw = 0; rw < R * W; ++rw) tot += rs.cnt[rw / W][rw % W][t];
+        incl = wave_incl_scan_op(tot, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+        if (lane == kWave - 1) rs.wsum[w] = incl;
+      }
+      lds_barrier();
+      if (t < 256) {
+        const int d = t;
+        uint32_t start = incl - tot;
+        for (int ww = 0; ww < w; ++ww) start += rs.wsum[ww];
+        uint32_t run = start;
+#pragma unroll 8
+        for (int rw = 0; rw < R * W; ++rw) {
+          uint16_t* c = &rs.cnt[rw / W][rw % W][d];
+          const uint32_t v = *c;
+          *c = (uint16_t)run;
+          run += v;
+        }
+        rs.delta[d] = (int32_t)rs.base[d] - (int32_t)start;
+        rs.base[d] += tot;
+      }
+      lds_barrier();
+      // stage the tile in digit order
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (valid[r]) {
+          const uint32_t place = rs.cnt[r][w][dig[r]] + rank[r];
+          rs.stage_k[place] = key[r];
+          rs.stage_v[place] = val[r];
+        }
+      }
+      lds_barrier();
+      // write it out in that order: runs of consecutive addresses per digit
+      for (int i = t; i < tn; i += NT) {
+        const uint32_t k = rs.stage_k[i];
+        const int32_t off = rs.delta[(k >> shift) & 255u] + i;
+        dst_k[off] = k;
+        dst_v[off] = rs.stage_v[i];
+      }
+      lds_barrier();
     }
     uint32_t* tk = src_k; src_k = dst_k; dst_k = tk;
     uint32_t* tv = src_v; src_v = dst_v; dst_v = tv;
     // make this pass's global writes visible to the next pass's reads
+    __threadfence_block();
+    __syncthreads();
+  }
+  // an odd number of passes left the result in (k1, v1): copy it back
+  if (src_k != k0) {
+    for (int i = t; i < n; i += NT) {
+      k0[i] = src_k[i];
+      v0[i] = src_v[i];
+    }
     __threadfence_block();
     __syncthreads();
   }
