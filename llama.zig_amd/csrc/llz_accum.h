@@ -112,14 +112,24 @@ __device__ float tile_accumulate(float s, const float (&x)[V], int L, float thr,
 }
 
 // Additive tile accumulation with implicit terms: R(k, j, tie) returns
-// RN(term_k / 2^(j-23)) (saturated at kSat) and sets tie; E(k) returns the
-// exact term, and is called only for the element at which an event is
-// resolved; present(k) is false for positions outside the sequence.  Lets a
-// caller supply roundings from a cheaper, exact-when-unambiguous estimate.
+// RN(term_k / 2^(j-23)) (saturated at kSat) and sets tie (a caller may also
+// set tie to make an element an event when it cannot round it cheaply); E(k)
+// returns the exact term, and is called only for an element at which an event
+// is resolved; present(k) is false for positions outside the sequence.  Tile
+// positions up to `done` are taken as already summed into s.  Lets a caller
+// supply roundings from a cheaper, exact-when-unambiguous estimate.
+//
+// An event takes two barriers: the per-wave inclusive sums (with the tie
+// flags) give every thread its exact prefix; each wave then resolves its own
+// first event as if no earlier wave had one, and the first wave that has one
+// holds the event (earlier waves' positions come first).
 template <int NT, int V, typename RFn, typename EFn, typename PFn>
-__device__ float tile_accumulate_fn(float s, RFn R, EFn E, PFn present, WgScratch<NT>& sh, int& bank) {
+__device__ float tile_accumulate_fn(float s, RFn R, EFn E, PFn present, WgScratch<NT>& sh, int& bank,
+                                    int done = -1) {
+  constexpr int W = WgScratch<NT>::W;
   const int t = (int)threadIdx.x;
-  int done = -1;
+  const int w = wave_id();
+  const int lane = lane_id();
   for (;;) {
     const Grid g = grid_of(s);
     uint32_t r[V];
@@ -135,48 +145,67 @@ __device__ float tile_accumulate_fn(float s, RFn R, EFn E, PFn present, WgScratc
       tsum = sat_add(tsum, r[k], kSat);
       ttie = ttie || tie[k];
     }
-    {
-      const uint32_t ws = wave_sum_sat(tsum, kSat);
-      const bool wt = bal64(ttie) != 0ull;
-      if (lane_id() == 0) sh.red[bank][wave_id()] = ws | (wt ? 0x80000000u : 0u);
-      lds_barrier();
-    }
-    uint32_t total = 0;
+    const uint32_t incl = wave_incl_scan_sat(tsum, kSat);
+    const bool wt = bal64(ttie) != 0ull;
+    if (lane == kWave - 1) sh.red[bank][w] = incl | (wt ? 0x80000000u : 0u);
+    lds_barrier();
+    uint32_t total = 0, before = 0;
     bool anytie = false;
 #pragma unroll
-    for (int w = 0; w < WgScratch<NT>::W; ++w) {
-      const uint32_t v = sh.red[bank][w];
+    for (int i = 0; i < W; ++i) {
+      const uint32_t v = sh.red[bank][i];
       total = sat_add(total, v & 0x7fffffffu, kSat);
+      if (i < w) before = sat_add(before, v & 0x7fffffffu, kSat);
       anytie = anytie || (v >> 31);
     }
-    bank ^= 1;
-    if (!anytie && g.N + total < kGridTop) return grid_value(g.N + total, g.j);
+    if (!anytie && g.N + total < kGridTop) {
+      bank ^= 1;
+      return grid_value(g.N + total, g.j);
+    }
 
-    const uint32_t excl = wg_excl_scan_sat<NT>(tsum, kSat, sh, bank);
-    uint32_t run = g.N + excl;
-    uint32_t my_evt = 0xffffffffu;
+    // this wave's first event, with the exact prefix before it
+    uint32_t run = g.N + sat_add(before, wave_shift_up1(incl), kSat);
+    int my_k = -1;
     uint32_t my_before = 0;
-    int my_k = 0;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       const int p = t * V + k;
-      if (p > done && present(k) && my_evt == 0xffffffffu) {
-        const uint32_t before = run;
+      if (p > done && present(k) && my_k < 0) {
+        const uint32_t b = run;
         run += r[k];
         if (tie[k] || run >= kGridTop) {
-          my_evt = (uint32_t)p;
-          my_before = before;
           my_k = k;
+          my_before = b;
         }
       }
     }
-    const uint32_t P = wg_min_u32<NT>(my_evt, sh, bank);
-    if (P == 0xffffffffu) return grid_value(g.N + total, g.j);
-    const bool owner = my_evt == P;
-    float s_post = 0.0f;
-    uint32_t unused = 0;
-    if (owner) s_post = grid_value(my_before, g.j) + E(my_k);
-    wg_bcast<NT>(owner, s_post, unused, sh, bank);
+    const uint64_t em = bal64(my_k >= 0);
+    const int owner = em != 0ull ? __ffsll((long long)em) - 1 : -1;
+    if (lane == owner) {
+      // E with a constant index (a caller's per-element arrays stay in registers)
+      float x = 0.0f;
+#pragma unroll
+      for (int k = 0; k < V; ++k)
+        if (k == my_k) x = E(k);
+      sh.red[bank ^ 1][w] = (uint32_t)(t * V + my_k);
+      sh.sw[w] = grid_value(my_before, g.j) + x;
+    } else if (owner < 0 && lane == 0) {
+      sh.red[bank ^ 1][w] = 0xffffffffu;
+    }
+    lds_barrier();
+    uint32_t P = 0xffffffffu;
+    float s_post = s;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      const uint32_t q = sh.red[bank ^ 1][i];
+      if (P == 0xffffffffu && q != 0xffffffffu) {
+        P = q;
+        s_post = sh.sw[i];
+      }
+    }
+    // both banks were used: the next writer of red[bank] follows the second
+    // barrier, after every read of it
+    if (P == 0xffffffffu) return grid_value(g.N + total, g.j);  // unreachable
     s = s_post;
     done = (int)P;
     if (done >= NT * V - 1) return s;

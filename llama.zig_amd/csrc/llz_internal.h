@@ -10,7 +10,10 @@ constexpr int kCandCap = 2048;  // candidate list capacity per row (power of two
 constexpr int kPenMax = 64;     // fused repetition penalty: window entries at most (one per lane)
 constexpr int kQovfWave = 512;  // k_stats special-queue overflow entries per wave (four chunks)
 constexpr int kQovfRow = 8 * kQovfWave;  // ... per row (eight waves)
-constexpr int kFbSlots = 64;    // full-row fallback buffers per call at most (rows beyond wait for one)
+// Full-row fallback buffer sets per call at most (rows beyond wait for one):
+// the number of CUs, since k_stats's LDS holds one row-workgroup per CU, so
+// no more rows than this can be inside the fallback at once.
+constexpr int kFbSlots = 256;
 
 // RowParams.flags
 constexpr uint32_t kFlagTIsOne = 1u;    // temperature == 1.0f exactly: (v - m) / T == v - m

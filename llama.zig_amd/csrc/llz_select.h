@@ -469,27 +469,169 @@ __device__ int prefix_filters(const List& L, int M, float p_nc, int n, const Row
   return K > M ? -1 : K;
 }
 
-// Entropy sum over the whole row in index order (sampler.zig:129-132).
+// Entropy sum over the whole row in index order (sampler.zig:129-132):
+// entropy -= p * log(p) for every p = RN(e / S) > 0, which is the exact
+// sequential sum of the terms t = -RN(p * log(p)) >= 0 (a - b == a + (-b)).
+// Wave 0 sums the first 512 terms alone (wave_accumulate: the many binade
+// crossings of a sum that starts at 0 cost no barriers there); the rest goes
+// through tile_accumulate_fn, which needs of each term its rounding RN(t / u)
+// on the running sum's grid u = 2^(j-23), taken from an estimate wherever the
+// estimate's error bound fixes it.
+//
+// Estimate, for 2^-110 <= p~ <= 2^-2, from the reference's own argument x =
+// RN(RN(v - m) / T):
+//   x log2(e) = a_hi + a_lo (a_hi = RN(x L2E), a_lo = fma(x, L2E, -a_hi) +
+//   x L2E_lo, L2E + L2E_lo = log2(e) to 2^-49);  e~ = fma(e0, a_lo ln2, e0),
+//   e0 = exp2(a_hi);  p~ = RN(e~ RN(1 / S));  l~ = RN(log2(p~) RN(ln 2));
+//   t~ = -RN(p~ l~).
+// Relative errors against the reference's e = expf(x) (< 1 ulp), p = RN(e /
+// S), l = logf(p) (< 1 ulp), t: the hardware exp2 and log2 are taken to be
+// within 1 ulp of their results; e~ / exp(x) - 1 <= 1.5 * 2^-23 (exp2, the
+// fma, and terms below 2^-33); p~ / p - 1 <= dp = 4 * 2^-23; with |log p| >=
+// ln 4, l~ / l - 1 <= dp / ln 4 + 3 * 2^-23; so t~ / t - 1 <= 10.9 * 2^-23 to
+// first order, and eps = 24 * 2^-23 is more than twice that.  y~ = t~
+// 2^(23-j) is exact; when [y~(1 - eps), y~(1 + eps)] lies strictly between k
+// - 1/2 and k + 1/2 (y~ < 2^22), RN(t / u) = k and t / u is no tie; when y~(1
+// - eps) >= 2^24 the term leaves the binade by itself (kSat, as grid_round).
+// Below: p~ < 2^-110 (or x < -88) means p < 2^-108, so t < 2^-108 * 88 <
+// 2^-101.5 rounds to 0 on every grid j >= -60.  NaN estimates, p~ > 2^-2,
+// finer grids and uncertain roundings take the exact term, evaluated once per
+// element with the reference's operations.
+// Out of line, so that the kernel's common path does not carry its
+// registers; the row's parameters come by value (a reference would make the
+// kernel store them to its stack).
+struct EntropyResult {
+  float H;
+  int bank;
+};
+
 template <class Src>
-__device__ float entropy_pass(const Src& X, int n, float m, float S, const RowParams& P,
-                              SampleShared& sh, int& bank) {
-  const bool t1 = (P.flags & kFlagTIsOne) != 0;
-  const bool vec = (P.flags & kFlagVecSrc) != 0;
-  float H = 0.0f;
+__device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float S, float T, uint32_t flags,
+                                                   SampleShared& sh, int bank) {
+  constexpr int EV = 2 * kLaneV;  // logits per thread per tile
+  constexpr int ET = kNT * EV;
+  constexpr int EP = kWave * EV;  // the prologue's terms (wave 0's share of the first tile)
+  constexpr float L2E = 1.44269502e+0f;     // RN(log2(e))
+  constexpr float L2E_LO = 1.92596303e-8f;  // RN(log2(e) - L2E)
+  constexpr float LN2 = 6.93147182e-1f;     // RN(ln 2)
+  constexpr float EPS = 24.0f * 0x1p-23f;
+  const bool t1 = (flags & kFlagTIsOne) != 0;
+  const bool vec = (flags & kFlagVecSrc) != 0;
+  const float rS = 1.0f / S;
   const int t = (int)threadIdx.x;
-  for (int base = 0; base < n; base += kTile) {
-    float v[kV], term[kV];
-    X.load4(base + t * kV, n, vec, v);
+  const float* __restrict__ xs = X.x;
+
+  // Loads of a thread's EV logits from pos.  With 16-byte loads, every
+  // thread loads from min(pos, nlast) (the last start that stays inside the
+  // row), so no branch separates a tile's loads from the work they overlap;
+  // the one thread whose span crosses the row's end re-reads its logits
+  // where they are used (fix_tail).
+  const bool vec8 = vec && n >= EV;
+  const int nlast = vec8 ? ((n - EV) & ~3) : 0;
+  auto load_raw = [&](int pos, float (&r)[EV]) {
+    if (vec8) {
+      const int pc = min(pos, nlast);
+      const float4 q0 = *reinterpret_cast<const float4*>(xs + pc);
+      const float4 q1 = *reinterpret_cast<const float4*>(xs + pc + 4);
+      r[0] = q0.x; r[1] = q0.y; r[2] = q0.z; r[3] = q0.w;
+      r[4] = q1.x; r[5] = q1.y; r[6] = q1.z; r[7] = q1.w;
+    } else {
 #pragma unroll
-    for (int k = 0; k < kV; ++k) {
-      const float p = row_exp(v[k], m, P.temperature, t1) / S;
-      // entropy -= p * log(p) for p > 0; the term enters negated (exact)
-      term[k] = p > 0.0f ? -(p * log_f32(p)) : -0.0f;
+      for (int k = 0; k < EV; ++k) r[k] = pos + k < n ? xs[pos + k] : 0.0f;
     }
-    int st;
-    H = tile_accumulate<kNT, kV, false>(H, term, min(kTile, n - base), -1.0f, st, sh.wg, bank);
+  };
+  auto fix_tail = [&](int pos, float (&r)[EV]) {
+    if (vec8 && pos > nlast && pos < n) {
+#pragma unroll
+      for (int k = 0; k < EV; ++k) r[k] = pos + k < n ? xs[pos + k] : 0.0f;
+    }
+  };
+  // sampler.zig:85 and :131 on one argument x; the term is +0 when p == 0
+  auto exact_term = [&](float x) {
+    const float p = exp_f32(x) / S;
+    return p > 0.0f ? -(p * log_f32(p)) : 0.0f;
+  };
+
+  float raw[EV];
+  load_raw(t * EV, raw);
+  fix_tail(t * EV, raw);
+  float H = 0.0f;
+  {
+    uint32_t unused = 0;
+    if (wave_id() == 0) {
+      float x[EV];
+#pragma unroll
+      for (int k = 0; k < EV; ++k) {
+        const int pos = t * EV + k;
+        float a = X.fix(pos, raw[k]) - m;
+        if (!t1) a = a / T;
+        const float te = exact_term(a);
+        x[k] = pos < n && te > 0.0f ? te : -0.0f;  // absent: past the row, or p * log(p) == 0
+      }
+      H = wave_accumulate<EV>(0.0f, x);
+    }
+    wg_bcast<kNT>(t == 0, H, unused, sh.wg, bank);
   }
-  return H;
+
+  for (int base = 0; base < n; base += ET) {
+    const int pos = base + t * EV;
+    if (base > 0) fix_tail(pos, raw);
+    float xa[EV];
+#pragma unroll
+    for (int k = 0; k < EV; ++k) {
+      float a = (pos + k < n ? X.fix(pos + k, raw[k]) : 0.0f) - m;
+      if (!t1) a = a / T;
+      xa[k] = a;  // the reference's argument
+    }
+    if (base + ET < n) load_raw(pos + ET, raw);  // the next tile's loads fly during this one
+
+    float tl[EV], te[EV];
+    uint32_t mid = 0, tiny = 0, have = 0;
+#pragma unroll
+    for (int k = 0; k < EV; ++k) {
+      const float x = xa[k];
+      const float ah = x * L2E;
+      const float al = fmaf(x, L2E, -ah) + x * L2E_LO;
+      const float e0 = __builtin_amdgcn_exp2f(ah);
+      const float pt = fmaf(e0, al * LN2, e0) * rS;
+      tl[k] = -(pt * (__builtin_amdgcn_logf(pt) * LN2));
+      te[k] = 0.0f;
+      const bool tn = x < -88.0f || pt < 0x1p-110f;
+      tiny |= (tn ? 1u : 0u) << k;
+      mid |= (!tn && pt <= 0x1p-2f ? 1u : 0u) << k;
+    }
+    auto exact = [&](int k) {
+      if (!((have >> k) & 1u)) {
+        // the empty volatile asm keeps the evaluation inside this branch:
+        // the term is loop-invariant in tile_accumulate_fn, and hoisted out
+        // of the branch it would be computed for every element
+        float x = xa[k];
+        asm volatile("" : "+v"(x));
+        te[k] = exact_term(x);
+        have |= 1u << k;
+      }
+      return te[k];
+    };
+    // the certified cases are selected without branches; one branch per
+    // element leads to the exact term
+    auto R = [&](int k, int j, bool& tie) -> uint32_t {
+      tie = false;
+      const float y = ldexpf(tl[k], 23 - j);
+      const float d = y * EPS;
+      const float r = rintf(y);
+      const bool big = y - d >= 0x1p24f;
+      const bool cert = y < 0x1p22f && fabsf(y - r) + d < 0.5f;
+      const bool is_tiny = ((tiny >> k) & 1u) != 0u;
+      const bool ok = is_tiny ? j >= -60 : (((mid >> k) & 1u) != 0u && (big || cert));
+      uint32_t out = is_tiny ? 0u : (big ? kSat : (uint32_t)r);
+      if (!ok) out = grid_round(exact(k), j, tie);
+      return out;
+    };
+    auto E = [&](int k) { return exact(k); };
+    auto present = [&](int k) { return pos + k < n; };
+    H = tile_accumulate_fn<kNT, EV>(H, R, E, present, sh.wg, bank, base == 0 ? EP - 1 : -1);
+  }
+  return EntropyResult{H, bank};
 }
 
 // Total and draw over p-order positions [0, K) whose keep flag is set
@@ -829,7 +971,11 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
       lds_barrier();
     } else if (typical && K >= 2) {
       path |= kPathEntropy;
-      H = entropy_pass(X, n, m, S, P, sh, bank);
+      {
+        const EntropyResult er = entropy_pass<Src>(X, n, m, S, P.temperature, P.flags, sh, bank);
+        H = er.H;
+        bank = er.bank;
+      }
       const int ksort = next_pow2(K);
       for (int q = t; q < ksort; q += kNT) {
         if (q < K) {
@@ -979,7 +1125,11 @@ __device__ __noinline__ void select_full_row(const KArgs* A, const PenShared* pe
   if (K < 0) K = 0;
   if (typical && K >= 2) {
     path |= kPathEntropy;
-    H = entropy_pass(X, n, m, S, P, sh, bank);
+    {
+        const EntropyResult er = entropy_pass<Src>(X, n, m, S, P.temperature, P.flags, sh, bank);
+        H = er.H;
+        bank = er.bank;
+      }
     for (int i = t; i < n; i += kNT) mask[i] = 0;
     __threadfence();
     __syncthreads();

@@ -90,6 +90,7 @@ struct WgScratch {
   uint32_t red[2][W];
   float fb[2][4];
   uint32_t ub[2][4];
+  float sw[W];  // per-wave float results (tile_accumulate_fn's events)
   int bank;
 };
 

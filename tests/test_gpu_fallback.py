@@ -3,8 +3,8 @@ largest configurations at their full batch.
 
 Rows whose kept set outgrows the candidate list take the full-row fallback
 (a stable radix sort of the row in the workspace).  A call holds at most
-min(rows, 64) such buffer sets; rows beyond wait for one.  The first test
-makes every row of a 160-row batch take the fallback and compares all of
+min(rows, 256) such buffer sets; rows beyond wait for one.  The first test
+makes every row of a 320-row batch take the fallback and compares all of
 them with the oracle.  The others run configurations 4 and 5 at their full
 batch (1024 x 256000 and 4096 x 128256): determinism, the per-row outputs'
 invariants, and oracle parity on rows spread over the batch.
@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 
 def test_fallback_pool_contention(cuda):
-    rows, n = 160, 20000
+    rows, n = 320, 20000
     x = np.random.default_rng(21).normal(0, 0.3, (rows, n)).astype(np.float32)
     p = Params(temperature=1.2, top_k=0, top_p=0.9, min_p=0.0, repetition_penalty=1.0)
     u = llz.rng_uniforms(31, rows)
