@@ -209,6 +209,15 @@ void llz_sampler_set_state(llz_sampler *s, const uint64_t state[4]);
 int llz_debug_math(const float *d_in, float *d_exp, float *d_log, float *d_expm1, float *d_tanh,
                    int64_t n, void *stream);
 
+/* Test hook (no counterpart in the reference): the largest relative error,
+ * in units of 2^-23, of the hardware exp2 (op 0) or log2 (op 1) that the
+ * kernels' estimates use, over the `count` floats whose bit patterns start at
+ * `first_bits`, against double-precision exp2 / log2.  Writes
+ * round-toward-zero(error * 2^20), saturated at 0xffffffff, to *d_max_err
+ * (device memory, one u32, overwritten).  The estimates' error bounds assume
+ * at most 1 unit (1 ulp) on the ranges the kernels evaluate. */
+int llz_debug_hw_error(int32_t op, uint32_t first_bits, uint32_t count, uint32_t *d_max_err, void *stream);
+
 /* Measurement hook (no counterpart in the reference): while set, every
  * llz_sample_rows call records `begin_event` right before and `end_event`
  * right after its per-row sampling kernel, on the call's stream (both are

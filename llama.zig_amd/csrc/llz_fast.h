@@ -39,7 +39,7 @@
 // (X = (v - m) log2(e) / T, |X| <= 25 - j): the reference's own two
 // roundings of its argument (one when T == 1: RN(x / 1) is exact) and the
 // rounding of log2(e)/T contribute 3|X| 2^-24 (2|X| when T == 1, in log2
-// units); with B_w = c_w - m RN(log2(e)/T) (|B_w| <= 32, checked; the kernel
+// units); with B_w = c_w - m RN(log2(e)/T) (|B_w| <= 64, checked; the kernel
 // bounds with the wave's rounded value |aw| = |RN(B_w)|), the rounding of
 // v RN(log2(e)/T) - c_w adds at most (|X| + |B_w|) 2^-24 and that of the
 // argument of R_w at most |B_w| 2^-24, so together ln2 (4|X| + 2|B_w|) 2^-24
@@ -294,7 +294,7 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
 
 // Relative error bound of the estimate for terms that matter on grid j
 // (see the header comment), doubled.  bw = |B_w|, the magnitude of the wave's
-// rounded R_w argument fma(m, -RN(log2(e)/T), c_w) (at most 32); t1: T == 1,
+// rounded R_w argument fma(m, -RN(log2(e)/T), c_w) (at most 64); t1: T == 1,
 // where the reference's argument takes one rounding instead of two.
 __device__ __forceinline__ float fast_eps(int j, float bw, bool t1) {
   const float ax = (float)(25 - j);

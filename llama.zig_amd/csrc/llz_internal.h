@@ -93,5 +93,6 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
                          hipStream_t st);
 hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, float* out_expm1, float* out_tanh,
                              int64_t n, hipStream_t st);
+hipError_t launch_hw_error(int op, uint32_t first, uint32_t count, uint32_t* max_err, hipStream_t st);
 
 }  // namespace llz

@@ -5,6 +5,8 @@
 //   k_argmax      greedy rows (temperature <= 0)          sampler.zig:31-41,50
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "llz_internal.h"
 #include "llz_rowops.h"
 
@@ -86,8 +88,45 @@ __global__ __launch_bounds__(256) void k_math_probe(const float* __restrict__ in
 }
 
 // ---------------------------------------------------------------------------
+// k_hw_error: the largest relative error of the hardware exp2 (op 0) or log2
+// (op 1) over a range of float bit patterns, against double precision, as
+// error * 2^43 (units of 2^-23, times 2^20) folded into *max_err.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_hw_error(int op, uint32_t first, uint32_t count,
+                                                  uint32_t* __restrict__ max_err) {
+  uint32_t worst = 0;
+  const uint64_t step = (uint64_t)gridDim.x * 256u;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < count; i += step) {
+    const float x = __uint_as_float(first + (uint32_t)i);
+    float r;
+    double y;
+    if (op == 0) {
+      r = __builtin_amdgcn_exp2f(x);
+      y = exp2((double)x);
+    } else {
+      r = __builtin_amdgcn_logf(x);
+      y = log2((double)x);
+    }
+    const double q = fabs((double)r - y) / fabs(y) * 0x1p43;
+    worst = max(worst, q < 4.0e9 ? (uint32_t)q : 0xffffffffu);  // NaN -> saturated
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) worst = max(worst, (uint32_t)__shfl_xor((int)worst, m, kWave));
+  if (lane_id() == 0) atomicMax(max_err, worst);
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
+__global__ void k_zero_u32(uint32_t* p) { *p = 0u; }
+
+hipError_t launch_hw_error(int op, uint32_t first, uint32_t count, uint32_t* max_err, hipStream_t st) {
+  hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(1), 0, st, max_err);
+  const uint64_t blocks = std::min<uint64_t>(4096, ((uint64_t)count + 255) / 256);
+  hipLaunchKernelGGL(k_hw_error, dim3((unsigned)blocks), dim3(256), 0, st, op, first, count, max_err);
+  return hipGetLastError();
+}
+
 hipError_t launch_math_probe(const float* in, float* out_exp, float* out_log, float* out_expm1, float* out_tanh,
                              int64_t n, hipStream_t st) {
   const int64_t blocks = (n + 255) / 256;

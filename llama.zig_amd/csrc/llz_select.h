@@ -636,13 +636,16 @@ __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float 
 
 // Total and draw over p-order positions [0, K) whose keep flag is set
 // (sampler.zig:156-168).  keep(q) -> bool.
+// first: the id of indices[0] (the row's first element in p order) when L
+// does not start with it (0xffffffff: L.id(0)).
 template <typename List, typename Keep>
 __device__ void total_and_draw(const List& L, int K, Keep keep, float u, float& total,
-                               uint32_t& token, uint32_t& consumed, SampleShared& sh, int& bank) {
+                               uint32_t& token, uint32_t& consumed, SampleShared& sh, int& bank,
+                               uint32_t first = 0xffffffffu) {
   int st;
   total = seq_accumulate<false>(0.0f, K, -1.0f, st, [&](int q) { return keep(q) ? L.p(q) : -0.0f; }, sh,
                                 bank);
-  const uint32_t tok0 = L.id(0);
+  const uint32_t tok0 = first != 0xffffffffu ? first : L.id(0);
   if (total <= 0.0f) {
     token = tok0;
     consumed = 0;
@@ -1038,6 +1041,151 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
 
 // The full-row fallback of k_select: every probability, stable radix sort of
 // the whole row in the workspace, the filters and the draw over it.
+// Typical-p over the full row (sampler.zig:128-154) in the full-row
+// fallback.  What the reference's loop keeps is the selected elements before
+// the first position of the typical order (dev ascending, index ascending
+// among equal devs: std.mem.sort is stable) where the cumulative probability
+// of the selected ones exceeds typical_p; so only the order's head up to that
+// position is needed, not the whole row sorted by dev:
+//  1. each element's dev key (the bits of dev >= 0; 0xffffffff when it is not
+//     selected) in index order, and a histogram of the selected ones by the
+//     key's top 11 bits (a monotone bucket of dev) with their count and an
+//     approximate probability sum;
+//  2. the head: the buckets up to the first one where the approximate
+//     cumulative sum exceeds typical_p (1 + 2^-5);
+//  3. the head's elements, in index order, sorted by key (stable);
+//  4. the exact cumulative sum over the sorted head.  If it does not exceed
+//     typical_p inside the head (the approximate sums misled, or the head is
+//     everything), steps 1-4 run again with every selected element.
+// Selected: the element's p-order position is below K, i.e. its key ~p bits
+// pk and index i satisfy (pk, i) <= (keyK, idK), the key and id at position
+// K - 1 (every element when K == n).  Returns the head's length C (sorted
+// (key, id) in Ck, Cv), the first position st whose sum exceeds
+// typical_p (-1: none, and then C == K), and the id of the row's first
+// element in p order (p desc, id asc).
+struct TypicalHead {
+  int C, st;
+  uint32_t first;
+};
+
+template <class Src>
+__device__ TypicalHead typical_head(const Src& X, int n, float m, float S, float H, const RowParams& P, int K,
+                                    uint32_t keyK, uint32_t idK, uint32_t* Bk, uint32_t* Bv, uint32_t* Ck,
+                                    uint32_t* Cv, SampleShared& sh, int& bank) {
+  constexpr int HB = 2048;  // histogram buckets: key >> 20 for keys <= 0x7fffffff
+  constexpr int TV = 8;     // elements per thread per tile
+  const int t = (int)threadIdx.x;
+  const bool t1 = (P.flags & kFlagTIsOne) != 0;
+  const bool vec = (P.flags & kFlagVecSrc) != 0;
+  uint32_t* hcnt = sh.u.post.radix.stage_k;                        // [HB]
+  float* hsum = reinterpret_cast<float*>(sh.u.post.radix.stage_v);  // [HB]
+  TypicalHead r{0, -1, 0u};
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    // ---- 1. dev keys (and on the first attempt the histogram)
+    if (attempt == 0) {
+      for (int b = t; b < HB; b += kNT) {
+        hcnt[b] = 0u;
+        hsum[b] = 0.0f;
+      }
+      lds_barrier();
+    }
+    uint32_t bpk = 0xffffffffu, bid = 0xffffffffu;  // this thread's first element in p order
+    for (int base = 0; base < n; base += kNT * TV) {
+      const int pos = base + t * TV;
+      float va[kLaneV], vb[kLaneV];
+      X.load4(pos, n, vec, va);
+      X.load4(pos + kLaneV, n, vec, vb);
+#pragma unroll
+      for (int k = 0; k < TV; ++k) {
+        const int i = pos + k;
+        if (i < n) {
+          const float p = row_exp(k < kLaneV ? va[k] : vb[k - kLaneV], m, P.temperature, t1) / S;
+          const uint32_t pk = ~__float_as_uint(p);
+          const bool sel = K >= n || pk < keyK || (pk == keyK && (uint32_t)i <= idK);
+          const float surprise = p > 0.0f ? -log_f32(p) : kInf;
+          const uint32_t dk = sel ? __float_as_uint(fabsf(surprise - H)) : 0xffffffffu;
+          Bk[i] = dk;
+          if (pk < bpk || (pk == bpk && (uint32_t)i < bid)) {
+            bpk = pk;
+            bid = (uint32_t)i;
+          }
+          if (attempt == 0 && sel) {
+            atomicAdd(&hcnt[dk >> 20], 1u);
+            atomicAdd(&hsum[dk >> 20], p);
+          }
+        }
+      }
+    }
+    if (attempt == 0) {
+      const uint32_t gpk = wg_min_u32<kNT>(bpk, sh.wg, bank);
+      r.first = wg_min_u32<kNT>(bpk == gpk ? bid : 0xffffffffu, sh.wg, bank);
+    }
+    __threadfence();
+    __syncthreads();
+    // ---- 2. the head's last bucket (wave 0: 32 buckets per lane)
+    if (wave_id() == 0) {
+      int bstar = HB - 1;
+      if (attempt == 0) {
+        const int lane = lane_id();
+        constexpr int PL = HB / kWave;
+        float ls = 0.0f;
+        for (int b = 0; b < PL; ++b) ls += hsum[lane * PL + b];
+        const float incl = __uint_as_float(wave_incl_scan_op(__float_as_uint(ls), 0u, [](uint32_t a, uint32_t b) {
+          return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+        }));
+        const float thr = P.typical_p * (1.0f + 0x1p-5f);
+        float run = incl - ls;
+        int hit = HB;
+        for (int b = 0; b < PL && hit == HB; ++b) {
+          run += hsum[lane * PL + b];
+          if (run > thr) hit = lane * PL + b;
+        }
+        const uint64_t hm = bal64(hit < HB);
+        if (hm != 0ull) bstar = (int)readlane_u32((uint32_t)hit, __ffsll((long long)hm) - 1);
+      }
+      if (lane_id() == 0) sh.misc[2] = (uint32_t)bstar;
+    }
+    __syncthreads();
+    const uint32_t bstar = sh.misc[2];
+    // ---- 3. the head in index order
+    int C = 0;
+    for (int base = 0; base < n; base += kNT * TV) {
+      const int pos = base + t * TV;
+      uint32_t dk[TV];
+      uint32_t cnt = 0;
+#pragma unroll
+      for (int k = 0; k < TV; ++k) {
+        dk[k] = pos + k < n ? Bk[pos + k] : 0xffffffffu;
+        cnt += (dk[k] != 0xffffffffu && (dk[k] >> 20) <= bstar) ? 1u : 0u;
+      }
+      uint32_t o = (uint32_t)C + wg_excl_scan_sat<kNT>(cnt, 0x7fffffffu, sh.wg, bank);
+#pragma unroll
+      for (int k = 0; k < TV; ++k) {
+        if (dk[k] != 0xffffffffu && (dk[k] >> 20) <= bstar) {
+          Ck[o] = dk[k];
+          Cv[o] = (uint32_t)(pos + k);
+          ++o;
+        }
+      }
+      C += (int)wg_sum_sat<kNT>(cnt, 0x7fffffffu, sh.wg, bank);
+    }
+    __threadfence();
+    __syncthreads();
+    // ---- 4. sorted by key, then the exact cumulative sum
+    wg_radix_sort_pairs<kNT>(Ck, Cv, Bk, Bv, C, sh.u.post.radix);
+    __threadfence();
+    __syncthreads();
+    int st;
+    list_accumulate<kNT, 2, false>(
+        0.0f, C, P.typical_p, st,
+        [&](int d) { return row_exp(X.at((int)Cv[d]), m, P.temperature, t1) / S; }, sh.wg, bank);
+    r.C = C;
+    r.st = st;
+    if (st >= 0 || C >= K) break;
+  }
+  return r;
+}
+
 template <class Src>
 __device__ __noinline__ void select_full_row(const KArgs* A, const PenShared* pen, SampleShared& sh, int bank,
                                              float m, float S, uint32_t path) {
@@ -1102,102 +1250,134 @@ __device__ __noinline__ void select_full_row(const KArgs* A, const PenShared* pe
   uint32_t* Ck = Q.fb + 4 * fs + fo;
   uint32_t* Cv = Q.fb + 5 * fs + fo;
   uint8_t* mask = Q.fb_mask + fo;
-  for (int base = 0; base < n; base += kTile) {
-    float v[kV];
-    const int pos = base + t * kV;
-    X.load4(pos, n, vec, v);
-#pragma unroll
-    for (int k = 0; k < kV; ++k) {
-      if (pos + k < n) {
-        const float p = row_exp(v[k], m, P.temperature, t1) / S;
-        Ak[pos + k] = ~__float_as_uint(p);
-        Av[pos + k] = (uint32_t)(pos + k);
-      }
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  wg_radix_sort_pairs<kNT>(Ak, Av, Bk, Bv, n, sh.u.post.radix);
-  __threadfence();
-  __syncthreads();
+  // With typical-p and no prefix filter every element is selected (K = n),
+  // and the p order matters only among the elements typical-p keeps: the
+  // whole row is then never sorted by p.
+  const bool filters = (P.top_k > 0 && P.top_k < (uint32_t)n) || (P.top_p > 0.0f && P.top_p < 1.0f) ||
+                       P.min_p > 0.0f;
+  const bool lazy_p = typical && !filters && n >= 2;
   const GlobalList GL{Ak, Av};
-  K = prefix_filters(GL, n, kInf, n, P, S, sh, bank);  // M = n: never -1
-  if (K < 0) K = 0;
-  if (typical && K >= 2) {
-    path |= kPathEntropy;
-    {
-        const EntropyResult er = entropy_pass<Src>(X, n, m, S, P.temperature, P.flags, sh, bank);
-        H = er.H;
-        bank = er.bank;
-      }
-    for (int i = t; i < n; i += kNT) mask[i] = 0;
-    __threadfence();
-    __syncthreads();
-    for (int q = t; q < K; q += kNT) mask[Av[q]] = 1;
-    __threadfence();
-    __syncthreads();
-    // selected ids in index order with their dev keys (stream compaction)
-    int written = 0;
-    for (int base = 0; base < n; base += kNT) {
-      const int i = base + t;
-      const bool sel = i < n && mask[i] == 1;
-      const uint32_t before = wg_excl_scan_sat<kNT>(sel ? 1u : 0u, 0x7fffffffu, sh.wg, bank);
-      if (sel) {
-        const float p = row_exp(X.at(i), m, P.temperature, t1) / S;
-        const float surprise = p > 0.0f ? -log_f32(p) : kInf;
-        Bk[written + before] = __float_as_uint(fabsf(surprise - H));
-        Bv[written + before] = (uint32_t)i;
-      }
-      written += (int)wg_sum_sat<kNT>(sel ? 1u : 0u, 0x7fffffffu, sh.wg, bank);
-    }
-    __threadfence();
-    __syncthreads();
-    wg_radix_sort_pairs<kNT>(Bk, Bv, Ck, Cv, written, sh.u.post.radix);
-    __threadfence();
-    __syncthreads();
-    int st;
-    list_accumulate<kNT, 2, false>(
-        0.0f, written, P.typical_p, st,
-        [&](int d) { return row_exp(X.at((int)Bv[d]), m, P.temperature, t1) / S; }, sh.wg, bank);
-    const int keep_n = st >= 0 ? st : written;
-    for (int d = t; d < keep_n; d += kNT) mask[Bv[d]] = 2;
-    __threadfence();
-    __syncthreads();
-    total_and_draw(GL, K, [&](int q) { return mask[Av[q]] == 2; }, u, total, token, consumed, sh, bank);
-  } else if (typical && K == 1) {
-    const bool k0 = !(GL.p(0) > P.typical_p);
-    total_and_draw(GL, K, [&](int q) { return k0; }, u, total, token, consumed, sh, bank);
-  } else {
-    total_and_draw(GL, K, [&](int q) { return true; }, u, total, token, consumed, sh, bank);
-  }
-  // outputs (kept list compaction is thread-serial: diagnostic use only)
-  const bool use_mask = typical && K >= 2;
-  uint32_t kept = 0;
-  for (int q = t; q < K; q += kNT) {
-    bool kq = use_mask ? mask[Av[q]] == 2 : (typical && K == 1 ? !(GL.p(0) > P.typical_p) : true);
-    kept += kq ? 1u : 0u;
-  }
-  kept = wg_sum_sat<kNT>(kept, 0x7fffffffu, sh.wg, bank);
-  if (t == 0) {
-    if (Q.kept_ids || Q.kept_probs) {
-      int o = 0;
-      for (int q = 0; q < K && o < P.kept_cap; ++q) {
-        bool kq = use_mask ? mask[Av[q]] == 2 : (typical && K == 1 ? !(GL.p(0) > P.typical_p) : true);
-        if (kq) {
-          if (Q.kept_ids) Q.kept_ids[(int64_t)row * P.kept_cap + o] = GL.id(q);
-          if (Q.kept_probs) Q.kept_probs[(int64_t)row * P.kept_cap + o] = GL.p(q);
-          ++o;
+  if (!lazy_p) {
+    for (int base = 0; base < n; base += kTile) {
+      float v[kV];
+      const int pos = base + t * kV;
+      X.load4(pos, n, vec, v);
+#pragma unroll
+      for (int k = 0; k < kV; ++k) {
+        if (pos + k < n) {
+          const float p = row_exp(v[k], m, P.temperature, t1) / S;
+          Ak[pos + k] = ~__float_as_uint(p);
+          Av[pos + k] = (uint32_t)(pos + k);
         }
       }
     }
-    Q.tokens[row] = token;
-    if (Q.consumed) Q.consumed[row] = (uint8_t)consumed;
-    if (Q.kept_count) Q.kept_count[row] = kept;
-    if (Q.row_stats) {
-      float* rs = Q.row_stats + (int64_t)row * 4;
-      rs[0] = m; rs[1] = S; rs[2] = H; rs[3] = total;
+    __threadfence();
+    __syncthreads();
+    wg_radix_sort_pairs<kNT>(Ak, Av, Bk, Bv, n, sh.u.post.radix);
+    __threadfence();
+    __syncthreads();
+    K = prefix_filters(GL, n, kInf, n, P, S, sh, bank);  // M = n: never -1
+    if (K < 0) K = 0;
+  } else {
+    K = n;
+  }
+
+  // The final list (the kept elements among positions [0, Kf) of a list in
+  // p order) and its outputs.
+  auto finish = [&](const auto& L, int Kf, auto keep, uint32_t first) {
+    total_and_draw(L, Kf, keep, u, total, token, consumed, sh, bank, first);
+    uint32_t kept = 0;
+    for (int q = t; q < Kf; q += kNT) kept += keep(q) ? 1u : 0u;
+    kept = wg_sum_sat<kNT>(kept, 0x7fffffffu, sh.wg, bank);
+    if (t == 0) {
+      if (Q.kept_ids || Q.kept_probs) {  // thread-serial: diagnostic use only
+        int o = 0;
+        for (int q = 0; q < Kf && o < P.kept_cap; ++q) {
+          if (keep(q)) {
+            if (Q.kept_ids) Q.kept_ids[(int64_t)row * P.kept_cap + o] = L.id(q);
+            if (Q.kept_probs) Q.kept_probs[(int64_t)row * P.kept_cap + o] = L.p(q);
+            ++o;
+          }
+        }
+      }
+      Q.tokens[row] = token;
+      if (Q.consumed) Q.consumed[row] = (uint8_t)consumed;
+      if (Q.kept_count) Q.kept_count[row] = kept;
+      if (Q.row_stats) {
+        float* rs = Q.row_stats + (int64_t)row * 4;
+        rs[0] = m; rs[1] = S; rs[2] = H; rs[3] = total;
+      }
+      if (Q.status) Q.status[row] = path;
     }
-    if (Q.status) Q.status[row] = path;
+  };
+
+  if (typical && K >= 2) {
+    path |= kPathEntropy;
+    {
+      const EntropyResult er = entropy_pass<Src>(X, n, m, S, P.temperature, P.flags, sh, bank);
+      H = er.H;
+      bank = er.bank;
+    }
+    const uint32_t keyK = K < n ? Ak[K - 1] : 0u;
+    const uint32_t idK = K < n ? Av[K - 1] : 0u;
+    const TypicalHead th = typical_head<Src>(X, n, m, S, H, P, K, keyK, idK, Bk, Bv, Ck, Cv, sh, bank);
+    // the cut: the first element of the typical order that is not kept
+    const bool cut = th.st >= 0;
+    const uint32_t dkc = cut ? Ck[th.st] : 0u, idc = cut ? Cv[th.st] : 0u;
+    if (!lazy_p) {
+      // keep flags in p order: (dev key, id) before the cut's
+      for (int q = t; q < K; q += kNT) {
+        const float p = GL.p(q);
+        const float surprise = p > 0.0f ? -log_f32(p) : kInf;
+        const uint32_t dk = __float_as_uint(fabsf(surprise - H));
+        const uint32_t id = GL.id(q);
+        mask[q] = (!cut || dk < dkc || (dk == dkc && id < idc)) ? 1 : 0;
+      }
+      __threadfence();
+      __syncthreads();
+      finish(GL, K, [&](int q) { return mask[q] != 0; }, 0xffffffffu);
+    } else {
+      // the kept elements are the head's first keep_n; put them in p order
+      const int keep_n = cut ? th.st : th.C;
+      if (keep_n <= kCap) {
+        const int ks = next_pow2(max(keep_n, 1));
+        for (int d = t; d < ks; d += kNT) {
+          if (d < keep_n) {
+            const uint32_t id = Cv[d];
+            const float p = row_exp(X.at((int)id), m, P.temperature, t1) / S;
+            sh.cand[d] = ((uint64_t)(~__float_as_uint(p)) << 32) | id;
+          } else {
+            sh.cand[d] = ~0ull;
+          }
+        }
+        lds_barrier();
+        lds_bitonic_sort_u64<kNT>(sh.cand, ks);
+        lds_barrier();
+        finish(LdsList{sh.cand}, keep_n, [&](int) { return true; }, th.first);
+      } else {
+        // by id, then stably by ~p bits: (p desc, id asc)
+        for (int d = t; d < keep_n; d += kNT) {
+          const uint32_t id = Cv[d];
+          const float p = row_exp(X.at((int)id), m, P.temperature, t1) / S;
+          Ak[d] = id;
+          Av[d] = ~__float_as_uint(p);
+        }
+        __threadfence();
+        __syncthreads();
+        wg_radix_sort_pairs<kNT>(Ak, Av, Bk, Bv, keep_n, sh.u.post.radix);
+        __threadfence();
+        __syncthreads();
+        wg_radix_sort_pairs<kNT>(Av, Ak, Bk, Bv, keep_n, sh.u.post.radix);
+        __threadfence();
+        __syncthreads();
+        finish(GlobalList{Av, Ak}, keep_n, [&](int) { return true; }, th.first);
+      }
+    }
+  } else if (typical && K == 1) {
+    const bool k0 = !(GL.p(0) > P.typical_p);
+    finish(GL, K, [&](int) { return k0; }, 0xffffffffu);
+  } else {
+    finish(GL, K, [&](int) { return true; }, 0xffffffffu);
   }
   // release the slot once every thread is done with it (a value no later
   // call's epoch takes)

@@ -750,7 +750,7 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
 #pragma unroll
       for (int i = 0; i < W; ++i) {
         const float awi = fmaf(m, -l2e_t, F.cw[i]);
-        bad = bad | ((G > i) & !(fabsf(awi) <= 32.0f));
+        bad = bad | ((G > i) & !(fabsf(awi) <= 64.0f));
         const float ri = __builtin_amdgcn_exp2f(awi);
         const float b = W * lane + i < G ? av[i] * ri : 0.0f;
         rtot += b;

@@ -39,7 +39,7 @@ EXPORTED = (
     "llz_argmax_rows", "llz_rng_seed", "llz_rng_next", "llz_rng_float", "llz_rng_uniforms",
     "llz_sampler_create", "llz_sampler_destroy", "llz_sampler_sample", "llz_sampler_sample_uniform",
     "llz_sampler_get_state",
-    "llz_sampler_set_state", "llz_debug_math", "llz_debug_kernel_events", "llz_strerror",
+    "llz_sampler_set_state", "llz_debug_math", "llz_debug_hw_error", "llz_debug_kernel_events", "llz_strerror",
 )
 
 
@@ -157,6 +157,8 @@ def _lib():
         L.llz_sampler_set_state.restype = None
         L.llz_debug_math.argtypes = [vp, vp, vp, vp, vp, i64, vp]
         L.llz_debug_math.restype = C.c_int
+        L.llz_debug_hw_error.argtypes = [i32, C.c_uint32, C.c_uint32, vp, vp]
+        L.llz_debug_hw_error.restype = C.c_int
         L.llz_debug_kernel_events.argtypes = [vp, vp]
         L.llz_debug_kernel_events.restype = C.c_int
         L.llz_strerror.argtypes = [C.c_int]
@@ -333,6 +335,16 @@ def debug_math(x, extra: bool = False):
                                x.numel(), _stream_ptr(None))
     _check(rc, "llz_debug_math")
     return (e, lg, em1, th) if extra else (e, lg)
+
+
+def debug_hw_error(op: int, first_bits: int, count: int) -> float:
+    """Largest relative error, in units of 2^-23, of the hardware exp2 (op 0)
+    or log2 (op 1) over `count` float bit patterns from `first_bits`."""
+    torch = _torch()
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rc = _lib().llz_debug_hw_error(op, first_bits, count, out.data_ptr(), _stream_ptr(None))
+    _check(rc, "llz_debug_hw_error")
+    return float(int(out.cpu().numpy().view("uint32")[0])) / 2.0 ** 20
 
 
 def set_kernel_events(begin=None, end=None) -> None:

@@ -113,6 +113,20 @@ def test_device_log_matches_oracle(cuda, name, lo, hi, step):
         assert bad.size == 0, f"{name}: {bad.size} mismatches, first x={xs[bad[0]]!r}"
 
 
+@pytest.mark.parametrize("name,op,lo,hi", [
+    ("exp2-negative", 0, 0x80000000, 0xc2fc0000),   # -0 .. -126 (every input with a normal result)
+    ("exp2-positive", 0, 0x00000000, 0x42800000),   # 0 .. 64
+    ("log2-entropy", 1, 0x08800000, 0x3e800000),    # 2^-110 .. 2^-2
+])
+def test_hardware_exp2_log2_within_one_ulp(cuda, name, op, lo, hi):
+    """The certified estimates (the single-pass statistics, the streaming
+    normaliser, the entropy pass) take the hardware exp2 and log2 to be within
+    1 ulp of the exact result (relative error <= 2^-23); checked on every
+    float of the ranges they evaluate, against double precision."""
+    err = llz.debug_hw_error(op, lo, hi - lo + 1)
+    assert err <= 1.0, f"{name}: {err} units of 2^-23"
+
+
 # ---------------------------------------------------------------------------
 # the five configurations and the headline batch, full vocab
 # ---------------------------------------------------------------------------
@@ -171,6 +185,11 @@ EDGE = [
     ("all-filters", Params(temperature=1.3, top_k=20, top_p=0.8, min_p=0.01, typical_p=0.9,
                            repetition_penalty=1.0)),
     ("no-filters", Params(temperature=1.0, top_p=1.0, repetition_penalty=1.0)),
+    # wide kept sets (beyond the candidate list on flat rows): typical-p after
+    # a prefix filter in the full-row fallback
+    ("typical-wide-top-p", Params(temperature=2.0, top_p=0.99, typical_p=0.9, repetition_penalty=1.0)),
+    ("typical-wide-min-p", Params(temperature=2.0, top_p=1.0, min_p=1e-3, typical_p=0.7,
+                                  repetition_penalty=1.0)),
 ]
 
 
