@@ -97,6 +97,8 @@ enum {
     LLZ_PATH_ENTROPY = 2,        /* typical-p entropy pass ran (sampler.zig:128-154)       */
     LLZ_PATH_FULL_SORT = 4,      /* kept set beyond the candidate list: full-row sort      */
     LLZ_PATH_STREAM_NORM = 8,    /* normaliser not certified in one pass: streaming pass   */
+    LLZ_PATH_WALK_ROUNDS = 16,   /* diagnostic: more EXACT segments than one round's slots  */
+    LLZ_PATH_RESOLVE_GENERIC = 32, /* diagnostic: a crossing beyond the tabulated binades   */
     LLZ_PATH_ERROR = (int)0x80000000u
 };
 

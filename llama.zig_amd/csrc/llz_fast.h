@@ -147,6 +147,7 @@ struct FastShared {
   int ne;         // combine: number of entries
   float s_run;    // combine: running sum at next_g
   int done;
+  uint32_t diag;  // kPathWalkRounds / kPathResolveGeneric (diagnostics for the row's status)
 };
 
 typedef float llz_f4v __attribute__((ext_vector_type(4)));

@@ -30,6 +30,8 @@ constexpr uint32_t kPathSumLe0 = 1u;
 constexpr uint32_t kPathEntropy = 2u;
 constexpr uint32_t kPathFallback = 4u;      // full-row radix sort
 constexpr uint32_t kPathNormFallback = 8u;  // streaming normaliser (row not certified by the fast path)
+constexpr uint32_t kPathWalkRounds = 16u;    // diagnostic: the walk took more than one round of EXACT slots
+constexpr uint32_t kPathResolveGeneric = 32u;  // diagnostic: an event beyond a segment's tabulated grids
 constexpr uint32_t kPathError = 0x80000000u;
 
 struct RowParams {

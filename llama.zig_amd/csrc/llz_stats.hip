@@ -250,7 +250,7 @@ __device__ __forceinline__ SlotAhead slot_ahead(const FastShared& F, int slot) {
 // (N * 2^(j-23), N < 2^24), kept in scalar registers; the slot's data was
 // read ahead into X.
 __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slot, int J0, int ng,
-                                              const SlotAhead& X, const FastShared& F) {
+                                              const SlotAhead& X, FastShared& F) {
   const int lane = lane_id();
   uint32_t N = N_io;
   int j = j_io;
@@ -320,6 +320,7 @@ __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slo
       tm = uni_u64(F.u.x.tmask[slot][k]);
     } else {
       const float s = uni_f(resolve_generic(__uint_as_float(grid_bits(N, j)), X.e4.x, X.e4.y, X.e4.z, X.e4.w, p));
+      if (lane == 0) F.diag |= kPathResolveGeneric;
       const Grid g = grid_of(s);
       N = g.N;
       j = g.j;
@@ -685,6 +686,7 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
     F.next_e = 0;
     F.s_run = 0.0f;
     F.done = 0;
+    F.diag = 0;
   }
   __syncthreads();
 
@@ -1060,6 +1062,7 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
     // segments beyond the slots in further rounds
     for (int round = 0; !F.fail; ++round) {
       if (round > 0) {
+        if (t == 0) F.diag |= kPathWalkRounds;
         if (w == 0) {  // slots for the EXACT segments from the stopping entry's on, in order
           const int g_from = (int)((F.u.x.ent_a[F.next_e] >> 2) & 1023u);
           int cnt = 0;
@@ -1228,6 +1231,12 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
   static_assert(sizeof(SampleShared) <= sizeof(F.u), "the selection's memory must lie inside F.u");
   select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified, u_row, certified && pre_ok,
              cand_pre, cand_n0, X, O, XF ? &pen_sh : nullptr, kernel_args_ptr());
+  // the walk's diagnostics join the status thread 0 wrote (F.diag lies past
+  // the selection's memory)
+  if (t == 0 && Q.status) {
+    const uint32_t d = F.diag;
+    if (d != 0u) Q.status[row] |= d;
+  }
 }
 
 }  // namespace

@@ -162,7 +162,35 @@ def test_headline_full_batch_properties(cuda):
             assert g1["tokens"][r] in g1["kept_ids"][r, :kc]
         # kept probabilities are non-increasing
         assert np.all(np.diff(g1["kept_probs"][r, :kc]) <= 0)
-    compare_rows(x, w.params, u, g1, rows=range(0, w.rows, 17))
+    compare_rows(x, w.params, u, g1)
+
+
+def test_walk_rare_paths_reached(cuda):
+    """The single pass's rarer walk paths are exercised and exact: rows with
+    more EXACT segments than one round's slots, and rows with a crossing
+    beyond a segment's tabulated binades (configuration 5's peaked rows have
+    both), compared with the oracle."""
+    import torch
+
+    w = WORKLOADS["c5"]
+    rows = 64
+    x = w.logits(rows)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    cfg = llz.SamplerConfig.of(w.params)
+    res = llz.sample_rows(torch.from_numpy(x).to(cuda), cfg, torch.from_numpy(u).to(cuda), kept_cap=64,
+                          stats=True, path=True)
+    torch.cuda.synchronize()
+    paths = res.row_path.cpu().numpy().view(np.uint32)
+    rounds = np.flatnonzero(paths & llz.PATH_WALK_ROUNDS)
+    generic = np.flatnonzero(paths & llz.PATH_RESOLVE_GENERIC)
+    assert rounds.size > 0, "no row needed a second round of EXACT slots"
+    assert generic.size > 0, "no row reached resolve_generic"
+    assert not np.any(paths[np.union1d(rounds, generic)] & llz.PATH_STREAM_NORM)
+    g = dict(tokens=res.tokens.cpu().numpy().view(np.uint32), consumed=res.consumed.cpu().numpy(),
+             kept_count=res.kept_count.cpu().numpy().view(np.uint32),
+             kept_ids=res.kept_ids.cpu().numpy().view(np.uint32), kept_probs=res.kept_probs.cpu().numpy(),
+             stats=res.row_stats.cpu().numpy(), cap=64)
+    compare_rows(x, w.params, u, g, rows=np.union1d(rounds[:8], generic[:8]))
 
 
 # ---------------------------------------------------------------------------
