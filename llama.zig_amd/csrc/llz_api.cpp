@@ -53,7 +53,7 @@ uint32_t post_bits(const llz_logit_post* post) {
 // with their owner words; the penalised copy only for windows too long to
 // fuse.
 struct Layout {
-  size_t status, cand, qovf, owner, fb, fb_mask, penal, total;
+  size_t status, claim, cand, qovf, owner, fb, fb_mask, penal, total;
   int fb_slots;
   bool has_penal;
 };
@@ -66,6 +66,7 @@ Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int
   const size_t ns = (size_t)L.fb_slots;
   size_t off = 0;
   L.status = off;  off = align_up(off + r * sizeof(uint32_t));
+  L.claim = off;   off = align_up(off + sizeof(uint64_t));
   L.cand = off;    off = align_up(off + r * (size_t)kCandCap * sizeof(uint64_t));
   L.qovf = off;    off = align_up(off + r * (size_t)kQovfRow * sizeof(uint32_t));
   L.owner = off;   off = align_up(off + ns * sizeof(uint64_t));
@@ -96,6 +97,32 @@ float candidate_theta(const llz_sampler_config* cfg, int32_t vocab) {
   // the row maximum (e == 1) and its probability ties must stay certified
   if (!(theta <= 0.5f)) theta = 0.5f;
   return theta;
+}
+
+// The number of CUs of the device a stream runs on (cached per device; the
+// last stream's device is remembered per thread, since asking the runtime for
+// a stream's device costs more than a launch).
+int device_cus(hipStream_t st) {
+  static std::atomic<int> cache[64];
+  thread_local hipStream_t last_st = nullptr;
+  thread_local int last_dev = -1;
+  int dev = 0;
+  if (st && st == last_st) {
+    dev = last_dev;
+  } else if (st) {
+    if (hipStreamGetDevice(st, &dev) != hipSuccess) return -1;
+    last_st = st;
+    last_dev = dev;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return -1;
+  }
+  if (dev < 0 || dev >= 64) return -1;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c <= 0) {
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) return -1;
+    cache[dev].store(c, std::memory_order_relaxed);
+  }
+  return c;
 }
 
 int check_common(const float* d_logits, int64_t row_stride, int32_t rows, int32_t vocab) {
@@ -170,6 +197,7 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   if (n_prev > 0 && !d_prev_tokens) return LLZ_E_INVALID_ARG;
   if (extras && (extras->d_kept_ids || extras->d_kept_probs) && extras->kept_cap <= 0)
     return LLZ_E_INVALID_ARG;
+  if (rows >= (1 << 24)) return LLZ_E_INVALID_ARG;  // the row-claim counter's width
   hipStream_t st = (hipStream_t)stream;
   const uint32_t xb = post_bits(post);
   const float cap = (xb & kXfCap) ? post->final_logit_softcapping : 0.0f;
@@ -232,6 +260,13 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   P.pen_w = (xf_src & kXfPen) ? window : 0;
   P.prev_stride = prev_stride;
   P.fb_slots = L.fb_slots;
+  {
+    // at most one k_stats workgroup per CU (its shared memory allows no more),
+    // all resident at once; rows beyond them are claimed
+    const int cus = device_cus(st);
+    if (cus <= 0) return LLZ_E_HIP;
+    P.grid = rows < cus ? rows : cus;
+  }
   P.epoch = g_epoch.fetch_add(1, std::memory_order_relaxed) & ((1ull << 62) - 1);
   // LLZ_TEST_QUEUE_CAP: a smaller special-queue chunk, so that tests reach
   // the chunked queue on ordinary rows (the kernel clamps it to its own)
@@ -258,6 +293,7 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   Q.fb_mask = (uint8_t*)(ws + L.fb_mask);
   Q.fb_owner = (unsigned long long*)(ws + L.owner);
   Q.qovf = (uint32_t*)(ws + L.qovf);
+  Q.claim = (unsigned long long*)(ws + L.claim);
   Q.prev_win = (xf_src & kXfPen) ? d_prev_tokens + (n_prev - window) : nullptr;
   e = launch_sample(P, Q, g_ev_begin, g_ev_end, st);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;

@@ -57,6 +57,7 @@ struct RowParams {
   int32_t pen_w;     // kXfPen: window length (<= kPenMax)
   int64_t prev_stride;
   int32_t fb_slots;  // full-row fallback buffers in the workspace
+  int32_t grid;      // k_stats workgroups: rows [0, grid) one each, the rest claimed (Q.claim)
   uint64_t epoch;    // this call's tag: a fallback slot whose owner word holds it is in use
 };
 
@@ -76,6 +77,7 @@ struct RowPtrs {
   uint8_t* fb_mask;       // [fb_slots][n]
   unsigned long long* fb_owner;  // [fb_slots] epoch of the row using each slot
   uint32_t* qovf;         // [rows][kQovfRow] k_stats special-queue overflow
+  unsigned long long* claim;  // rows claimed beyond the grid: (epoch tag << 24) | count
   const uint32_t* prev_win;  // kXfPen: row 0's window (its last pen_w history tokens)
 };
 

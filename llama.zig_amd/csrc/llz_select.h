@@ -687,10 +687,10 @@ __device__ __forceinline__ Src make_src(const RowParams& P, const RowPtrs& Q, in
 // The streaming normaliser (sampler.zig:83-88) for a row k_stats could not
 // certify; fills the candidate list in LDS.
 template <class Src>
-__device__ __noinline__ NormResult select_norm_fallback(const KArgs* A, const PenShared* pen, SampleShared& sh,
+__device__ __noinline__ NormResult select_norm_fallback(const KArgs* A, int row, const PenShared* pen, SampleShared& sh,
                                                         int bank, float m_known) {
   const RowParams& P = A->P;
-  const Src X = make_src<Src>(P, A->Q, blockIdx.x, pen);
+  const Src X = make_src<Src>(P, A->Q, row, pen);
   if (threadIdx.x == 0) sh.cand_count = 0;
   NormResult r;
   r.S = row_normaliser(X, P.n, P, sh, bank, r.m, m_known);
@@ -699,8 +699,8 @@ __device__ __noinline__ NormResult select_norm_fallback(const KArgs* A, const Pe
 }
 
 template <class Src>
-__device__ __noinline__ void select_full_row(const KArgs* A, const PenShared* pen, SampleShared& sh, int bank,
-                                             float m, float S, uint32_t path);
+__device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenShared* pen, SampleShared& sh,
+                                             int bank, float m, float S, uint32_t path);
 
 constexpr int kShortMax = 256;  // longest candidate list of the short path
 
@@ -709,9 +709,8 @@ constexpr int kShortMax = 256;  // longest candidate list of the short path
 // alone (sampler.zig:92-126, 156-168), with the same certified-prefix rules
 // as prefix_filters.  Returns false, on every thread, when elements outside
 // the list decide the cut: the caller then takes the full-row fallback.
-__device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& Q, SampleShared& sh, int c,
+__device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& Q, int row, SampleShared& sh, int c,
                                              float m, float S, uint32_t path, float u_row) {
-  const int row = blockIdx.x;
   const int t = (int)threadIdx.x, lane = lane_id(), w = wave_id();
   const int n = P.n;
   uint64_t* key = sh.cand;               // (~p bits, id): ascending = (p desc, id asc)
@@ -840,7 +839,7 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
   return sh.misc[0] == 0u;
 }
 
-// The rest of sampleWithRandom (sampler.zig:89-168) for row blockIdx.x,
+// The rest of sampleWithRandom (sampler.zig:89-168) for row `row`,
 // after k_stats' phases: from the row maximum m, the normaliser S and the
 // candidate list in Q.cand (cc entries), or, for a row k_stats could not
 // certify, from the streaming normaliser.  Every thread of the workgroup
@@ -851,15 +850,14 @@ template <class Src>
 __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q, SampleShared& sh, float m,
                                            float S, uint32_t cc_in, bool uncertified, float u_row, bool pre_ok,
                                            uint64_t cand_pre, uint32_t cand_n0, const Src& X, const Src& O,
-                                           const PenShared* pen, const KArgs* A) {
+                                           const PenShared* pen, const KArgs* A, int row) {
   int bank = 0;
-  const int row = blockIdx.x;
   const int t = (int)threadIdx.x;
   const int n = P.n;
   uint32_t path = 0;
   if (uncertified) {
     // the streaming normaliser (sampler.zig:83-88) fills the candidate list in LDS
-    const NormResult r = select_norm_fallback<Src>(A, pen, sh, bank, m);
+    const NormResult r = select_norm_fallback<Src>(A, row, pen, sh, bank, m);
     S = r.S;
     m = r.m;
     bank = r.bank;
@@ -928,7 +926,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   const bool ovf = cc > (uint32_t)kCap;
   const int c = ovf ? kCap : (int)cc;
   if (!ovf && c <= kShortMax && !(P.typical_p > 0.0f && P.typical_p < 1.0f)) {
-    if (!select_short(P, Q, sh, c, m, S, path, u_row)) select_full_row<Src>(A, pen, sh, bank, m, S, path);
+    if (!select_short(P, Q, row, sh, c, m, S, path, u_row)) select_full_row<Src>(A, row, pen, sh, bank, m, S, path);
     return;
   }
   const int csort = next_pow2(c);
@@ -1036,7 +1034,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   }
 
   // ---- full-row fallback: every probability, stable radix sort, filters
-  select_full_row<Src>(A, pen, sh, bank, m, S, path);
+  select_full_row<Src>(A, row, pen, sh, bank, m, S, path);
 }
 
 // The full-row fallback of k_select: every probability, stable radix sort of
@@ -1187,11 +1185,10 @@ __device__ TypicalHead typical_head(const Src& X, int n, float m, float S, float
 }
 
 template <class Src>
-__device__ __noinline__ void select_full_row(const KArgs* A, const PenShared* pen, SampleShared& sh, int bank,
-                                             float m, float S, uint32_t path) {
+__device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenShared* pen, SampleShared& sh,
+                                             int bank, float m, float S, uint32_t path) {
   const RowParams& P = A->P;
   const RowPtrs& Q = A->Q;
-  const int row = blockIdx.x;
   const Src X = make_src<Src>(P, Q, row, pen);
   const int t = (int)threadIdx.x;
   const int n = P.n;

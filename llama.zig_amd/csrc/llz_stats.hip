@@ -488,21 +488,37 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
   }
 }
 
+// Shared memory of k_stats.
+union StatsShared {
+  FastShared fast;      // phases L .. C
+  SampleShared select;  // then the selection stage
+};
+
+// The next row beyond the grid for a workgroup that finished one: a counter
+// word tagged with the low 40 bits of the call's epoch (a word left by
+// another call, or not yet written, counts as 0 for this one).  Returns grid +
+// the count before the claim (>= rows: nothing left).
+__device__ __noinline__ int claim_row(unsigned long long* word, unsigned long long epoch, int grid) {
+  const unsigned long long tag = (epoch & ((1ull << 40) - 1)) << 24;
+  unsigned long long old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    const unsigned long long cnt = (old & ~((1ull << 24) - 1)) == tag ? (old & ((1ull << 24) - 1)) : 0ull;
+    const unsigned long long seen = atomicCAS(word, old, tag | (cnt + 1));
+    if (seen == old) return grid + (int)cnt;
+    old = seen;
+  }
+}
+
 // FASTLD: 16-byte aligned rows with n % 4 == 0 (one float4 per lane per
 // segment through buffer loads); otherwise element loads.  XF: the rows are
 // read through post-processing and/or the fused repetition penalty
 // (llz_xform.h); otherwise as they are.
 template <bool FASTLD, bool XF>
-__global__ __launch_bounds__(NT) void k_stats(KArgs A) {
+__device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& U, PenShared& pen_sh) {
   const RowParams P = A.P;
   const RowPtrs Q = A.Q;
-  __shared__ union {
-    FastShared fast;      // phases L .. C
-    SampleShared select;  // then the selection stage
-  } U;
-  __shared__ PenShared pen_sh;  // kXfPen: the row's penalised positions
+  constexpr int dcap = DCAP;  // EXACT slots per round
   FastShared& F = U.fast;
-  const int row = blockIdx.x;
   const int t = (int)threadIdx.x, lane = lane_id();
   const int w = __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform: scalar registers
   const int n = P.n;
@@ -749,6 +765,7 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
     {
       float rtot = 0.0f, before_w = 0.0f, b_w = 0.0f;
       bool bad = false;
+      int gc = -1;  // the lane's last segment whose estimated sum is at least 1/2
 #pragma unroll
       for (int i = 0; i < W; ++i) {
         const float awi = fmaf(m, -l2e_t, F.cw[i]);
@@ -758,7 +775,17 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
         rtot += b;
         before_w += i < w ? b : 0.0f;
         b_w = i == w ? b : b_w;
+        gc = b >= 0.5f ? W * lane + i : gc;
       }
+      // gm: the last segment whose estimated sum is at least 1/2.  The row's
+      // maximum element has the term exp(0) = 1 exactly, estimated within a
+      // tiny relative error, so its segment's estimate is above 1/2: the
+      // maximum lies in segment gm or before.  The reference's running sum,
+      // once it has added a term, is at least that term (RN(s + e) >= e for
+      // s >= 0) and never decreases: after segment gm it is at least 1.
+      // (lane k holds round k's segments, so the highest lane with one holds gm)
+      const uint64_t cm = bal64(gc >= 0);
+      const int gm = cm != 0ull ? (int)readlane_u32((uint32_t)gc, 63 - __builtin_clzll(cm)) : -1;
       const float rin = wave_incl_scan_f32(rtot);
       const float rex = __uint_as_float(wave_shift_up1(__float_as_uint(rin)));
       const float total = __uint_as_float(lane_readlast(__float_as_uint(rin)));
@@ -767,7 +794,11 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
       if (!bad && have) {
         const float excl = rex + before_w;
         const float incl = excl + b_w;
-        const float lo = excl * (1.0f - DELTA), hi = incl * (1.0f + DELTA);
+        // the prediction's lower end, raised to 1 after the maximum's segment
+        // (a sum of 1 plus small terms would otherwise straddle 1 for the
+        // rest of the row)
+        const float lo = gm >= 0 && w + W * lane > gm ? fmaxf(excl * (1.0f - DELTA), 1.0f) : excl * (1.0f - DELTA);
+        const float hi = incl * (1.0f + DELTA);
         const int elo = (int)(__float_as_uint(lo) >> 23) - 127;
         const int ehi = (int)(__float_as_uint(hi) >> 23) - 127;
         const bool plain = lo >= 0x1p-64f && hi <= 3.0e38f && elo == ehi;
@@ -796,7 +827,7 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
       base = __builtin_amdgcn_readfirstlane(base);
       if (have) {
         const int slot = (w == 0 && lane == 0) ? 0 : base + __popcll(exm & lt_mask);
-        const bool got = ex && slot < DCAP;
+        const bool got = ex && slot < dcap;
         F.sdump[w + W * lane] = (int8_t)(got ? slot : -1);
         if (got) F.slotseg[slot] = (int16_t)(w + W * lane);
       }
@@ -953,7 +984,7 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
           batch(k0, false, k0 < KV ? to_v4(d[k0 < KV ? k0 : 0]) : lds_q(k0), lds_q(k0 + 1), lds_q(k0 + 2), lds_q(k0 + 3));
       }
       __syncthreads();
-      exact_loads<FASTLD>(F, xr, w, min(F.nslot, DCAP), n);
+      exact_loads<FASTLD>(F, xr, w, min(F.nslot, dcap), n);
       ctab[lane] = make_float4(sclo_l, schi_l, __uint_as_float(tsp_l), 0.0f);  // read by this wave only
 #pragma unroll
       for (int b = 0; b < (KV - 1) / 4; ++b) {
@@ -974,7 +1005,7 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
       // this wave's EXACT slots (slot s on wave s % W, loaded by this wave),
       // while the re-reads land; slot 0, the row's first segment, needs no
       // tables: wave 0 sums it term by term
-      for (int slot = w; slot < min(F.nslot, DCAP); slot += W) {
+      for (int slot = w; slot < min(F.nslot, dcap); slot += W) {
         slot_terms(F, Q, P, X, row, slot, n, m, theta, t1);
         if (slot != 0) slot_tables(F, slot);
       }
@@ -1072,12 +1103,12 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
             const uint64_t mk = bal64(ex);
             const int slot = cnt + __popcll(mk & lt_mask);
             if (ex) {
-              F.sdump[g] = (int8_t)(slot < DCAP ? slot : -1);
-              if (slot < DCAP) F.slotseg[slot] = (int16_t)g;
+              F.sdump[g] = (int8_t)(slot < dcap ? slot : -1);
+              if (slot < dcap) F.slotseg[slot] = (int16_t)g;
             }
             cnt += __popcll(mk);
           }
-          if (lane == 0) F.nslot = min(cnt, DCAP);
+          if (lane == 0) F.nslot = min(cnt, dcap);
         }
         __syncthreads();
         const int nslot = F.nslot;
@@ -1230,12 +1261,45 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
   // walk's results, lie past F.u): no barrier here
   static_assert(sizeof(SampleShared) <= sizeof(F.u), "the selection's memory must lie inside F.u");
   select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified, u_row, certified && pre_ok,
-             cand_pre, cand_n0, X, O, XF ? &pen_sh : nullptr, kernel_args_ptr());
+             cand_pre, cand_n0, X, O, XF ? &pen_sh : nullptr, kernel_args_ptr(), row);
   // the walk's diagnostics join the status thread 0 wrote (F.diag lies past
   // the selection's memory)
   if (t == 0 && Q.status) {
     const uint32_t d = F.diag;
     if (d != 0u) Q.status[row] |= d;
+  }
+}
+
+// One row per workgroup: launches whose rows fit the CUs at once.
+template <bool FASTLD, bool XF>
+__global__ __launch_bounds__(NT) void k_stats(KArgs A) {
+  __shared__ StatsShared U;
+  __shared__ PenShared pen_sh;  // kXfPen: the row's penalised positions
+  stats_row<FASTLD, XF>(A, (int)blockIdx.x, U, pen_sh);
+}
+
+// More rows than CUs: one workgroup per CU (all resident), each taking rows
+// [0, grid) one each and then claiming the next unclaimed row until none is
+// left, so rows of unequal cost spread over every CU.  (Launched one row per
+// workgroup instead, the hardware hands workgroups to the XCDs in turn, so a
+// batch whose cost alternates from row to row loads half of the XCDs only.)
+template <bool FASTLD, bool XF>
+__global__ __launch_bounds__(NT) void k_stats_rows(KArgs A) {
+  __shared__ StatsShared U;
+  __shared__ PenShared pen_sh;
+  __shared__ int next_row;
+  for (int row = (int)blockIdx.x;;) {
+    // the arguments through a pointer the compiler cannot see through, so
+    // that each row loads them where it uses them instead of holding them in
+    // registers across rows
+    const __attribute__((address_space(4))) KArgs* Ap =
+        (const __attribute__((address_space(4))) KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(Ap));
+    stats_row<FASTLD, XF>(*(const KArgs*)Ap, row, U, pen_sh);
+    if (threadIdx.x == 0) next_row = claim_row(A.Q.claim, A.P.epoch, A.P.grid);
+    __syncthreads();  // also: every wave is done with this row's shared memory
+    row = next_row;
+    if (row >= A.P.rows) return;
   }
 }
 
@@ -1247,7 +1311,12 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
   if (ev_begin && hipEventRecord(ev_begin, st) != hipSuccess) return hipErrorUnknown;
   const bool fastld = (P.flags & kFlagVecSrc) != 0 && (P.n % 4) == 0;
   const bool xf = P.xf_src != 0u || P.xf_orig != 0u;
-  if (fastld && !xf)
+  if (P.grid < P.rows && fastld) {
+    if (!xf)
+      hipLaunchKernelGGL((k_stats_rows<true, false>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
+    else
+      hipLaunchKernelGGL((k_stats_rows<true, true>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
+  } else if (fastld && !xf)
     hipLaunchKernelGGL((k_stats<true, false>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
   else if (fastld)
     hipLaunchKernelGGL((k_stats<true, true>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});

@@ -165,32 +165,52 @@ def test_headline_full_batch_properties(cuda):
     compare_rows(x, w.params, u, g1)
 
 
-def test_walk_rare_paths_reached(cuda):
-    """The single pass's rarer walk paths are exercised and exact: rows with
-    more EXACT segments than one round's slots, and rows with a crossing
-    beyond a segment's tabulated binades (configuration 5's peaked rows have
-    both), compared with the oracle."""
+def _run_paths(cuda, x, params, u, cap=64):
     import torch
 
-    w = WORKLOADS["c5"]
-    rows = 64
-    x = w.logits(rows)
-    u = llz.rng_uniforms(w.uniform_seed, rows)
-    cfg = llz.SamplerConfig.of(w.params)
-    res = llz.sample_rows(torch.from_numpy(x).to(cuda), cfg, torch.from_numpy(u).to(cuda), kept_cap=64,
-                          stats=True, path=True)
+    cfg = llz.SamplerConfig.of(params)
+    res = llz.sample_rows(torch.from_numpy(np.ascontiguousarray(x)).to(cuda), cfg,
+                          torch.from_numpy(np.ascontiguousarray(u, dtype=np.float32)).to(cuda),
+                          kept_cap=cap, stats=True, path=True)
     torch.cuda.synchronize()
-    paths = res.row_path.cpu().numpy().view(np.uint32)
-    rounds = np.flatnonzero(paths & llz.PATH_WALK_ROUNDS)
+    out = dict(tokens=res.tokens.cpu().numpy().view(np.uint32), consumed=res.consumed.cpu().numpy(),
+               kept_count=res.kept_count.cpu().numpy().view(np.uint32),
+               kept_ids=res.kept_ids.cpu().numpy().view(np.uint32), kept_probs=res.kept_probs.cpu().numpy(),
+               stats=res.row_stats.cpu().numpy(), cap=cap)
+    return res.row_path.cpu().numpy().view(np.uint32), out
+
+
+def test_walk_rare_paths_reached(cuda):
+    """The single pass's rarer walk paths are exercised and exact:
+    - later rounds of EXACT slots: rows whose running sum sits just above 1/2
+      (one early term of e = 1/2, then terms far below the grid) for most of
+      the row, so that every segment's prediction straddles the binade
+      boundary and is EXACT (far more than one round's 48 slots);
+    - a crossing beyond a segment's tabulated binades: configuration 5's
+      peaked rows, whose dominant token lifts the sum across about 20
+      binades inside one segment.
+    Those rows are compared with the oracle."""
+    n, rows = 128256, 4
+    g = np.random.default_rng(41)
+    x = g.normal(-20.0, 1.0, (rows, n)).astype(np.float32)
+    for r in range(rows):
+        x[r, 10 + 97 * r] = np.float32(-0.6931472)  # e = exp(v - max) = 1/2
+        x[r, n - 1 - 311 * r] = 0.0                 # the row maximum, late in the row
+    params = Params(temperature=1.0, top_k=40, top_p=0.95, min_p=0.0, repetition_penalty=1.0)
+    u = llz.rng_uniforms(9, rows)
+    paths, out = _run_paths(cuda, x, params, u)
+    assert np.all(paths & llz.PATH_WALK_ROUNDS), f"rows without later rounds: {paths}"
+    assert not np.any(paths & llz.PATH_STREAM_NORM), f"rows left the single pass: {paths}"
+    compare_rows(x, params, u, out)
+
+    w = WORKLOADS["c5"]
+    x = w.logits(32)
+    u = llz.rng_uniforms(w.uniform_seed, 32)
+    paths, out = _run_paths(cuda, x, w.params, u)
     generic = np.flatnonzero(paths & llz.PATH_RESOLVE_GENERIC)
-    assert rounds.size > 0, "no row needed a second round of EXACT slots"
-    assert generic.size > 0, "no row reached resolve_generic"
-    assert not np.any(paths[np.union1d(rounds, generic)] & llz.PATH_STREAM_NORM)
-    g = dict(tokens=res.tokens.cpu().numpy().view(np.uint32), consumed=res.consumed.cpu().numpy(),
-             kept_count=res.kept_count.cpu().numpy().view(np.uint32),
-             kept_ids=res.kept_ids.cpu().numpy().view(np.uint32), kept_probs=res.kept_probs.cpu().numpy(),
-             stats=res.row_stats.cpu().numpy(), cap=64)
-    compare_rows(x, w.params, u, g, rows=np.union1d(rounds[:8], generic[:8]))
+    assert generic.size > 0, f"no row reached resolve_generic: {paths}"
+    assert not np.any(paths & llz.PATH_STREAM_NORM), f"rows left the single pass: {paths}"
+    compare_rows(x, w.params, u, out, rows=generic[:8])
 
 
 # ---------------------------------------------------------------------------
