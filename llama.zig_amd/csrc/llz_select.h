@@ -469,6 +469,41 @@ __device__ int prefix_filters(const List& L, int M, float p_nc, int n, const Row
   return K > M ? -1 : K;
 }
 
+// A row read tile by tile, eight logits per thread (thread t holds positions
+// t*8 .. t*8+7 of a 4096-logit tile), with the next tile's loads issued
+// before the current tile's work.  With 16-byte loads every thread loads
+// from min(pos, nlast) (the last start that stays inside the row), so no
+// branch separates a tile's loads from the work they overlap; the one
+// thread whose span crosses the row's end re-reads its logits where they are
+// used (fix_tail).  Positions past the row read as 0.
+struct RowTiles8 {
+  static constexpr int V = 8;
+  const float* xs;
+  int n;
+  bool vec8;
+  int nlast;
+  __device__ RowTiles8(const float* x, int n_, bool vec) : xs(x), n(n_), vec8(vec && n_ >= V),
+                                                          nlast(vec && n_ >= V ? ((n_ - V) & ~3) : 0) {}
+  __device__ __forceinline__ void load(int pos, float (&r)[V]) const {
+    if (vec8) {
+      const int pc = min(pos, nlast);
+      const float4 q0 = *reinterpret_cast<const float4*>(xs + pc);
+      const float4 q1 = *reinterpret_cast<const float4*>(xs + pc + 4);
+      r[0] = q0.x; r[1] = q0.y; r[2] = q0.z; r[3] = q0.w;
+      r[4] = q1.x; r[5] = q1.y; r[6] = q1.z; r[7] = q1.w;
+    } else {
+#pragma unroll
+      for (int k = 0; k < V; ++k) r[k] = pos + k < n ? xs[pos + k] : 0.0f;
+    }
+  }
+  __device__ __forceinline__ void fix_tail(int pos, float (&r)[V]) const {
+    if (vec8 && pos > nlast && pos < n) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) r[k] = pos + k < n ? xs[pos + k] : 0.0f;
+    }
+  }
+};
+
 // Entropy sum over the whole row in index order (sampler.zig:129-132):
 // entropy -= p * log(p) for every p = RN(e / S) > 0, which is the exact
 // sequential sum of the terms t = -RN(p * log(p)) >= 0 (a - b == a + (-b)).
@@ -519,33 +554,9 @@ __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float 
   const bool vec = (flags & kFlagVecSrc) != 0;
   const float rS = 1.0f / S;
   const int t = (int)threadIdx.x;
-  const float* __restrict__ xs = X.x;
 
-  // Loads of a thread's EV logits from pos.  With 16-byte loads, every
-  // thread loads from min(pos, nlast) (the last start that stays inside the
-  // row), so no branch separates a tile's loads from the work they overlap;
-  // the one thread whose span crosses the row's end re-reads its logits
-  // where they are used (fix_tail).
-  const bool vec8 = vec && n >= EV;
-  const int nlast = vec8 ? ((n - EV) & ~3) : 0;
-  auto load_raw = [&](int pos, float (&r)[EV]) {
-    if (vec8) {
-      const int pc = min(pos, nlast);
-      const float4 q0 = *reinterpret_cast<const float4*>(xs + pc);
-      const float4 q1 = *reinterpret_cast<const float4*>(xs + pc + 4);
-      r[0] = q0.x; r[1] = q0.y; r[2] = q0.z; r[3] = q0.w;
-      r[4] = q1.x; r[5] = q1.y; r[6] = q1.z; r[7] = q1.w;
-    } else {
-#pragma unroll
-      for (int k = 0; k < EV; ++k) r[k] = pos + k < n ? xs[pos + k] : 0.0f;
-    }
-  };
-  auto fix_tail = [&](int pos, float (&r)[EV]) {
-    if (vec8 && pos > nlast && pos < n) {
-#pragma unroll
-      for (int k = 0; k < EV; ++k) r[k] = pos + k < n ? xs[pos + k] : 0.0f;
-    }
-  };
+  const RowTiles8 rt(X.x, n, vec);
+  static_assert(RowTiles8::V == EV, "eight logits per thread");
   // sampler.zig:85 and :131 on one argument x; the term is +0 when p == 0
   auto exact_term = [&](float x) {
     const float p = exp_f32(x) / S;
@@ -553,8 +564,8 @@ __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float 
   };
 
   float raw[EV];
-  load_raw(t * EV, raw);
-  fix_tail(t * EV, raw);
+  rt.load(t * EV, raw);
+  rt.fix_tail(t * EV, raw);
   float H = 0.0f;
   {
     uint32_t unused = 0;
@@ -575,7 +586,7 @@ __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float 
 
   for (int base = 0; base < n; base += ET) {
     const int pos = base + t * EV;
-    if (base > 0) fix_tail(pos, raw);
+    if (base > 0) rt.fix_tail(pos, raw);
     float xa[EV];
 #pragma unroll
     for (int k = 0; k < EV; ++k) {
@@ -583,7 +594,7 @@ __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float 
       if (!t1) a = a / T;
       xa[k] = a;  // the reference's argument
     }
-    if (base + ET < n) load_raw(pos + ET, raw);  // the next tile's loads fly during this one
+    if (base + ET < n) rt.load(pos + ET, raw);  // the next tile's loads fly during this one
 
     float tl[EV], te[EV];
     uint32_t mid = 0, tiny = 0, have = 0;
@@ -1255,22 +1266,34 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
   const bool lazy_p = typical && !filters && n >= 2;
   const GlobalList GL{Ak, Av};
   if (!lazy_p) {
-    for (int base = 0; base < n; base += kTile) {
-      float v[kV];
-      const int pos = base + t * kV;
-      X.load4(pos, n, vec, v);
+    // (~p bits, id) in index order, the next tile's loads in flight; the
+    // smallest key lets the sort skip the digits every key shares
+    constexpr int TV = RowTiles8::V;
+    const RowTiles8 rt(X.x, n, vec);
+    float raw[TV];
+    rt.load(t * TV, raw);
+    uint32_t kmin = 0xffffffffu;
+    for (int base = 0; base < n; base += kNT * TV) {
+      const int pos = base + t * TV;
+      if (base > 0) rt.fix_tail(pos, raw);
+      float v[TV];
 #pragma unroll
-      for (int k = 0; k < kV; ++k) {
+      for (int k = 0; k < TV; ++k) v[k] = pos + k < n ? X.fix(pos + k, raw[k]) : 0.0f;
+      if (base + kNT * TV < n) rt.load(pos + kNT * TV, raw);
+#pragma unroll
+      for (int k = 0; k < TV; ++k) {
         if (pos + k < n) {
-          const float p = row_exp(v[k], m, P.temperature, t1) / S;
-          Ak[pos + k] = ~__float_as_uint(p);
+          const uint32_t key = ~__float_as_uint(row_exp(v[k], m, P.temperature, t1) / S);
+          kmin = min(kmin, key);
+          Ak[pos + k] = key;
           Av[pos + k] = (uint32_t)(pos + k);
         }
       }
     }
+    kmin = wg_min_u32<kNT>(kmin, sh.wg, bank);
     __threadfence();
     __syncthreads();
-    wg_radix_sort_pairs<kNT>(Ak, Av, Bk, Bv, n, sh.u.post.radix);
+    wg_radix_sort_pairs<kNT>(Ak, Av, Bk, Bv, n, sh.u.post.radix, kmin);
     __threadfence();
     __syncthreads();
     K = prefix_filters(GL, n, kInf, n, P, S, sh, bank);  // M = n: never -1

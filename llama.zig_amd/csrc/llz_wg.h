@@ -184,9 +184,11 @@ __device__ void lds_bitonic_sort_u64(uint64_t* a, int n) {
 // global memory, by one workgroup.  (k0, v0) is the input and the output;
 // (k1, v1) is the ping-pong buffer.  Equal keys keep input order.
 //
-// One read of the keys counts the digits of all four passes; a pass whose
-// digit is the same for every key moves nothing and is skipped (it would
-// keep the order).  A pass handles tiles of kRadixRounds * NT elements:
+// The digits are those of key - kbase (kbase: at most the smallest key, so
+// that the order is the keys' own): keys that span few values then share
+// their high digits.  One read of the keys counts the digits of all four
+// passes; a pass whose digit is the same for every key moves nothing and is
+// skipped (it would keep the order).  A pass handles tiles of kRadixRounds * NT elements:
 // round r of a tile holds elements tile + r NT + t, so (round, wave, lane)
 // order is input order.  Each round ranks its elements within their wave
 // (lanes with the same digit found by eight ballots), the counts of every
@@ -209,7 +211,7 @@ struct RadixScratch {
 
 template <int NT>
 __device__ void wg_radix_sort_pairs(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, int n,
-                                    RadixScratch& rs) {
+                                    RadixScratch& rs, uint32_t kbase = 0u) {
   static_assert(NT % kWave == 0 && NT / kWave <= 8 && NT >= 256 && NT <= 512, "radix sort layout");
   static_assert(kRadixRounds * 512 <= 65536, "tile places fit 16 bits");
   constexpr int W = NT / kWave;
@@ -225,7 +227,7 @@ __device__ void wg_radix_sort_pairs(uint32_t* k0, uint32_t* v0, uint32_t* k1, ui
   for (int d = t; d < 4 * 256; d += NT) (&rs.hist[0][0])[d] = 0;
   __syncthreads();
   for (int i = t; i < n; i += NT) {
-    const uint32_t key = k0[i];
+    const uint32_t key = k0[i] - kbase;
     atomicAdd(&rs.hist[0][key & 255u], 1u);
     atomicAdd(&rs.hist[1][(key >> 8) & 255u], 1u);
     atomicAdd(&rs.hist[2][(key >> 16) & 255u], 1u);
@@ -289,7 +291,7 @@ __device__ void wg_radix_sort_pairs(uint32_t* k0, uint32_t* v0, uint32_t* k1, ui
       lds_barrier();
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        dig[r] = (key[r] >> shift) & 255u;
+        dig[r] = ((key[r] - kbase) >> shift) & 255u;
         // lanes of this wave with the same digit
         uint64_t peers = bal64(valid[r]);
 #pragma unroll
@@ -341,7 +343,7 @@ __device__ void wg_radix_sort_pairs(uint32_t* k0, uint32_t* v0, uint32_t* k1, ui
       // write it out in that order: runs of consecutive addresses per digit
       for (int i = t; i < tn; i += NT) {
         const uint32_t k = rs.stage_k[i];
-        const int32_t off = rs.delta[(k >> shift) & 255u] + i;
+        const int32_t off = rs.delta[((k - kbase) >> shift) & 255u] + i;
         dst_k[off] = k;
         dst_v[off] = rs.stage_v[i];
       }
