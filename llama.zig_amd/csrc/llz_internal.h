@@ -34,6 +34,25 @@ constexpr uint32_t kPathWalkRounds = 16u;    // diagnostic: the walk took more t
 constexpr uint32_t kPathResolveGeneric = 32u;  // diagnostic: an event beyond a segment's tabulated grids
 constexpr uint32_t kPathError = 0x80000000u;
 
+// Phase timestamps (measurement builds only, -DLLZ_PHASE_STAMPS): thread 0
+// of a row's workgroup records s_memrealtime (100 MHz) at the boundaries of
+// the kernel's phases, slot k of row r at llz_phase_stamps[r * kStampSlots +
+// k].  In ordinary builds LLZ_STAMP compiles to nothing.
+constexpr int kStampRows = 4096;
+constexpr int kStampSlots = 32;
+#ifdef LLZ_PHASE_STAMPS
+static __device__ unsigned long long llz_phase_stamps[kStampRows * kStampSlots];  // read by llz_stats.hip's copy-out
+#define LLZ_STAMP(row, k)                                                                     \
+  do {                                                                                        \
+    if (threadIdx.x == 0 && (row) < ::llz::kStampRows)                                        \
+      ::llz::llz_phase_stamps[(row) * ::llz::kStampSlots + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define LLZ_STAMP(row, k) \
+  do {                    \
+  } while (0)
+#endif
+
 struct RowParams {
   float temperature;
   float top_p;

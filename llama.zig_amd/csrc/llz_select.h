@@ -535,6 +535,7 @@ struct RowTiles8 {
 // Out of line, so that the kernel's common path does not carry its
 // registers; the row's parameters come by value (a reference would make the
 // kernel store them to its stack).
+
 struct EntropyResult {
   float H;
   int bank;
@@ -869,6 +870,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   if (uncertified) {
     // the streaming normaliser (sampler.zig:83-88) fills the candidate list in LDS
     const NormResult r = select_norm_fallback<Src>(A, row, pen, sh, bank, m);
+    LLZ_STAMP(row, 7);
     S = r.S;
     m = r.m;
     bank = r.bank;
@@ -988,6 +990,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
         H = er.H;
         bank = er.bank;
       }
+      LLZ_STAMP(row, 12);
       const int ksort = next_pow2(K);
       for (int q = t; q < ksort; q += kNT) {
         if (q < K) {
@@ -1249,6 +1252,7 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
     }
     return;
   }
+  LLZ_STAMP(row, 8);
   const int64_t fo = (int64_t)slot * n;
   const int64_t fs = (int64_t)P.fb_slots * n;
   uint32_t* Ak = Q.fb + 0 * fs + fo;
@@ -1275,7 +1279,7 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
     uint32_t kmin = 0xffffffffu;
     for (int base = 0; base < n; base += kNT * TV) {
       const int pos = base + t * TV;
-      if (base > 0) rt.fix_tail(pos, raw);
+      rt.fix_tail(pos, raw);  // also in the first tile: a span crossing the row's end
       float v[TV];
 #pragma unroll
       for (int k = 0; k < TV; ++k) v[k] = pos + k < n ? X.fix(pos + k, raw[k]) : 0.0f;
@@ -1293,10 +1297,13 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
     kmin = wg_min_u32<kNT>(kmin, sh.wg, bank);
     __threadfence();
     __syncthreads();
+    LLZ_STAMP(row, 9);
     wg_radix_sort_pairs<kNT>(Ak, Av, Bk, Bv, n, sh.u.post.radix, kmin);
     __threadfence();
     __syncthreads();
+    LLZ_STAMP(row, 10);
     K = prefix_filters(GL, n, kInf, n, P, S, sh, bank);  // M = n: never -1
+    LLZ_STAMP(row, 11);
     if (K < 0) K = 0;
   } else {
     K = n;
@@ -1338,9 +1345,11 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
       H = er.H;
       bank = er.bank;
     }
+    LLZ_STAMP(row, 12);
     const uint32_t keyK = K < n ? Ak[K - 1] : 0u;
     const uint32_t idK = K < n ? Av[K - 1] : 0u;
     const TypicalHead th = typical_head<Src>(X, n, m, S, H, P, K, keyK, idK, Bk, Bv, Ck, Cv, sh, bank);
+    LLZ_STAMP(row, 13);
     // the cut: the first element of the typical order that is not kept
     const bool cut = th.st >= 0;
     const uint32_t dkc = cut ? Ck[th.st] : 0u, idc = cut ? Cv[th.st] : 0u;
@@ -1403,6 +1412,7 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
   // call's epoch takes)
   __threadfence();
   __syncthreads();
+  LLZ_STAMP(row, 14);
   if (t == 0) atomicExch(&Q.fb_owner[slot], P.epoch ^ (1ull << 63));
 }
 

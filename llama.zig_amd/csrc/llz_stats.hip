@@ -21,6 +21,7 @@ namespace {
 
 using namespace fastp;
 constexpr float kInfS = __builtin_inff();
+constexpr int kScanDepth = 8;  // rows beyond the single pass: float4 loads in flight per thread in the max scan
 
 
 
@@ -92,14 +93,17 @@ __device__ __forceinline__ void push_cand(FastShared& F, const RowPtrs& Q, int r
   if (slot < (uint32_t)kCandCap) Q.cand[(int64_t)row * kCandCap + slot] = ((uint64_t)__float_as_uint(e) << 32) | id;
 }
 
-// EXACT slots are spread over the waves in turn: slot s to wave s % W.
-// Slot 0 is the row's first segment in the first round.
+// EXACT slots per wave: slot 0 on wave 0 alone, slots 1.. on waves 1 .. W-1
+// in turn (slot s on wave 1 + (s - 1) % (W - 1)).  Slot 0 is the row's first
+// segment in the first round, which wave 0 then sums term by term; the other
+// waves take the slots that need tables.  Wave w's slots: w, w + slot_step(w), ...
+__device__ __forceinline__ int slot_step(int w) { return w == 0 ? DCAP : W - 1; }
 
 // Issue the re-reads of this wave's EXACT slots into their dump areas (the
 // caller waits for them).
 template <bool FASTLD>
 __device__ __forceinline__ void exact_loads(FastShared& F, const float* xr, int w, int nslot, int n) {
-  for (int slot = w; slot < nslot; slot += W) seg_to_lds(xr, F.slotseg[slot], n, FASTLD, &F.u.x.dump[slot][0]);
+  for (int slot = w; slot < nslot; slot += slot_step(w)) seg_to_lds(xr, F.slotseg[slot], n, FASTLD, &F.u.x.dump[slot][0]);
 }
 
 // The exact terms of four consecutive positions (sampler.zig:85), without
@@ -190,11 +194,11 @@ __device__ __forceinline__ void slot_tables(FastShared& F, int slot) {
 }
 
 // Rounds after the first: the terms and tables of this wave's slots (slot s
-// on wave s % W, all loaded by this wave and waited for).
+// on its wave (slot_step), all loaded by this wave and waited for).
 template <class Src>
 __device__ __forceinline__ void exact_segments(FastShared& F, const RowPtrs& Q, const RowParams& P, const Src& X,
                                                int row, int w, int nslot, int n, float m, float theta, bool t1) {
-  for (int slot = w; slot < nslot; slot += W) {
+  for (int slot = w; slot < nslot; slot += slot_step(w)) {
     slot_terms(F, Q, P, X, row, slot, n, m, theta, t1);
     slot_tables(F, slot);
   }
@@ -519,6 +523,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   const RowPtrs Q = A.Q;
   constexpr int dcap = DCAP;  // EXACT slots per round
   FastShared& F = U.fast;
+  LLZ_STAMP(row, 0);
   const int t = (int)threadIdx.x, lane = lane_id();
   const int w = __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform: scalar registers
   const int n = P.n;
@@ -680,10 +685,26 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   }
   if (lane < nseg_w) F.v.aseg[w + W * lane] = my_a;
   if (!fits) {  // rows the fast path does not take: maximum and NaN scan only
-    for (int i = t; i < n; i += NT) {
-      const float v = X.at(i);
-      mx = fmaxf(mx, v);
-      nanf |= (uint32_t)(v != v);
+    if constexpr (FASTLD) {
+      // kScanDepth float4 loads per thread in flight (64 KB per workgroup)
+      constexpr int U = kScanDepth;
+      for (int b = t * 4; b < n; b += NT * 4 * U) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = ld4(xr, b + u * (NT * 4), n);  // absent: -inf
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float4 f = X.fix4(b + u * (NT * 4), v[u], n);
+          mx = fmaxf(mx, max4(f));  // fmaxf skips NaN, as the scalar loop did
+          nanf |= (uint32_t)((f.x != f.x) | (f.y != f.y) | (f.z != f.z) | (f.w != f.w));
+        }
+      }
+    } else {
+      for (int i = t; i < n; i += NT) {
+        const float v = X.at(i);
+        mx = fmaxf(mx, v);
+        nanf |= (uint32_t)(v != v);
+      }
     }
   }
   mx = wave_max_f32(mx);
@@ -705,6 +726,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     F.diag = 0;
   }
   __syncthreads();
+  LLZ_STAMP(row, 1);
 
   // ---- phase M: row maximum, scale factors, binade prediction, first slots
   float m = -kInfS;
@@ -833,6 +855,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       }
     }
     __syncthreads();
+    LLZ_STAMP(row, 2);
     const bool flood = F.flood != 0u;
     const float theta = flood ? kInfS : P.cand_theta;
 
@@ -984,6 +1007,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
           batch(k0, false, k0 < KV ? to_v4(d[k0 < KV ? k0 : 0]) : lds_q(k0), lds_q(k0 + 1), lds_q(k0 + 2), lds_q(k0 + 3));
       }
       __syncthreads();
+      LLZ_STAMP(row, 22);
       exact_loads<FASTLD>(F, xr, w, min(F.nslot, dcap), n);
       ctab[lane] = make_float4(sclo_l, schi_l, __uint_as_float(tsp_l), 0.0f);  // read by this wave only
 #pragma unroll
@@ -994,21 +1018,24 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       ccnt = lane == qch ? qn : ccnt;  // the last chunk's entries
       if (qovf && lane == 0) atomicOr(&F.fail, 1u);
     }
+    LLZ_STAMP(row, 3);
 
     // ---- phase F+X: this round's EXACT slots (re-read during phase S) and
     // the remaining specials, whose re-reads land while the slots are
     // evaluated
     if (!F.fail) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the EXACT slots' re-reads (and phase S's stores)
+      LLZ_STAMP(row, 16);
       const int qn0 = (int)readlane_u32(ccnt, 0);
       reread(qn0);
-      // this wave's EXACT slots (slot s on wave s % W, loaded by this wave),
+      // this wave's EXACT slots (slot_step: slot 0 alone on wave 0, loaded by this wave),
       // while the re-reads land; slot 0, the row's first segment, needs no
       // tables: wave 0 sums it term by term
-      for (int slot = w; slot < min(F.nslot, dcap); slot += W) {
+      for (int slot = w; slot < min(F.nslot, dcap); slot += slot_step(w)) {
         slot_terms(F, Q, P, X, row, slot, n, m, theta, t1);
         if (slot != 0) slot_tables(F, slot);
       }
+      LLZ_STAMP(row, 17);
       if (w == 0) {
         // the row's first segment (slot 0) from 0, term by term as
         // sampler.zig:87 adds them: four chains of 64 terms, one term per
@@ -1024,7 +1051,9 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
           F.next_e = 1;
         }
       }
+      LLZ_STAMP(row, 18);
       settle(qn0);
+      LLZ_STAMP(row, 19);
       // the chunks past the LDS queue (rare)
       for (int c = 1; c <= qch; ++c) {
         const int cn = (int)readlane_u32(ccnt, c);
@@ -1034,6 +1063,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       }
     }
     __syncthreads();
+    LLZ_STAMP(row, 4);
 
     // ---- phase B: the walk's entries, built in parallel (wave c takes
     // segments 64c .. 64c + 63, one per lane): a run of PLAIN segments on one
@@ -1082,6 +1112,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       if (t == 0) F.ne = ne;
     }
     __syncthreads();
+    LLZ_STAMP(row, 5);
 
     // waves 1.. read the candidate list while wave 0 walks, one entry per
     // thread from thread 64 on (entries a later round collects are read at
@@ -1091,6 +1122,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       cand_pre = Q.cand[(int64_t)row * kCandCap + (t - kWave)];
     // ---- phase C: the walk over the entries in index order (wave 0); EXACT
     // segments beyond the slots in further rounds
+    LLZ_STAMP(row, 20);
     for (int round = 0; !F.fail; ++round) {
       if (round > 0) {
         if (t == 0) F.diag |= kPathWalkRounds;
@@ -1237,6 +1269,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
           }
           e = held + last + 1;
         }
+        LLZ_STAMP(row, 21);
         if (lane == 0) {
           F.s_run = __uint_as_float(grid_bits(N, jc));
           F.next_e = e;
@@ -1249,6 +1282,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     }
 
     // ---- hand-over to the selection stage
+    LLZ_STAMP(row, 6);
     certified = F.fail == 0u;
     S = F.s_run;
     cc = flood ? (uint32_t)kCandCap + 1u : F.ncand;
@@ -1262,6 +1296,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   static_assert(sizeof(SampleShared) <= sizeof(F.u), "the selection's memory must lie inside F.u");
   select_row(P, Q, U.select, m, certified ? S : 0.0f, certified ? cc : 0u, !certified, u_row, certified && pre_ok,
              cand_pre, cand_n0, X, O, XF ? &pen_sh : nullptr, kernel_args_ptr(), row);
+  LLZ_STAMP(row, 15);
   // the walk's diagnostics join the status thread 0 wrote (F.diag lies past
   // the selection's memory)
   if (t == 0 && Q.status) {
@@ -1331,3 +1366,17 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
 }
 
 }  // namespace llz
+
+#ifdef LLZ_PHASE_STAMPS
+// Measurement builds: the phase timestamps of rows 0 .. rows - 1 (kStampSlots
+// per row, 0 where a row did not reach the boundary) into dst.
+extern "C" int llz_debug_phase_stamps(unsigned long long* dst, int rows, int clear) {
+  if (rows <= 0 || rows > llz::kStampRows || !dst) return -1;
+  const size_t bytes = (size_t)rows * llz::kStampSlots * sizeof(unsigned long long);
+  if (clear) {
+    static unsigned long long zeros[llz::kStampRows * llz::kStampSlots];
+    return hipMemcpyToSymbol(HIP_SYMBOL(llz::llz_phase_stamps), zeros, sizeof(zeros)) == hipSuccess ? 0 : -3;
+  }
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(llz::llz_phase_stamps), bytes) == hipSuccess ? 0 : -3;
+}
+#endif

@@ -23,7 +23,9 @@ from typing import Optional, Tuple
 import numpy as np
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_DIR, "libllzsample.so")
+# LLZ_LIBRARY selects another build of the same library (the phase-stamp
+# measurement build, libllzsample_stamp.so); by default the product build.
+LIB_PATH = os.environ.get("LLZ_LIBRARY") or os.path.join(PKG_DIR, "libllzsample.so")
 
 LLZ_OK = 0
 LLZ_E_INVALID_ARG = -1

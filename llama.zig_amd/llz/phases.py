@@ -1,0 +1,97 @@
+"""Phase timings of the fused sampling kernel, per row, from the measurement
+build (libllzsample_stamp.so: ``make -C llama.zig_amd stamp``).
+
+Thread 0 of each row's workgroup records s_memrealtime (100 MHz, 10 ns) at
+the phase boundaries; this script runs a workload a few times through that
+build and prints, per phase, the median and the largest duration over the
+rows that reached both of its boundaries, in microseconds.
+
+    python llama.zig_amd/llz/phases.py --workload headline [--rows R] [--reps K]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+STAMP_LIB = os.path.join(PKG, "libllzsample_stamp.so")
+
+# slot -> boundary (slots as the kernel writes them)
+SLOTS = {
+    0: "start", 1: "L end", 2: "M end", 3: "S end", 4: "F+X end", 5: "B end", 6: "C end (walk)",
+    7: "streaming normaliser end", 8: "full row: buffers claimed", 9: "full row: keys written",
+    10: "full row: sorted", 11: "full row: prefix filters", 12: "entropy end", 13: "typical head end",
+    14: "full row end", 15: "row end",
+    16: "F+X: re-reads landed (wave 0)", 17: "F+X: slots done (wave 0)", 18: "F+X: first segment summed (wave 0)",
+    19: "F+X: specials settled (wave 0)", 20: "C: walk start", 21: "C: walk done (wave 0)",
+    22: "S: LDS-resident batches done",
+}
+# phases as (name, from slot, to slot)
+PHASES = [
+    ("L (loads)", 0, 1), ("M", 1, 2), ("S", 2, 3), ("F+X", 3, 4), ("B", 4, 5), ("C (walk)", 5, 6),
+    ("selection (single pass)", 6, 15), ("streaming normaliser", 6, 7),
+    ("full row: claim", 7, 8), ("full row: keys", 8, 9), ("full row: sort", 9, 10),
+    ("full row: prefix filters", 10, 11), ("entropy pass", 11, 12), ("entropy pass (after short list)", 6, 12),
+    ("typical head", 12, 13), ("full row: rest", 13, 14), ("whole row", 0, 15),
+    ("S: LDS-resident batches", 2, 22), ("S: register batches", 22, 3),
+    ("F+X: wait for re-reads (w0)", 3, 16), ("F+X: slots (w0)", 16, 17), ("F+X: first segment (w0)", 17, 18),
+    ("F+X: settle (w0)", 18, 19), ("F+X: barrier wait (w0)", 19, 4), ("C: candidate reads", 5, 20),
+    ("C: walk (w0)", 20, 21), ("C: after walk", 21, 6),
+]
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--workload", default="headline")
+    ap.add_argument("--rows", type=int, default=0, help="rows (default: the workload's batch)")
+    ap.add_argument("--reps", type=int, default=3)
+    a = ap.parse_args()
+    os.environ["LLZ_LIBRARY"] = STAMP_LIB
+    sys.path.insert(0, PKG)
+    import numpy as np
+    import torch
+
+    import llz
+    from llz.workloads import WORKLOADS
+
+    w = WORKLOADS[a.workload]
+    rows = a.rows or w.rows
+    L = llz.library()
+    L.llz_debug_phase_stamps.argtypes = [C.c_void_p, C.c_int, C.c_int]
+    L.llz_debug_phase_stamps.restype = C.c_int
+    rows_st = min(rows, 4096)
+    buf = np.zeros((rows_st, 32), np.uint64)
+    x = torch.from_numpy(w.logits(rows)).cuda()
+    u = torch.from_numpy(llz.rng_uniforms(w.uniform_seed, rows)).cuda()
+    cfg = llz.SamplerConfig.of(w.params)
+    res = None
+    for _ in range(a.reps):
+        assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 1) == 0
+        torch.cuda.synchronize()
+        res = llz.sample_rows(x, cfg, u, path=True)
+        torch.cuda.synchronize()
+    assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 0) == 0
+    paths = res.row_path.cpu().numpy()
+    st = buf.astype(np.int64)
+    t0 = st[:, 0][st[:, 0] > 0].min()
+    out = {"workload": w.name, "rows": rows, "paths": {int(k): int(v) for k, v in zip(*np.unique(paths, return_counts=True))},
+           "phases_us": {}}
+    for name, f, to in PHASES:
+        ok = (st[:, f] > 0) & (st[:, to] > 0)
+        if not ok.any():
+            continue
+        d = (st[ok, to] - st[ok, f]) / 100.0  # 100 MHz ticks -> us
+        out["phases_us"][name] = {"rows": int(ok.sum()), "median": round(float(np.median(d)), 2),
+                                  "max": round(float(d.max()), 2)}
+    end = st[:, 15][st[:, 15] > 0]
+    out["kernel_span_us"] = round(float((end.max() - t0) / 100.0), 2)
+    print(json.dumps(out, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
