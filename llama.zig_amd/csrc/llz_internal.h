@@ -32,6 +32,7 @@ constexpr uint32_t kPathFallback = 4u;      // full-row radix sort
 constexpr uint32_t kPathNormFallback = 8u;  // streaming normaliser (row not certified by the fast path)
 constexpr uint32_t kPathWalkRounds = 16u;    // diagnostic: the walk took more than one round of EXACT slots
 constexpr uint32_t kPathResolveGeneric = 32u;  // diagnostic: an event beyond a segment's tabulated grids
+constexpr uint32_t kPathBuckets = 64u;        // full row without a sort: kept prefix, total and draw by p-key buckets
 constexpr uint32_t kPathError = 0x80000000u;
 
 // Phase timestamps (measurement builds only, -DLLZ_PHASE_STAMPS): thread 0

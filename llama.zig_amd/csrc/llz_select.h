@@ -5,6 +5,7 @@
 #pragma once
 
 #include "llz_accum.h"
+#include "llz_bucket.h"
 #include "llz_rowops.h"
 
 namespace llz {
@@ -25,6 +26,7 @@ struct SampleShared {
   union {
     NormShared<kNT> norm;   // streaming normaliser (rows k_stats could not certify)
     PostShared post;        // sort, filters and draw
+    BucketShared bkt;       // long kept prefixes without typical-p (llz_bucket.h)
   } u;
 };
 
@@ -1198,6 +1200,200 @@ __device__ TypicalHead typical_head(const Src& X, int n, float m, float S, float
   return r;
 }
 
+// Top-k / top-p / min-p, the total and the draw by buckets (llz_bucket.h)
+// for a row without typical-p whose kept prefix overflowed the candidate
+// list.  Ak: the row's key buffer (n words).  Returns false when the row
+// needs the sorting path (nothing is written then but Ak).
+template <class Src>
+__device__ bool select_buckets(const Src& X, int n, float m, float S, float u, const RowParams& P, uint32_t* Ak,
+                               SampleShared& sh, int& bank, BucketResult& res) {
+  BucketShared& bs = sh.u.bkt;
+  const int t = (int)threadIdx.x;
+  const bool t1 = (P.flags & kFlagTIsOne) != 0;
+  const bool vec = (P.flags & kFlagVecSrc) != 0;
+  const bool topp = P.top_p > 0.0f && P.top_p < 1.0f;
+  const uint32_t Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? P.top_k : (uint32_t)n;
+  // probs[indices[0]] is the maximum's, whose e is exp(0) = 1 (sampler.zig:121)
+  const float p0 = 1.0f / S;
+  const float thr_m = p0 * P.min_p;
+  const uint32_t kmin = ~__float_as_uint(p0);  // every key is at least this
+  const double D = kBucketDelta;
+
+  // ---- A: the exact p of every element (sampler.zig:85, :90), its key, and
+  // the coarse histogram
+  for (int b = t; b < kNB; b += kNT) {
+    bs.cnt[b] = 0u;
+    bs.mass[b] = 0.0f;
+  }
+  lds_barrier();
+  uint32_t km = 0, fk = 0xffffffffu, fid = 0xffffffffu;
+  {
+    constexpr int TV = RowTiles8::V;
+    const RowTiles8 rt(X.x, n, vec);
+    float raw[TV];
+    rt.load(t * TV, raw);
+    for (int base = 0; base < n; base += kNT * TV) {
+      const int pos = base + t * TV;
+      rt.fix_tail(pos, raw);
+      float v[TV];
+#pragma unroll
+      for (int k = 0; k < TV; ++k) v[k] = pos + k < n ? X.fix(pos + k, raw[k]) : 0.0f;
+      if (base + kNT * TV < n) rt.load(pos + kNT * TV, raw);
+      uint32_t key[TV];
+#pragma unroll
+      for (int k = 0; k < TV; ++k) {
+        const float p = row_exp(v[k], m, P.temperature, t1) / S;
+        const bool in = pos + k < n;
+        key[k] = in ? ~__float_as_uint(p) : 0xffffffffu;
+        if (in) {
+          km += p >= thr_m ? 1u : 0u;
+          if (key[k] < fk) {  // positions ascend within a thread: the first of equal keys stays
+            fk = key[k];
+            fid = (uint32_t)(pos + k);
+          }
+          const uint32_t cb = min((key[k] - kmin) >> kCoarseShift, (uint32_t)kNB - 1u);
+          atomicAdd(&bs.cnt[cb], 1u);
+          atomicAdd(&bs.mass[cb], p);
+        }
+      }
+      if (pos + TV <= n && (reinterpret_cast<uintptr_t>(Ak + pos) & 15u) == 0u) {
+        *reinterpret_cast<uint4*>(Ak + pos) = make_uint4(key[0], key[1], key[2], key[3]);
+        *reinterpret_cast<uint4*>(Ak + pos + 4) = make_uint4(key[4], key[5], key[6], key[7]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < TV; ++k)
+          if (pos + k < n) Ak[pos + k] = key[k];
+      }
+    }
+  }
+  km = P.min_p > 0.0f ? wg_sum_sat<kNT>(km, 0x7fffffffu, sh.wg, bank) : (uint32_t)n;
+  const uint32_t gk = wg_min_u32<kNT>(fk, sh.wg, bank);
+  const uint32_t first = wg_min_u32<kNT>(fk == gk ? fid : 0xffffffffu, sh.wg, bank);  // indices[0]
+  const uint32_t Lw = min(Kk, km);  // positions top-k and min-p keep
+  __threadfence();
+  __syncthreads();
+
+  // ---- the region the chain can reach: coarse buckets up to the first whose
+  // count reaches Lw or whose mass passes top-p (with a margin)
+  if (wave_id() == 0) {
+    int cs = kNB - 1;
+    bucket_scan(bs, [&](int b, uint32_t ec, double em) {
+      const uint32_t ic = ec + bs.cnt[b];
+      const double im = em + (double)bs.mass[b];
+      if (b < cs && (ic >= Lw || (topp && im > (double)P.top_p * (1.0 + 0x1p-8)))) cs = b;
+    });
+    cs = (int)wave_min_u32((uint32_t)cs);
+    if (lane_id() == 0) bs.ctl[0] = (uint32_t)cs;
+  }
+  __syncthreads();
+  BucketRange br;
+  {
+    const uint64_t span = (uint64_t)(bs.ctl[0] + 1u) << kCoarseShift;
+    int sh_f = 0;
+    while ((span >> sh_f) > (uint64_t)kNB) ++sh_f;
+    br.kmin = kmin;
+    br.kcut = (uint32_t)min((uint64_t)kmin + span, (uint64_t)0xffffffffu);
+    br.shift = sh_f;
+  }
+  // ---- A': the fine histogram of the region from the stored keys
+  for (int b = t; b < kNB; b += kNT) {
+    bs.cnt[b] = 0u;
+    bs.mass[b] = 0.0f;
+  }
+  lds_barrier();
+  for (int base = 0; base < n; base += kNT * 8) {
+    const int pos = base + t * 8;
+    uint32_t k[8];
+    bucket_keys8(Ak, pos, n, k);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (br.in(k[i])) {
+        const int b = br.of(k[i]);
+        atomicAdd(&bs.cnt[b], 1u);
+        atomicAdd(&bs.mass[b], key_p(k[i]));
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- the running sum of top-p and the total (sampler.zig:112-117, :156-159)
+  if (wave_id() == 0) {
+    bucket_scan(bs, [&](int b, uint32_t ec, double em) {
+      const uint32_t c = bs.cnt[b];
+      const uint32_t ic = ec + c;
+      const double im = em + (double)bs.mass[b];
+      uint8_t cl = kBExact;
+      int j = 0;
+      if (c == 0) {
+        cl = kBEmpty;
+      } else if (ec >= Lw || (topp && em * (1.0 - D) > (double)P.top_p)) {
+        cl = kBNone;  // the chain stops before it
+      } else {
+        const double lo = em * (1.0 - D), hi = im * (1.0 + D);
+        const int elo = dbl_binade(lo), ehi = dbl_binade(hi);
+        const bool exact = b == 0 || (ec < Lw && Lw < ic) || (topp && hi > (double)P.top_p) || !(lo >= 0x1p-120) ||
+                           elo != ehi || elo > 126;
+        cl = exact ? kBExact : kBPlain;
+        j = exact ? 0 : elo;
+      }
+      bs.cls[b] = cl;
+      bs.jg[b] = (int8_t)j;
+    });
+  }
+  __syncthreads();
+  float v, before;
+  uint32_t pos, id;
+  bool stop;
+  uint32_t why = bucket_chain<false, kNT>(Ak, n, br, bs, 0.0f, Lw, topp ? P.top_p : -1.0f, v, before, pos, stop, id);
+  if (why != 0u) {
+    res.why = why;
+    return false;
+  }
+  const uint32_t K = pos;                  // the top-p cut, or Lw
+  const float total = stop ? before : v;   // the sum of the kept prefix
+  res.why = 0u;
+  res.K = K;
+  res.total = total;
+  res.token = first;
+  res.consumed = 0;
+  if (!(total > 0.0f)) return true;  // sampler.zig:160: indices[0], no draw
+
+  // ---- the draw (sampler.zig:162-168)
+  const float r0 = u * total;
+  if (wave_id() == 0) {
+    bucket_scan(bs, [&](int b, uint32_t ec, double em) {
+      const uint32_t c = bs.cnt[b];
+      const uint32_t ic = ec + c;
+      const double im = em + (double)bs.mass[b];
+      uint8_t cl = kBExact;
+      int j = 0;
+      if (c == 0) {
+        cl = kBEmpty;
+      } else if (ec >= K || (double)r0 - em * (1.0 - D) <= 0.0) {
+        cl = kBNone;  // past the kept prefix, or the draw stops before it
+      } else {
+        const double hi = (double)r0 - em * (1.0 - D);  // the value before the bucket, at most
+        const double lo = (double)r0 - im * (1.0 + D);  // after it, at least
+        const int elo = dbl_binade(lo), ehi = dbl_binade(hi);
+        const bool exact = (ec < K && K < ic) || !(lo >= 0x1p-120) || elo != ehi || ehi > 126;
+        cl = exact ? kBExact : kBPlain;
+        j = exact ? 0 : elo;
+      }
+      bs.cls[b] = cl;
+      bs.jg[b] = (int8_t)j;
+    });
+  }
+  __syncthreads();
+  why = bucket_chain<true, kNT>(Ak, n, br, bs, r0, K, -1.0f, v, before, pos, stop, id);
+  if (why != 0u) {
+    res.why = 32u + why;
+    return false;
+  }
+  res.token = stop ? id : first;  // never at or below 0: indices[0]
+  res.consumed = 1;
+  return true;
+}
+
 template <class Src>
 __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenShared* pen, SampleShared& sh,
                                              int bank, float m, float S, uint32_t path) {
@@ -1268,6 +1464,38 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
   const bool filters = (P.top_k > 0 && P.top_k < (uint32_t)n) || (P.top_p > 0.0f && P.top_p < 1.0f) ||
                        P.min_p > 0.0f;
   const bool lazy_p = typical && !filters && n >= 2;
+  // release the slot once every thread is done with it (a value no later
+  // call's epoch takes)
+  auto release = [&]() {
+    __threadfence();
+    __syncthreads();
+    LLZ_STAMP(row, 14);
+    if (t == 0) atomicExch(&Q.fb_owner[slot], P.epoch ^ (1ull << 63));
+  };
+  // Without typical-p the kept prefix, the total and the draw come from
+  // buckets of the p keys (llz_bucket.h), without a sort of the row.  The
+  // kept ids in p order (a diagnostic output) need the sort.
+  if (!typical && filters && !Q.kept_ids && !Q.kept_probs && n >= kBucketMinN) {
+    BucketResult br;
+    br.why = 0u;
+    if (select_buckets<Src>(X, n, m, S, u, P, Ak, sh, bank, br)) {
+      LLZ_STAMP(row, 11);
+      if (t == 0) {
+        Q.tokens[row] = br.token;
+        if (Q.consumed) Q.consumed[row] = (uint8_t)br.consumed;
+        if (Q.kept_count) Q.kept_count[row] = br.K;
+        if (Q.row_stats) {
+          float* rs = Q.row_stats + (int64_t)row * 4;
+          rs[0] = m; rs[1] = S; rs[2] = 0.0f; rs[3] = br.total;
+        }
+        if (Q.status) Q.status[row] = path | kPathBuckets;
+      }
+      release();
+      return;
+    }
+    __syncthreads();  // every thread is past the bucket path: the sort below overwrites its keys
+    path |= min(br.why, 255u) << 8;  // diagnostic: why the bucket path declined
+  }
   const GlobalList GL{Ak, Av};
   if (!lazy_p) {
     // (~p bits, id) in index order, the next tile's loads in flight; the
@@ -1408,12 +1636,7 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
   } else {
     finish(GL, K, [&](int) { return true; }, 0xffffffffu);
   }
-  // release the slot once every thread is done with it (a value no later
-  // call's epoch takes)
-  __threadfence();
-  __syncthreads();
-  LLZ_STAMP(row, 14);
-  if (t == 0) atomicExch(&Q.fb_owner[slot], P.epoch ^ (1ull << 63));
+  release();
 }
 
 }  // namespace llz
