@@ -42,20 +42,32 @@ constexpr int kCoarseShift = 17;   // coarse histogram: 2^17 keys per bucket
 constexpr int kBucketMinN = 8192;  // shorter rows keep the sorting path
 // Relative margin of the predictions: the exact running value differs from
 // the histogram's real-valued prefix by the sequential rounding (about
-// sqrt(count) half-units on random data, far below this) and the f32
-// rounding of the bucket masses.
-constexpr double kBucketDelta = 0x1p-12;
+// sqrt(count / 12) units of the running value's grid on random data: 9e-6
+// relative after configuration 4's 217k terms, so 2^-16 declined 3% of its
+// rows), the truncation of lower-binade terms in the bucket masses and their
+// f32 rounding (each about 2^-24).
+constexpr double kBucketDelta = 0x1p-13;
+constexpr int kCountShift = 44;  // histogram word: count << 44 | sum of scaled significands
+// Bucket arrays are padded by one entry per 64 buckets: wave 0's scans give
+// each lane 64 consecutive buckets, which unpadded would sit in one LDS bank.
+constexpr int kNBP = kNB + kNB / 64;
+__device__ __forceinline__ int bix(int b) { return b + (b >> 6); }
 
 enum : uint8_t { kBNone = 0, kBEmpty = 1, kBPlain = 2, kBExact = 3, kBExactTie = 4 };
 
-struct BucketShared {
-  uint32_t cnt[kNB];    // elements per bucket
-  float mass[kNB];      // their p, summed in any order (predictions only)
-  uint32_t sum[kNB];    // PLAIN: integer sum of RN(p / u) on grid jg
-  uint32_t off[kNB];    // EXACT: first position in the sorted list
-  int8_t jg[kNB];       // PLAIN: the binade of the running value
-  uint8_t cls[kNB];
-  uint8_t tie[kNB];     // PLAIN: bit 0 a term is a tie on grid jg, bit 1 the sum reached kSat
+struct BucketShared {  // arrays indexed through bix()
+  uint32_t cnt[kNBP];   // elements per bucket
+  float mass[kNBP];     // their p summed (predictions only)
+  union {
+    struct {
+      uint32_t sum[kNBP];  // PLAIN: integer sum of RN(p / u) on grid jg
+      uint32_t off[kNBP];  // EXACT: first position in the sorted list
+    };
+    uint64_t hist[kNBP];   // histogram passes: count << 44 | the significands of p scaled to the bucket's top binade
+  };
+  int8_t jg[kNBP];      // PLAIN: the binade of the running value
+  uint8_t cls[kNBP];
+  uint8_t tie[kNBP];    // PLAIN: bit 0 a term is a tie on grid jg, bit 1 the sum reached kSat
   uint64_t list[kBList];  // EXACT buckets' elements, (key << 32 | id), sorted
   uint32_t nlist;
   uint32_t ctl[8];
@@ -84,6 +96,33 @@ __device__ __forceinline__ void bucket_keys8(const uint32_t* Kp, int pos, int n,
 }
 
 __device__ __forceinline__ float key_p(uint32_t key) { return __uint_as_float(~key); }
+
+// Biased exponent of p = key_p(key) (1 for subnormals) and its 24-bit
+// significand: p = sig * 2^(E - 150).
+__device__ __forceinline__ uint32_t key_E(uint32_t key) {
+  const uint32_t e = (~key >> 23) & 0xffu;
+  return e == 0u ? 1u : e;
+}
+__device__ __forceinline__ uint32_t key_sig(uint32_t key) {
+  const uint32_t b = ~key;
+  return (b & 0x7fffffu) | (((b >> 23) & 0xffu) != 0u ? 0x800000u : 0u);
+}
+
+// One element's histogram word for a bucket whose largest p has biased
+// exponent Etop: its count and its significand scaled to 2^(Etop - 150)
+// (terms of lower binades lose their low bits: relative error < 2^-23 each).
+__device__ __forceinline__ uint64_t hist_word(uint32_t key, uint32_t Etop) {
+  const uint32_t d = Etop - key_E(key);  // >= 0: p <= the bucket's largest
+  const uint64_t v = d < 24u ? (uint64_t)(key_sig(key) >> d) : 0ull;
+  return (1ull << kCountShift) | v;
+}
+
+// Count and mass of a bucket from its histogram word (Etop as above).
+__device__ __forceinline__ void hist_unpack(uint64_t h, uint32_t Etop, uint32_t& cnt, float& mass) {
+  cnt = (uint32_t)(h >> kCountShift);
+  const double sig = (double)(h & ((1ull << kCountShift) - 1ull));
+  mass = (float)(sig * exp2((double)((int)Etop - 150)));
+}
 
 // Binade of a positive double (its unbiased exponent; -1023 for 0).
 __device__ __forceinline__ int dbl_binade(double x) {
@@ -128,8 +167,8 @@ __device__ __forceinline__ void bucket_scan(BucketShared& bs, ClsFn cls_of) {
   uint32_t c = 0;
   double ms = 0.0;
   for (int i = 0; i < PL; ++i) {
-    c += bs.cnt[lane * PL + i];
-    ms += (double)bs.mass[lane * PL + i];
+    c += bs.cnt[bix(lane * PL + i)];
+    ms += (double)bs.mass[bix(lane * PL + i)];
   }
   uint32_t ci = c;
   double mi = ms;
@@ -147,8 +186,8 @@ __device__ __forceinline__ void bucket_scan(BucketShared& bs, ClsFn cls_of) {
   for (int i = 0; i < PL; ++i) {
     const int b = lane * PL + i;
     cls_of(b, ec, em);
-    ec += bs.cnt[b];
-    em += (double)bs.mass[b];
+    ec += bs.cnt[bix(b)];
+    em += (double)bs.mass[bix(b)];
   }
 }
 
@@ -167,8 +206,8 @@ template <int NT>
 __device__ void bucket_sums(const uint32_t* Kp, int n, const BucketRange& br, BucketShared& bs) {
   const int t = (int)threadIdx.x;
   for (int b = t; b < kNB; b += NT) {
-    bs.sum[b] = 0u;
-    bs.tie[b] = 0u;
+    bs.sum[bix(b)] = 0u;
+    bs.tie[bix(b)] = 0u;
   }
   __syncthreads();
   for (int base = 0; base < n; base += NT * 8) {
@@ -179,22 +218,22 @@ __device__ void bucket_sums(const uint32_t* Kp, int n, const BucketRange& br, Bu
     for (int i = 0; i < 8; ++i) {
       if (!br.in(k[i])) continue;
       const int b = br.of(k[i]);
-      if (bs.cls[b] == kBPlain) {
+      if (bs.cls[bix(b)] == kBPlain) {
         bool tie;
-        const uint32_t r = grid_round(key_p(k[i]), bs.jg[b], tie);  // <= kSat
+        const uint32_t r = grid_round(key_p(k[i]), bs.jg[bix(b)], tie);  // <= kSat
         // terms <= kSat and a flag once the sum reaches kSat: no wrap goes unseen
-        const uint32_t old = atomicAdd(&bs.sum[b], r);
-        if (tie) bs.tie[b] |= 1u;
-        if (old >= kSat) bs.tie[b] |= 2u;
+        const uint32_t old = atomicAdd(&bs.sum[bix(b)], r);
+        if (tie) bs.tie[bix(b)] |= 1u;
+        if (old >= kSat) bs.tie[bix(b)] |= 2u;
       }
     }
   }
   __syncthreads();
   for (int b = t; b < kNB; b += NT) {
-    if (bs.cls[b] == kBPlain && (bs.tie[b] & 2u))
-      bs.cls[b] = kBNone;
-    else if (bs.cls[b] == kBPlain && bs.tie[b])
-      bs.cls[b] = kBExact;
+    if (bs.cls[bix(b)] == kBPlain && (bs.tie[bix(b)] & 2u))
+      bs.cls[bix(b)] = kBNone;
+    else if (bs.cls[bix(b)] == kBPlain && bs.tie[bix(b)])
+      bs.cls[bix(b)] = kBExact;
   }
   __syncthreads();
 }
@@ -213,7 +252,7 @@ __device__ int bucket_batch(const uint32_t* Kp, int n, const BucketRange& br, Bu
     uint32_t c = 0;
     for (int i = 0; i < PL; ++i) {
       const int b = lane * PL + i;
-      c += (b >= blo && bs.cls[b] == kBExact) ? bs.cnt[b] : 0u;
+      c += (b >= blo && bs.cls[bix(b)] == kBExact) ? bs.cnt[bix(b)] : 0u;
     }
     uint32_t ci = c;
 #pragma unroll
@@ -225,10 +264,10 @@ __device__ int bucket_batch(const uint32_t* Kp, int n, const BucketRange& br, Bu
     int bhi = kNB;
     for (int i = 0; i < PL; ++i) {
       const int b = lane * PL + i;
-      const bool ex = b >= blo && bs.cls[b] == kBExact;
-      if (ex && run + bs.cnt[b] > (uint32_t)kBList && b < bhi) bhi = b;
-      bs.off[b] = run;
-      run += ex ? bs.cnt[b] : 0u;
+      const bool ex = b >= blo && bs.cls[bix(b)] == kBExact;
+      if (ex && run + bs.cnt[bix(b)] > (uint32_t)kBList && b < bhi) bhi = b;
+      bs.off[bix(b)] = run;
+      run += ex ? bs.cnt[bix(b)] : 0u;
     }
     bhi = (int)wave_min_u32((uint32_t)bhi);
     if (lane == 0) {
@@ -247,7 +286,7 @@ __device__ int bucket_batch(const uint32_t* Kp, int n, const BucketRange& br, Bu
     for (int i = 0; i < 8; ++i) {
       if (!br.in(k[i])) continue;
       const int b = br.of(k[i]);
-      if (b >= blo && b < bhi && bs.cls[b] == kBExact) {
+      if (b >= blo && b < bhi && bs.cls[bix(b)] == kBExact) {
         const uint32_t slot = atomicAdd(&bs.nlist, 1u);  // < kBList: the range's counts fit
         bs.list[slot] = ((uint64_t)k[i] << 32) | (uint32_t)(pos + i);
       }
@@ -284,9 +323,9 @@ __device__ uint32_t bucket_walk(const BucketShared& bs, float& v, float& before,
   before = v;
   for (int b0 = b_from & ~(kWave - 1); b0 < b_to; b0 += kWave) {
     const int b = b0 + lane;  // < kNB
-    const uint32_t cl = bs.cls[b];
-    const int jb = bs.jg[b];
-    const uint32_t sm = bs.sum[b], ct = bs.cnt[b], of = bs.off[b];
+    const uint32_t cl = bs.cls[bix(b)];
+    const int jb = bs.jg[bix(b)];
+    const uint32_t sm = bs.sum[bix(b)], ct = bs.cnt[bix(b)], of = bs.off[bix(b)];
     int i = b0 < b_from ? b_from - b0 : 0;
     const int iend = min(kWave, b_to - b0);
     while (i < iend) {
@@ -345,14 +384,16 @@ __device__ uint32_t bucket_walk(const BucketShared& bs, float& v, float& before,
 template <bool SUB, int NT>
 __device__ uint32_t bucket_chain(const uint32_t* Kp, int n, const BucketRange& br, BucketShared& bs, float v0,
                                  uint32_t lim, float thr, float& v_out, float& before_out, uint32_t& pos_out,
-                                 bool& stop_out, uint32_t& id_out) {
+                                 bool& stop_out, uint32_t& id_out, int row) {
   bucket_sums<NT>(Kp, n, br, bs);
+  LLZ_STAMP(row, 29);
   float v = v0, before = v0;
   uint32_t pos = 0, id = 0xffffffffu, why = kWalkMore;
   bool stop = false;
   for (int blo = 0; why == kWalkMore;) {
     const int bhi = bucket_batch<NT>(Kp, n, br, bs, blo);
     if (bhi == blo) return 16u;  // one bucket holds more than the list
+    if (blo == 0) LLZ_STAMP(row, 30);
     if (wave_id() == 0) {
       why = bucket_walk<SUB>(bs, v, before, pos, lim, thr, stop, id, blo, bhi);
       if (lane_id() == 0) {
@@ -372,6 +413,7 @@ __device__ uint32_t bucket_chain(const uint32_t* Kp, int n, const BucketRange& b
     stop = bs.ctl[4] != 0u;
     id = bs.ctl[5];
     __syncthreads();  // every thread has read ctl before a next batch writes it
+    if (blo == 0) LLZ_STAMP(row, 31);
     blo = bhi;
   }
   v_out = v;

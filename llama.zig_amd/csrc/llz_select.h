@@ -1206,12 +1206,13 @@ __device__ TypicalHead typical_head(const Src& X, int n, float m, float S, float
 // needs the sorting path (nothing is written then but Ak).
 template <class Src>
 __device__ bool select_buckets(const Src& X, int n, float m, float S, float u, const RowParams& P, uint32_t* Ak,
-                               SampleShared& sh, int& bank, BucketResult& res) {
+                               SampleShared& sh, int& bank, BucketResult& res, int row) {
   BucketShared& bs = sh.u.bkt;
   const int t = (int)threadIdx.x;
   const bool t1 = (P.flags & kFlagTIsOne) != 0;
   const bool vec = (P.flags & kFlagVecSrc) != 0;
   const bool topp = P.top_p > 0.0f && P.top_p < 1.0f;
+  if (n >= (1 << 20)) return false;  // histogram counts hold 20 bits
   const uint32_t Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? P.top_k : (uint32_t)n;
   // probs[indices[0]] is the maximum's, whose e is exp(0) = 1 (sampler.zig:121)
   const float p0 = 1.0f / S;
@@ -1220,11 +1221,11 @@ __device__ bool select_buckets(const Src& X, int n, float m, float S, float u, c
   const double D = kBucketDelta;
 
   // ---- A: the exact p of every element (sampler.zig:85, :90), its key, and
-  // the coarse histogram
-  for (int b = t; b < kNB; b += kNT) {
-    bs.cnt[b] = 0u;
-    bs.mass[b] = 0.0f;
-  }
+  // the coarse histogram of a sample (every eighth element)
+  // top binade of coarse bucket b (its smallest key); the last one holds every
+  // key past the range too
+  auto coarse_Etop = [&](int b) { return key_E(kmin + ((uint32_t)b << kCoarseShift)); };
+  for (int b = t; b < kNB; b += kNT) bs.hist[bix(b)] = 0ull;
   lds_barrier();
   uint32_t km = 0, fk = 0xffffffffu, fid = 0xffffffffu;
   {
@@ -1251,9 +1252,10 @@ __device__ bool select_buckets(const Src& X, int n, float m, float S, float u, c
             fk = key[k];
             fid = (uint32_t)(pos + k);
           }
-          const uint32_t cb = min((key[k] - kmin) >> kCoarseShift, (uint32_t)kNB - 1u);
-          atomicAdd(&bs.cnt[cb], 1u);
-          atomicAdd(&bs.mass[cb], p);
+          if (k == 0) {  // every eighth element, weight 8 (count and mass)
+            const uint32_t cb = min((key[k] - kmin) >> kCoarseShift, (uint32_t)kNB - 1u);
+            atomicAdd(&bs.hist[bix(cb)], 8ull * hist_word(key[k], coarse_Etop((int)cb)));
+          }
         }
       }
       if (pos + TV <= n && (reinterpret_cast<uintptr_t>(Ak + pos) & 15u) == 0u) {
@@ -1272,15 +1274,20 @@ __device__ bool select_buckets(const Src& X, int n, float m, float S, float u, c
   const uint32_t Lw = min(Kk, km);  // positions top-k and min-p keep
   __threadfence();
   __syncthreads();
+  for (int b = t; b < kNB; b += kNT) hist_unpack(bs.hist[bix(b)], coarse_Etop(b), bs.cnt[bix(b)], bs.mass[bix(b)]);
+  __syncthreads();
+  LLZ_STAMP(row, 23);
 
   // ---- the region the chain can reach: coarse buckets up to the first whose
-  // count reaches Lw or whose mass passes top-p (with a margin)
+  // count reaches Lw or whose mass passes top-p, both with a margin for the
+  // histogram's sampling (about sqrt(8 count): 0.6% at 217k elements); a cut
+  // beyond the region only sends the row to the sorting path
   if (wave_id() == 0) {
     int cs = kNB - 1;
     bucket_scan(bs, [&](int b, uint32_t ec, double em) {
-      const uint32_t ic = ec + bs.cnt[b];
-      const double im = em + (double)bs.mass[b];
-      if (b < cs && (ic >= Lw || (topp && im > (double)P.top_p * (1.0 + 0x1p-8)))) cs = b;
+      const uint32_t ic = ec + bs.cnt[bix(b)];
+      const double im = em + (double)bs.mass[bix(b)];
+      if (b < cs && ((double)ic >= 1.05 * Lw + 2048.0 || (topp && im > (double)P.top_p * 1.05))) cs = b;
     });
     cs = (int)wave_min_u32((uint32_t)cs);
     if (lane_id() == 0) bs.ctl[0] = (uint32_t)cs;
@@ -1296,10 +1303,8 @@ __device__ bool select_buckets(const Src& X, int n, float m, float S, float u, c
     br.shift = sh_f;
   }
   // ---- A': the fine histogram of the region from the stored keys
-  for (int b = t; b < kNB; b += kNT) {
-    bs.cnt[b] = 0u;
-    bs.mass[b] = 0.0f;
-  }
+  auto fine_Etop = [&](int b) { return key_E(br.kmin + ((uint32_t)b << br.shift)); };
+  for (int b = t; b < kNB; b += kNT) bs.hist[bix(b)] = 0ull;
   lds_barrier();
   for (int base = 0; base < n; base += kNT * 8) {
     const int pos = base + t * 8;
@@ -1309,19 +1314,21 @@ __device__ bool select_buckets(const Src& X, int n, float m, float S, float u, c
     for (int i = 0; i < 8; ++i) {
       if (br.in(k[i])) {
         const int b = br.of(k[i]);
-        atomicAdd(&bs.cnt[b], 1u);
-        atomicAdd(&bs.mass[b], key_p(k[i]));
+        atomicAdd(&bs.hist[bix(b)], hist_word(k[i], fine_Etop(b)));
       }
     }
   }
   __syncthreads();
+  for (int b = t; b < kNB; b += kNT) hist_unpack(bs.hist[bix(b)], fine_Etop(b), bs.cnt[bix(b)], bs.mass[bix(b)]);
+  __syncthreads();
 
+  LLZ_STAMP(row, 24);
   // ---- the running sum of top-p and the total (sampler.zig:112-117, :156-159)
   if (wave_id() == 0) {
     bucket_scan(bs, [&](int b, uint32_t ec, double em) {
-      const uint32_t c = bs.cnt[b];
+      const uint32_t c = bs.cnt[bix(b)];
       const uint32_t ic = ec + c;
-      const double im = em + (double)bs.mass[b];
+      const double im = em + (double)bs.mass[bix(b)];
       uint8_t cl = kBExact;
       int j = 0;
       if (c == 0) {
@@ -1336,19 +1343,21 @@ __device__ bool select_buckets(const Src& X, int n, float m, float S, float u, c
         cl = exact ? kBExact : kBPlain;
         j = exact ? 0 : elo;
       }
-      bs.cls[b] = cl;
-      bs.jg[b] = (int8_t)j;
+      bs.cls[bix(b)] = cl;
+      bs.jg[bix(b)] = (int8_t)j;
     });
   }
   __syncthreads();
+  LLZ_STAMP(row, 25);
   float v, before;
   uint32_t pos, id;
   bool stop;
-  uint32_t why = bucket_chain<false, kNT>(Ak, n, br, bs, 0.0f, Lw, topp ? P.top_p : -1.0f, v, before, pos, stop, id);
+  uint32_t why = bucket_chain<false, kNT>(Ak, n, br, bs, 0.0f, Lw, topp ? P.top_p : -1.0f, v, before, pos, stop, id, row);
   if (why != 0u) {
     res.why = why;
     return false;
   }
+  LLZ_STAMP(row, 26);
   const uint32_t K = pos;                  // the top-p cut, or Lw
   const float total = stop ? before : v;   // the sum of the kept prefix
   res.why = 0u;
@@ -1362,9 +1371,9 @@ __device__ bool select_buckets(const Src& X, int n, float m, float S, float u, c
   const float r0 = u * total;
   if (wave_id() == 0) {
     bucket_scan(bs, [&](int b, uint32_t ec, double em) {
-      const uint32_t c = bs.cnt[b];
+      const uint32_t c = bs.cnt[bix(b)];
       const uint32_t ic = ec + c;
-      const double im = em + (double)bs.mass[b];
+      const double im = em + (double)bs.mass[bix(b)];
       uint8_t cl = kBExact;
       int j = 0;
       if (c == 0) {
@@ -1379,12 +1388,14 @@ __device__ bool select_buckets(const Src& X, int n, float m, float S, float u, c
         cl = exact ? kBExact : kBPlain;
         j = exact ? 0 : elo;
       }
-      bs.cls[b] = cl;
-      bs.jg[b] = (int8_t)j;
+      bs.cls[bix(b)] = cl;
+      bs.jg[bix(b)] = (int8_t)j;
     });
   }
   __syncthreads();
-  why = bucket_chain<true, kNT>(Ak, n, br, bs, r0, K, -1.0f, v, before, pos, stop, id);
+  LLZ_STAMP(row, 27);
+  why = bucket_chain<true, kNT>(Ak, n, br, bs, r0, K, -1.0f, v, before, pos, stop, id, row);
+  LLZ_STAMP(row, 28);
   if (why != 0u) {
     res.why = 32u + why;
     return false;
@@ -1478,7 +1489,7 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
   if (!typical && filters && !Q.kept_ids && !Q.kept_probs && n >= kBucketMinN) {
     BucketResult br;
     br.why = 0u;
-    if (select_buckets<Src>(X, n, m, S, u, P, Ak, sh, bank, br)) {
+    if (select_buckets<Src>(X, n, m, S, u, P, Ak, sh, bank, br, row)) {
       LLZ_STAMP(row, 11);
       if (t == 0) {
         Q.tokens[row] = br.token;

@@ -29,6 +29,9 @@ SLOTS = {
     16: "F+X: re-reads landed (wave 0)", 17: "F+X: slots done (wave 0)", 18: "F+X: first segment summed (wave 0)",
     19: "F+X: specials settled (wave 0)", 20: "C: walk start", 21: "C: walk done (wave 0)",
     22: "S: LDS-resident batches done",
+    23: "buckets: keys and coarse histogram", 24: "buckets: fine histogram", 25: "buckets: top-p classes",
+    26: "buckets: top-p walk", 27: "buckets: draw classes", 28: "buckets: draw walk",
+    29: "buckets (draw): sums", 30: "buckets (draw): first batch gathered", 31: "buckets (draw): first batch walked",
 }
 # phases as (name, from slot, to slot)
 PHASES = [
@@ -41,6 +44,10 @@ PHASES = [
     ("F+X: wait for re-reads (w0)", 3, 16), ("F+X: slots (w0)", 16, 17), ("F+X: first segment (w0)", 17, 18),
     ("F+X: settle (w0)", 18, 19), ("F+X: barrier wait (w0)", 19, 4), ("C: candidate reads", 5, 20),
     ("C: walk (w0)", 20, 21), ("C: after walk", 21, 6),
+    ("buckets: keys + coarse histogram", 8, 23), ("buckets: fine histogram", 23, 24),
+    ("buckets: top-p classes", 24, 25), ("buckets: top-p chain", 25, 26), ("buckets: draw classes", 26, 27),
+    ("buckets: draw chain", 27, 28), ("buckets draw: sums", 27, 29), ("buckets draw: 1st gather+sort", 29, 30),
+    ("buckets draw: 1st walk", 30, 31), ("buckets draw: rest", 31, 28),
 ]
 
 
