@@ -251,7 +251,12 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   P.kept_cap = extras ? extras->kept_cap : 0;
   P.src_stride = src_stride;
   P.orig_stride = row_stride;
-  P.flags = (cfg->temperature == 1.0f ? kFlagTIsOne : 0u) | (vec ? kFlagVecSrc : 0u) | kFlagFallback;
+  // the token alone: no probabilities and no row statistics asked for, and no
+  // typical-p (its entropy needs the exact normaliser)
+  const bool tok_only = !(extras && (extras->d_kept_probs || extras->d_row_stats)) &&
+                        !(cfg->typical_p > 0.0f && cfg->typical_p < 1.0f);
+  P.flags = (cfg->temperature == 1.0f ? kFlagTIsOne : 0u) | (vec ? kFlagVecSrc : 0u) | kFlagFallback |
+            (tok_only ? kFlagTokenOnly : 0u);
   P.xf_src = xf_src;
   P.xf_orig = xb;
   P.cap = cap;

@@ -148,6 +148,9 @@ struct FastShared {
   float s_run;    // combine: running sum at next_g
   int done;
   uint32_t diag;  // kPathWalkRounds / kPathResolveGeneric (diagnostics for the row's status)
+  float qsum[fastp::W];  // token-only rows: per wave, the sum of its estimates q
+  uint32_t tcand; // token-only rows: candidates collected
+  uint32_t tfail; // token-only rows: not certified (the exact phases follow)
 };
 
 typedef float llz_f4v __attribute__((ext_vector_type(4)));

@@ -19,6 +19,7 @@ constexpr int kFbSlots = 256;
 constexpr uint32_t kFlagTIsOne = 1u;    // temperature == 1.0f exactly: (v - m) / T == v - m
 constexpr uint32_t kFlagVecSrc = 2u;    // 16-byte loads are legal on the rows the chain reads
 constexpr uint32_t kFlagFallback = 4u;  // the full-row fallback buffers are present
+constexpr uint32_t kFlagTokenOnly = 8u;  // no probabilities or row statistics requested: the token alone
 
 // RowParams.xf_src / xf_orig: transforms applied as a row is read
 constexpr uint32_t kXfCap = 1u;    // v = tanh(v / cap) * cap   (main.zig:653-658)
@@ -32,6 +33,7 @@ constexpr uint32_t kPathFallback = 4u;      // full-row radix sort
 constexpr uint32_t kPathNormFallback = 8u;  // streaming normaliser (row not certified by the fast path)
 constexpr uint32_t kPathWalkRounds = 16u;    // diagnostic: the walk took more than one round of EXACT slots
 constexpr uint32_t kPathResolveGeneric = 32u;  // diagnostic: an event beyond a segment's tabulated grids
+constexpr uint32_t kPathTokenOnly = 128u;     // the token certified without the exact normaliser
 constexpr uint32_t kPathBuckets = 64u;        // full row without a sort: kept prefix, total and draw by p-key buckets
 constexpr uint32_t kPathError = 0x80000000u;
 
@@ -40,7 +42,7 @@ constexpr uint32_t kPathError = 0x80000000u;
 // the kernel's phases, slot k of row r at llz_phase_stamps[r * kStampSlots +
 // k].  In ordinary builds LLZ_STAMP compiles to nothing.
 constexpr int kStampRows = 4096;
-constexpr int kStampSlots = 32;
+constexpr int kStampSlots = 40;
 #ifdef LLZ_PHASE_STAMPS
 static __device__ unsigned long long llz_phase_stamps[kStampRows * kStampSlots];  // read by llz_stats.hip's copy-out
 #define LLZ_STAMP(row, k)                                                                     \

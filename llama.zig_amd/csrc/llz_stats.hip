@@ -14,6 +14,7 @@
 #include "llz_math.h"
 #include "llz_norm.h"
 #include "llz_select.h"
+#include "llz_token.h"
 #include "llz_wg.h"
 
 namespace llz {
@@ -684,6 +685,13 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     }
   }
   if (lane < nseg_w) F.v.aseg[w + W * lane] = my_a;
+  // token-only calls: this wave's sum of its estimates (the normaliser's
+  // estimate in phase M takes one value per wave)
+  const bool tok = (P.flags & kFlagTokenOnly) != 0u && fits;
+  if (tok) {
+    const float qs = wave_fold_f32(lane < nseg_w ? my_a : 0.0f);
+    if (lane == kWave - 1) F.qsum[w] = qs;
+  }
   if (!fits) {  // rows the fast path does not take: maximum and NaN scan only
     if constexpr (FASTLD) {
       // kScanDepth float4 loads per thread in flight (64 KB per workgroup)
@@ -735,6 +743,99 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   for (int i = 0; i < W; ++i) {
     m = fmaxf(m, F.mw[i]);
     nanrow = nanrow | (F.nanw[i] != 0u);
+  }
+  // ---- token-only rows (no probabilities or statistics asked for, no
+  // typical-p): the chain's decisions from the candidates' exact terms and an
+  // interval for the normaliser (token_select), without the rest of phase M
+  // and phases S .. C.  The normaliser's estimate: the waves' sums of
+  // estimates, each scaled by its R.  Candidates: the lanes of segments
+  // whose estimated sum reaches theta (1 - 2^-10) holding a term whose
+  // estimate does (estimates are within 2^-16 of the terms, and no term
+  // exceeds its segment's sum), re-read and evaluated exactly; the list lies
+  // in F.v, free once every wave has read the segment sums below.
+  if (tok && !nanrow && fabsf(m) <= 3.0e38f) {
+    float s_est = 0.0f;
+    bool tbad = false;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      const float awi = fmaf(m, -l2e_t, F.cw[i]);
+      tbad = tbad | ((G > i) & !(fabsf(awi) <= 64.0f));
+      s_est += G > i ? F.qsum[i] * __builtin_amdgcn_exp2f(awi) : 0.0f;
+    }
+    if (!tbad) {
+      const float Rw_t = __builtin_amdgcn_exp2f(fmaf(m, -l2e_t, cw));
+      const float theta_t = P.cand_theta;
+      const float thr_e = theta_t * (1.0f - 0x1p-10f);
+      const uint64_t segm = bal64(lane < nseg_w && my_a * Rw_t >= thr_e);
+      const float thr_q = thr_e / Rw_t;  // q R_w ~ e
+      if (t == 0) {
+        F.tcand = 0u;
+        F.tfail = 0u;
+      }
+      int tq = 0;
+      auto tscan = [&](const int k, const float4 q) {
+        const bool c = lane4 < seg_lim(k) && max3_raw(max3_raw(q.x, q.y, q.z), q.w, q.w) >= thr_q;
+        const uint64_t bm = bal64(c);
+        if (bm != 0ull) {
+          const int slot = tq + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
+          if (c && slot < QCAP) F.qpos[w][slot] = (uint32_t)((w + W * k) * SEG + lane4);
+          tq += __popcll(bm);
+        }
+      };
+#pragma unroll
+      for (int k = 0; k < KV; ++k)
+        if ((segm >> k) & 1ull) tscan(k, d[k]);
+      for (uint64_t rest = segm >> KV; rest != 0ull; rest &= rest - 1ull) {
+        const int k = KV + __ffsll((long long)rest) - 1;
+        tscan(k, *reinterpret_cast<const float4*>(&F.u.data[w][k - KV][lane * 4]));
+      }
+      float4 tv[QCAP / kWave];
+#pragma unroll
+      for (int h = 0; h < QCAP / kWave; ++h) {
+        const int i = h * kWave + lane;
+        const int pos = i < min(tq, QCAP) ? (int)F.qpos[w][i] : 0;
+        tv[h] = X.fix4(pos, FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n), n);
+      }
+      lds_barrier();  // F.tcand / F.tfail cleared
+      LLZ_STAMP(row, 32);
+      if (tq > QCAP && lane == 0) atomicOr(&F.tfail, 1u);
+      uint64_t* const tl = reinterpret_cast<uint64_t*>(&F.v);  // [kTokCap] collected, then [kTokCap] sorted
+#pragma unroll
+      for (int h = 0; h < QCAP / kWave; ++h) {
+        const int i = h * kWave + lane;
+        if (i < min(tq, QCAP)) {
+          const int pos = (int)F.qpos[w][i];
+          const float4 e = exact_terms4(tv[h], m, P.temperature, t1);  // sampler.zig:85
+          const float es[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            if (pos + c < n && es[c] >= theta_t) {
+              const uint32_t slot = atomicAdd(&F.tcand, 1u);
+              if (slot < (uint32_t)kTokCap) tl[slot] = ((uint64_t)(~__float_as_uint(es[c])) << 32) | (uint32_t)(pos + c);
+            }
+          }
+        }
+      }
+      __syncthreads();
+      LLZ_STAMP(row, 33);
+      const int tc = (int)F.tcand;
+      if (tc <= kTokCap && F.tfail == 0u) {
+        token_sort(tl, tl + kTokCap, reinterpret_cast<uint32_t*>(&F.qpos[0][0]), tc);
+        LLZ_STAMP(row, 34);
+        if (w == 0) token_select(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, u_row, theta_t, &F.tfail);
+      } else if (t == 0) {
+        F.tfail = 1u;
+      }
+      __syncthreads();
+      if (F.tfail == 0u) {
+        LLZ_STAMP(row, 15);
+        return;
+      }
+      // not certified: the exact phases, with the segment sums the list
+      // overwrote written again (F.qpos is rewritten in phase S)
+      if (lane < nseg_w) F.v.aseg[w + W * lane] = my_a;
+      __syncthreads();
+    }
   }
   // the segment sums of q of round `lane` (segments W lane .. W lane + W - 1,
   // one per wave), all read at once; absent ones are 0 (selects, not

@@ -1,0 +1,211 @@
+// llz_token.h -- the token of a row without its exact normaliser, for calls
+// that ask for no probabilities and no row statistics (the reference's
+// Sampler.sample returns the token alone, sampler.zig:26-28).
+//
+// Every decision of the chain after the normaliser S compares quantities
+// that scale with 1/S (sampler.zig:90-168):
+//   - the order (p desc, id asc) is the order of the terms e = exp((v-m)/T)
+//     wherever two terms differ by more than 2^-21 relative (then their
+//     quotients by any S round to different floats) or are equal;
+//   - min-p compares RN(e / S) with RN(RN(1 / S) min_p): a term above
+//     min_p (1 + 2^-22) passes and one below min_p (1 - 2^-22) fails,
+//     whatever S (three roundings of 2^-24 each);
+//   - the draw: r_q = RN(r_{q-1} - p_q) from RN(u * total) stops at the
+//     first r_q <= 0; with E the sum of the kept terms and C_q the sum of the
+//     first q+1, S r_q differs from u E - C_q by at most (3K + 7) 2^-24 E
+//     (K kept terms: the sums' and quotients' roundings), so a row whose
+//     u E - C_q stay clear of that band stops where the sign of u E - C_q
+//     first turns, whatever S;
+//   - top-p compares the running sum, which lies within (2q + 4) 2^-24 of
+//     C_q / S, with top_p: that needs S itself.  The reference's S is the
+//     sequential f32 sum of n positive terms, within (n - 1) 2^-24 / (1 - (n -
+//     1) 2^-24) of the real sum (the recursive-summation bound), which phase
+//     L's estimates give to 2^-14; a top-p decision that holds at both ends
+//     of that interval holds at S.
+// A row whose decisions all hold is finished here, bit-exact; any other row
+// continues with the exact phases.
+#pragma once
+
+#include "llz_internal.h"
+#include "llz_norm.h"
+#include "llz_wg.h"
+
+namespace llz {
+
+constexpr int kTokCap = 256;  // candidates of a token-only row at most
+
+// Rank sort of c distinct keys (e desc as ~bits, id asc) by the whole
+// workgroup: wave w counts against its eighth of the list.
+__device__ __forceinline__ void token_sort(const uint64_t* in, uint64_t* out, uint32_t* rank, int c) {
+  constexpr int NW = kNT / kWave;
+  const int t = (int)threadIdx.x, lane = lane_id(), w = wave_id();
+  for (int i = t; i < c; i += kNT) rank[i] = 0u;
+  lds_barrier();
+  const int j0 = (w * c) / NW, j1 = ((w + 1) * c) / NW;
+  for (int i = lane; i < c; i += kWave) {
+    const uint64_t ki = in[i];
+    uint32_t r = 0;
+    for (int j = j0; j < j1; ++j) r += in[j] < ki ? 1u : 0u;
+    if (r != 0u) atomicAdd(&rank[i], r);
+  }
+  lds_barrier();
+  for (int i = t; i < c; i += kNT) out[rank[i]] = in[i];
+  lds_barrier();
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = readlane_u32((uint32_t)b, l), hi = readlane_u32((uint32_t)(b >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// DPP move of a double (both halves), lanes the control leaves out get 0.
+template <int CTRL, int RM, int BM, bool BC>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = dpp_u32<CTRL, RM, BM, BC>(0u, (uint32_t)b);
+  const uint32_t hi = dpp_u32<CTRL, RM, BM, BC>(0u, (uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Inclusive prefix sum within a wave (the DPP pattern of wave_incl_scan_op).
+__device__ __forceinline__ double wave_incl_scan_f64(double x) {
+  double s = x;
+  s = s + dpp_f64<0x111, 0xf, 0xf, true>(x);
+  s = s + dpp_f64<0x112, 0xf, 0xf, true>(x);
+  s = s + dpp_f64<0x113, 0xf, 0xf, true>(x);
+  s = s + dpp_f64<0x114, 0xf, 0xe, false>(s);
+  s = s + dpp_f64<0x118, 0xf, 0xc, false>(s);
+  s = s + dpp_f64<0x142, 0xa, 0xf, false>(s);
+  s = s + dpp_f64<0x143, 0xc, 0xf, false>(s);
+  return s;
+}
+
+// Wave 0: the chain's decisions (sampler.zig:100-168) for a token-only row
+// from its candidates srt[0, c), sorted (e desc, id asc) -- every term e >=
+// theta, all of them exact -- and the estimate s_est of the normaliser.
+// Writes the token, the draw flag, the kept count and ids; sets *tfail
+// instead when a decision does not hold over the interval of S.
+// Out of line; the launch's arguments come through the kernel's argument
+// segment (as the other out-of-line paths take them).
+__device__ __noinline__ void token_select(const KArgs* A, int row, const uint64_t* srt, int c, float s_est, float u,
+                                          float theta, uint32_t* tfail) {
+  const RowParams& P = A->P;
+  const RowPtrs& Q = A->Q;
+  const int lane = lane_id();
+  const int n = P.n;
+  auto e_at = [&](int q) { return __uint_as_float(~(uint32_t)(srt[q] >> 32)); };
+  auto id_at = [&](int q) { return (uint32_t)srt[q]; };
+  bool ok = c >= 1;
+  // certified prefix M: list terms clear of every term outside the list
+  // (< theta); min-p: p < RN(RN(1/S) min_p) exactly for the terms below
+  // mp_lo, never for those above mp_hi, and the terms past M lie below
+  // theta (1 + 2^-21) < min_p (1 - 2^-21)
+  const float th_hi = theta * (1.0f + 0x1p-21f);
+  const bool mp = P.min_p > 0.0f;
+  const float mp_hi = P.min_p * (1.0f + 0x1p-22f), mp_lo = P.min_p * (1.0f - 0x1p-22f);
+  int M = 0, Km = 0;
+  for (int b = 0; b < c; b += kWave) {
+    const int q = b + lane;
+    const float e = q < c ? e_at(q) : 0.0f;
+    const bool inM = q < c && (theta == 0.0f || e > th_hi);
+    M += __popcll(bal64(inM));
+    Km += __popcll(bal64(inM && e > mp_hi));
+    if (mp && bal64(inM && !(e > mp_hi) && !(e < mp_lo)) != 0ull) ok = false;
+  }
+  if (!mp) Km = n;
+  const int Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
+  const int L = min(Kk, Km);
+  if (L > M) ok = false;
+  // the interval of the reference's normaliser
+  const double g = (double)(n - 1) * 0x1p-24;
+  const double gr = g / (1.0 - g) + 0x1p-14;
+  const double S_lo = (double)s_est * (1.0 - gr), S_hi = (double)s_est * (1.0 + gr);
+  if (!(S_lo > 0.0)) ok = false;
+  const bool topp = P.top_p > 0.0f && P.top_p < 1.0f;
+  // one pass over positions [0, L): the running sums C_q of the terms
+  // (double), top-p's cut (sampler.zig:111-118), and the order: adjacent terms
+  // up to max(L, 1) equal (then ordered by id) or apart by more than 2^-21
+  const int pe = min(max(L, 1), M - 1);
+  const int span = max(L, pe);
+  double carry = 0.0, C0 = 0.0;  // C0: lane q's C_q for q < 64
+  int cut = -1;
+  for (int b = 0; b < span && ok && cut < 0; b += kWave) {
+    const int q = b + lane;
+    const float e = q < c ? e_at(q) : 0.0f;
+    const double C = carry + wave_incl_scan_f64(q < L ? (double)e : 0.0);
+    if (b == 0) C0 = C;
+    if (topp) {
+      const double rel = (2.0 * q + 4.0) * 0x1p-24;
+      const bool lo_over = q < L && C / S_hi * (1.0 - rel) > (double)P.top_p;
+      const bool hi_over = q < L && C / S_lo * (1.0 + rel) > (double)P.top_p;
+      const uint64_t mh = bal64(hi_over);
+      if (mh != 0ull) {
+        const int fq = __ffsll((long long)mh) - 1;
+        if ((bal64(lo_over) >> fq) & 1ull)
+          cut = b + fq;
+        else
+          ok = false;
+      }
+    }
+    bool unc = false;
+    if (q < pe) {
+      const float eb = e_at(q + 1);
+      unc = e != eb && !(e > eb * (1.0f + 0x1p-21f));
+    }
+    if (bal64(unc) != 0ull) ok = false;
+    carry = readlane_f64(C, kWave - 1);
+  }
+  const int K = cut >= 0 ? min(L, cut) : L;
+  uint32_t token = c >= 1 ? id_at(0) : 0u, consumed = 0;  // indices[0]
+  if (ok && K > 0) {
+    // total and draw (sampler.zig:156-168): E = C_{K-1}; the draw stops at
+    // the first q with u E - C_q below -margin (none of them within it)
+    double E;
+    if (K <= kWave) {
+      E = readlane_f64(C0, K - 1);
+    } else {
+      E = 0.0;
+      for (int b = 0; b < K; b += kWave) {
+        const int q = b + lane;
+        E += readlane_f64(wave_incl_scan_f64(q < K ? (double)e_at(q) : 0.0), kWave - 1);
+      }
+    }
+    const double Au = (double)u * E;
+    const double margin = (4.0 * K + 16.0) * 0x1p-24 * E;
+    int st = -1;
+    double dcarry = 0.0;
+    for (int b = 0; b < K && st < 0 && ok; b += kWave) {
+      const int q = b + lane;
+      const double C = b == 0 ? C0 : dcarry + wave_incl_scan_f64(q < K ? (double)e_at(q) : 0.0);
+      const double dq = Au - C;
+      const bool unc = q < K && fabs(dq) <= margin;
+      const bool stp = q < K && dq < -margin;
+      const uint64_t mk = bal64(unc || stp);
+      if (mk != 0ull) {
+        const int fq = __ffsll((long long)mk) - 1;
+        if ((bal64(unc) >> fq) & 1ull)
+          ok = false;
+        else
+          st = b + fq;
+      }
+      dcarry = readlane_f64(C, kWave - 1);
+    }
+    consumed = 1;
+    if (st >= 0) token = id_at(st);
+  }
+  if (!ok) {
+    if (lane == 0) *tfail = 1u;
+    return;
+  }
+  if (Q.kept_ids)
+    for (int q = lane; q < K && q < P.kept_cap; q += kWave) Q.kept_ids[(int64_t)row * P.kept_cap + q] = id_at(q);
+  if (lane == 0) {
+    Q.tokens[row] = token;
+    if (Q.consumed) Q.consumed[row] = (uint8_t)consumed;
+    if (Q.kept_count) Q.kept_count[row] = (uint32_t)K;
+    if (Q.status) Q.status[row] = kPathTokenOnly;
+  }
+}
+
+}  // namespace llz

@@ -242,14 +242,18 @@ PATH_BUCKETS = 64  # full row without a sort: kept prefix, total and draw from p
 
 
 def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, post: Optional[LogitPost] = None,
-                kept_cap: int = 0, stats: bool = False, path: bool = False, workspace=None, stream=None,
-                out=None) -> SampleResult:
+                kept_cap: int = 0, probs: bool = True, stats: bool = False, path: bool = False, workspace=None,
+                stream=None, out=None) -> SampleResult:
     """Batched Sampler.sample over device rows.
 
     logits: float32 CUDA tensor [rows, vocab] (rows may be strided);
     uniforms: float32 CUDA tensor [rows]; prev_tokens: int32 CUDA tensor
     [n_prev] (shared) or [rows, n_prev].  Returns device tensors; the call is
-    asynchronous on ``stream`` (default: torch's current stream).
+    asynchronous on ``stream`` (default: torch's current stream).  With
+    kept_cap > 0 the kept ids (and, unless probs is False, their
+    probabilities) are returned; a call that asks for neither probabilities nor
+    row statistics may finish rows without the exact normaliser (the token,
+    draw flag, kept count and ids are the same either way).
     """
     torch = _torch()
     if not (logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2):
@@ -291,9 +295,10 @@ def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, post:
         ex.d_kept_count = res.kept_count.data_ptr()
         if kept_cap > 0:
             res.kept_ids = torch.full((rows, kept_cap), -1, dtype=torch.int32, device=dev)
-            res.kept_probs = torch.full((rows, kept_cap), float("nan"), dtype=torch.float32, device=dev)
             ex.d_kept_ids = res.kept_ids.data_ptr()
-            ex.d_kept_probs = res.kept_probs.data_ptr()
+            if probs:
+                res.kept_probs = torch.full((rows, kept_cap), float("nan"), dtype=torch.float32, device=dev)
+                ex.d_kept_probs = res.kept_probs.data_ptr()
             ex.kept_cap = kept_cap
         if stats:
             res.row_stats = torch.zeros((rows, 4), dtype=torch.float32, device=dev)

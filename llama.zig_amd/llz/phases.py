@@ -32,6 +32,7 @@ SLOTS = {
     23: "buckets: keys and coarse histogram", 24: "buckets: fine histogram", 25: "buckets: top-p classes",
     26: "buckets: top-p walk", 27: "buckets: draw classes", 28: "buckets: draw walk",
     29: "buckets (draw): sums", 30: "buckets (draw): first batch gathered", 31: "buckets (draw): first batch walked",
+    32: "token-only: candidate lanes queued", 33: "token-only: candidates evaluated", 34: "token-only: sorted",
 }
 # phases as (name, from slot, to slot)
 PHASES = [
@@ -48,6 +49,8 @@ PHASES = [
     ("buckets: top-p classes", 24, 25), ("buckets: top-p chain", 25, 26), ("buckets: draw classes", 26, 27),
     ("buckets: draw chain", 27, 28), ("buckets draw: sums", 27, 29), ("buckets draw: 1st gather+sort", 29, 30),
     ("buckets draw: 1st walk", 30, 31), ("buckets draw: rest", 31, 28),
+    ("token-only: scan", 2, 32), ("token-only: re-read and exact terms", 32, 33), ("token-only: sort", 33, 34),
+    ("token-only: decisions", 34, 15),
 ]
 
 
@@ -56,6 +59,7 @@ def main() -> int:
     ap.add_argument("--workload", default="headline")
     ap.add_argument("--rows", type=int, default=0, help="rows (default: the workload's batch)")
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--exact", action="store_true", help="ask for row statistics (the exact phases on every row)")
     a = ap.parse_args()
     os.environ["LLZ_LIBRARY"] = STAMP_LIB
     sys.path.insert(0, PKG)
@@ -71,7 +75,7 @@ def main() -> int:
     L.llz_debug_phase_stamps.argtypes = [C.c_void_p, C.c_int, C.c_int]
     L.llz_debug_phase_stamps.restype = C.c_int
     rows_st = min(rows, 4096)
-    buf = np.zeros((rows_st, 32), np.uint64)
+    buf = np.zeros((rows_st, 40), np.uint64)
     x = torch.from_numpy(w.logits(rows)).cuda()
     u = torch.from_numpy(llz.rng_uniforms(w.uniform_seed, rows)).cuda()
     cfg = llz.SamplerConfig.of(w.params)
@@ -79,7 +83,7 @@ def main() -> int:
     for _ in range(a.reps):
         assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 1) == 0
         torch.cuda.synchronize()
-        res = llz.sample_rows(x, cfg, u, path=True)
+        res = llz.sample_rows(x, cfg, u, path=True, stats=a.exact)
         torch.cuda.synchronize()
     assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 0) == 0
     paths = res.row_path.cpu().numpy()

