@@ -753,7 +753,8 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   // estimate does (estimates are within 2^-16 of the terms, and no term
   // exceeds its segment's sum), re-read and evaluated exactly; the list lies
   // in F.v, free once every wave has read the segment sums below.
-  if (tok && !nanrow && fabsf(m) <= 3.0e38f) {
+  if (tok && !nanrow && fabsf(m) <= 3.0e38f && P.cand_theta > 0.0f) {
+    LLZ_STAMP(row, 38);
     float s_est = 0.0f;
     bool tbad = false;
 #pragma unroll
@@ -772,22 +773,34 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         F.tcand = 0u;
         F.tfail = 0u;
       }
-      int tq = 0;
-      auto tscan = [&](const int k, const float4 q) {
-        const bool c = lane4 < seg_lim(k) && max3_raw(max3_raw(q.x, q.y, q.z), q.w, q.w) >= thr_q;
-        const uint64_t bm = bal64(c);
-        if (bm != 0ull) {
-          const int slot = tq + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
-          if (c && slot < QCAP) F.qpos[w][slot] = (uint32_t)((w + W * k) * SEG + lane4);
-          tq += __popcll(bm);
-        }
+      // the lane's candidate segments as a bit mask, then its positions at
+      // its place in the wave's queue.  Positions outside the row hold q = 0,
+      // below thr_q > 0.  The register segments without a branch, the
+      // LDS-resident ones where the segment's sum passes
+      uint32_t lm_lo = 0u, lm_hi = 0u;
+      auto tflag = [&](const int k, const float4 q) {
+        const uint32_t c = max3_raw(max3_raw(q.x, q.y, q.z), q.w, q.w) >= thr_q ? 1u : 0u;
+        if (k < 32)
+          lm_lo |= c << k;
+        else
+          lm_hi |= c << (k - 32);
       };
 #pragma unroll
-      for (int k = 0; k < KV; ++k)
-        if ((segm >> k) & 1ull) tscan(k, d[k]);
+      for (int k = 0; k < KV; ++k) tflag(k, d[k]);
       for (uint64_t rest = segm >> KV; rest != 0ull; rest &= rest - 1ull) {
         const int k = KV + __ffsll((long long)rest) - 1;
-        tscan(k, *reinterpret_cast<const float4*>(&F.u.data[w][k - KV][lane * 4]));
+        const float4 q = *reinterpret_cast<const float4*>(&F.u.data[w][k - KV][lane * 4]);
+        const uint32_t c = max3_raw(max3_raw(q.x, q.y, q.z), q.w, q.w) >= thr_q ? 1u : 0u;
+        lm_hi |= c << (k - 32);  // k >= KV > 32
+      }
+      uint64_t lm = ((uint64_t)lm_hi << 32) | lm_lo;
+      LLZ_STAMP(row, 39);
+      const uint32_t nb = (uint32_t)__popcll(lm);
+      const uint32_t nb_in = wave_incl_scan_op(nb, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+      const int tq = (int)readlane_u32(nb_in, kWave - 1);
+      for (uint32_t slot = nb_in - nb; lm != 0ull; lm &= lm - 1ull, ++slot) {
+        const int k = __ffsll((long long)lm) - 1;
+        if (slot < (uint32_t)QCAP) F.qpos[w][slot] = (uint32_t)((w + W * k) * SEG + lane4);
       }
       float4 tv[QCAP / kWave];
 #pragma unroll
@@ -816,7 +829,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
           }
         }
       }
-      __syncthreads();
+      lds_barrier();  // the list complete (LDS only: the re-reads were consumed above)
       LLZ_STAMP(row, 33);
       const int tc = (int)F.tcand;
       if (tc <= kTokCap && F.tfail == 0u) {
@@ -826,7 +839,9 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       } else if (t == 0) {
         F.tfail = 1u;
       }
-      __syncthreads();
+      // LDS only: the outputs' global stores need not land before the
+      // workgroup ends
+      lds_barrier();
       if (F.tfail == 0u) {
         LLZ_STAMP(row, 15);
         return;

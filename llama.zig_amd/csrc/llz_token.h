@@ -88,13 +88,19 @@ __device__ __forceinline__ double wave_incl_scan_f64(double x) {
 // instead when a decision does not hold over the interval of S.
 // Out of line; the launch's arguments come through the kernel's argument
 // segment (as the other out-of-line paths take them).
-__device__ __noinline__ void token_select(const KArgs* A, int row, const uint64_t* srt, int c, float s_est, float u,
+__device__ __forceinline__ void token_select(const KArgs* A, int row, const uint64_t* srt, int c, float s_est, float u,
                                           float theta, uint32_t* tfail) {
   const RowParams& P = A->P;
   const RowPtrs& Q = A->Q;
   const int lane = lane_id();
   const int n = P.n;
-  auto e_at = [&](int q) { return __uint_as_float(~(uint32_t)(srt[q] >> 32)); };
+  // the first kWave + 1 keys, read once: lane q holds keys q and q + 1
+  // (lists of at most kWave, the common case, read nothing more)
+  const uint64_t k0 = lane < c ? srt[lane] : ~0ull;
+  const uint64_t k1 = lane + 1 < c ? srt[lane + 1] : ~0ull;
+  auto e_of = [](uint64_t k) { return __uint_as_float(~(uint32_t)(k >> 32)); };
+  auto e_at = [&](int q) { return q < kWave ? e_of(k0) : e_of(srt[q]); };  // q: this lane's own position
+  auto e_next = [&](int q) { return q < kWave ? e_of(k1) : e_of(srt[q + 1]); };
   auto id_at = [&](int q) { return (uint32_t)srt[q]; };
   bool ok = c >= 1;
   // certified prefix M: list terms clear of every term outside the list
@@ -114,6 +120,7 @@ __device__ __noinline__ void token_select(const KArgs* A, int row, const uint64_
     if (mp && bal64(inM && !(e > mp_hi) && !(e < mp_lo)) != 0ull) ok = false;
   }
   if (!mp) Km = n;
+  LLZ_STAMP(row, 35);
   const int Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
   const int L = min(Kk, Km);
   if (L > M) ok = false;
@@ -121,7 +128,9 @@ __device__ __noinline__ void token_select(const KArgs* A, int row, const uint64_
   const double g = (double)(n - 1) * 0x1p-24;
   const double gr = g / (1.0 - g) + 0x1p-14;
   const double S_lo = (double)s_est * (1.0 - gr), S_hi = (double)s_est * (1.0 + gr);
-  if (!(S_lo > 0.0)) ok = false;
+  if (!(S_lo > 0.0) || !(S_hi < 1.0e300)) ok = false;
+  // 1/S at the interval's ends, rounded outwards (one rounding of 2^-53 each)
+  const double iS_hi = (1.0 / S_hi) * (1.0 - 0x1p-50), iS_lo = (1.0 / S_lo) * (1.0 + 0x1p-50);
   const bool topp = P.top_p > 0.0f && P.top_p < 1.0f;
   // one pass over positions [0, L): the running sums C_q of the terms
   // (double), top-p's cut (sampler.zig:111-118), and the order: adjacent terms
@@ -137,8 +146,8 @@ __device__ __noinline__ void token_select(const KArgs* A, int row, const uint64_
     if (b == 0) C0 = C;
     if (topp) {
       const double rel = (2.0 * q + 4.0) * 0x1p-24;
-      const bool lo_over = q < L && C / S_hi * (1.0 - rel) > (double)P.top_p;
-      const bool hi_over = q < L && C / S_lo * (1.0 + rel) > (double)P.top_p;
+      const bool lo_over = q < L && C * iS_hi * (1.0 - rel) > (double)P.top_p;
+      const bool hi_over = q < L && C * iS_lo * (1.0 + rel) > (double)P.top_p;
       const uint64_t mh = bal64(hi_over);
       if (mh != 0ull) {
         const int fq = __ffsll((long long)mh) - 1;
@@ -150,14 +159,15 @@ __device__ __noinline__ void token_select(const KArgs* A, int row, const uint64_
     }
     bool unc = false;
     if (q < pe) {
-      const float eb = e_at(q + 1);
+      const float eb = e_next(q);
       unc = e != eb && !(e > eb * (1.0f + 0x1p-21f));
     }
     if (bal64(unc) != 0ull) ok = false;
     carry = readlane_f64(C, kWave - 1);
   }
   const int K = cut >= 0 ? min(L, cut) : L;
-  uint32_t token = c >= 1 ? id_at(0) : 0u, consumed = 0;  // indices[0]
+  LLZ_STAMP(row, 36);
+  uint32_t token = c >= 1 ? readlane_u32((uint32_t)k0, 0) : 0u, consumed = 0;  // indices[0]
   if (ok && K > 0) {
     // total and draw (sampler.zig:156-168): E = C_{K-1}; the draw stops at
     // the first q with u E - C_q below -margin (none of them within it)
@@ -192,14 +202,16 @@ __device__ __noinline__ void token_select(const KArgs* A, int row, const uint64_
       dcarry = readlane_f64(C, kWave - 1);
     }
     consumed = 1;
-    if (st >= 0) token = id_at(st);
+    if (st >= 0) token = st < kWave ? readlane_u32((uint32_t)k0, st) : id_at(st);
   }
+  LLZ_STAMP(row, 37);
   if (!ok) {
     if (lane == 0) *tfail = 1u;
     return;
   }
   if (Q.kept_ids)
-    for (int q = lane; q < K && q < P.kept_cap; q += kWave) Q.kept_ids[(int64_t)row * P.kept_cap + q] = id_at(q);
+    for (int q = lane; q < K && q < P.kept_cap; q += kWave)
+      Q.kept_ids[(int64_t)row * P.kept_cap + q] = q < kWave ? (uint32_t)k0 : id_at(q);
   if (lane == 0) {
     Q.tokens[row] = token;
     if (Q.consumed) Q.consumed[row] = (uint8_t)consumed;

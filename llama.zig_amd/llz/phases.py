@@ -33,6 +33,8 @@ SLOTS = {
     26: "buckets: top-p walk", 27: "buckets: draw classes", 28: "buckets: draw walk",
     29: "buckets (draw): sums", 30: "buckets (draw): first batch gathered", 31: "buckets (draw): first batch walked",
     32: "token-only: candidate lanes queued", 33: "token-only: candidates evaluated", 34: "token-only: sorted",
+    38: "token-only: row maximum read", 39: "token-only: candidate segments scanned",
+    35: "token-only: prefix and min-p counted", 36: "token-only: top-p and order checked", 37: "token-only: drawn",
 }
 # phases as (name, from slot, to slot)
 PHASES = [
@@ -49,8 +51,10 @@ PHASES = [
     ("buckets: top-p classes", 24, 25), ("buckets: top-p chain", 25, 26), ("buckets: draw classes", 26, 27),
     ("buckets: draw chain", 27, 28), ("buckets draw: sums", 27, 29), ("buckets draw: 1st gather+sort", 29, 30),
     ("buckets draw: 1st walk", 30, 31), ("buckets draw: rest", 31, 28),
-    ("token-only: scan", 2, 32), ("token-only: re-read and exact terms", 32, 33), ("token-only: sort", 33, 34),
-    ("token-only: decisions", 34, 15),
+    ("token-only: scan", 2, 32), ("M start (max, barrier)", 1, 38), ("token: estimate + scan", 38, 39),
+    ("token: queue + loads issued + barrier", 39, 32), ("token-only: re-read and exact terms", 32, 33), ("token-only: sort", 33, 34),
+    ("token-only: decisions", 34, 15), ("decisions: entry + counts", 34, 35), ("decisions: top-p + order", 35, 36),
+    ("decisions: draw", 36, 37), ("decisions: outputs + barrier", 37, 15),
 ]
 
 
@@ -60,6 +64,9 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=0, help="rows (default: the workload's batch)")
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--exact", action="store_true", help="ask for row statistics (the exact phases on every row)")
+    ap.add_argument("--dump", default="", help="also save every row's raw timestamps (.npy)")
+    ap.add_argument("--chain", type=int, default=1,
+                    help="launches back to back before reading (the last one's stamps, as in a benchmark loop)")
     a = ap.parse_args()
     os.environ["LLZ_LIBRARY"] = STAMP_LIB
     sys.path.insert(0, PKG)
@@ -83,9 +90,12 @@ def main() -> int:
     for _ in range(a.reps):
         assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 1) == 0
         torch.cuda.synchronize()
-        res = llz.sample_rows(x, cfg, u, path=True, stats=a.exact)
+        for _ in range(a.chain):
+            res = llz.sample_rows(x, cfg, u, path=True, stats=a.exact)
         torch.cuda.synchronize()
     assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 0) == 0
+    if a.dump:
+        np.save(a.dump, buf)
     paths = res.row_path.cpu().numpy()
     st = buf.astype(np.int64)
     t0 = st[:, 0][st[:, 0] > 0].min()
