@@ -290,7 +290,11 @@ __device__ float row_normaliser(const Src& X, int n, const RowParams& P, SampleS
     const int sb = gb + w * kSlice;
     int c0 = 0;        // first sub-chunk not yet added
     int dn = -1;       // positions of sub-chunk c0 already added (resolution in progress)
-    bool first = true;
+    // once the list has overflowed (the selection then reads the whole row
+    // and never the list), candidates stop being special: their roundings
+    // come from the estimates like every other element's (a wave reading
+    // the count while others still push sees a smaller count at worst)
+    bool first = __builtin_amdgcn_readfirstlane((int)sh.cand_count) <= kCap;
     for (;;) {  // (re)build the state for the grid of s
       const int jb = grid_of(s).j;
       slice_state(vcur, sb, n, m, P, t1, jb, first, max(0, c0 - w * kSub), sh, S);
