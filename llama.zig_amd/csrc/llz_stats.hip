@@ -716,6 +716,65 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     }
   }
   mx = wave_max_f32(mx);
+  // token-only rows: the lanes that may hold a candidate (a term that may
+  // reach thr_e; Rw scales this wave's estimates q to terms), queued in
+  // F.qpos[w] and re-read into tv.  The segments whose estimated sum reaches
+  // thr_e, then their lanes holding an estimate that does (estimates are
+  // within 2^-16 of the terms, no term exceeds its segment's sum, positions
+  // outside the row hold q = 0).  Returns the number of lanes found; none
+  // beyond QCAP is re-read.
+  float4 tv[QCAP / kWave];
+  auto tqueue = [&](const float Rw, const float thr_e) -> int {
+    const uint64_t segm = bal64(lane < nseg_w && my_a * Rw >= thr_e);
+    const float thr_q = thr_e / Rw;
+    // the lane's candidate segments as a bit mask: the register segments
+    // without a branch, the LDS-resident ones where the segment's sum passes
+    uint32_t lm_lo = 0u, lm_hi = 0u;
+    auto tflag = [&](const int k, const float4 q) {
+      const uint32_t c = max3_raw(max3_raw(q.x, q.y, q.z), q.w, q.w) >= thr_q ? 1u : 0u;
+      if (k < 32)
+        lm_lo |= c << k;
+      else
+        lm_hi |= c << (k - 32);
+    };
+#pragma unroll
+    for (int k = 0; k < KV; ++k) tflag(k, d[k]);
+    for (uint64_t rest = segm >> KV; rest != 0ull; rest &= rest - 1ull) {
+      const int k = KV + __ffsll((long long)rest) - 1;
+      const float4 q = *reinterpret_cast<const float4*>(&F.u.data[w][k - KV][lane * 4]);
+      const uint32_t c = max3_raw(max3_raw(q.x, q.y, q.z), q.w, q.w) >= thr_q ? 1u : 0u;
+      lm_hi |= c << (k - 32);  // k >= KV > 32
+    }
+    uint64_t lm = ((uint64_t)lm_hi << 32) | lm_lo;
+    const uint32_t nb = (uint32_t)__popcll(lm);
+    const uint32_t nb_in = wave_incl_scan_op(nb, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+    const int nq = (int)readlane_u32(nb_in, kWave - 1);
+    for (uint32_t slot = nb_in - nb; lm != 0ull; lm &= lm - 1ull, ++slot) {
+      const int k = __ffsll((long long)lm) - 1;
+      if (slot < (uint32_t)QCAP) F.qpos[w][slot] = (uint32_t)((w + W * k) * SEG + lane4);
+    }
+    __builtin_amdgcn_wave_barrier();  // this wave's own queue: LDS order suffices
+#pragma unroll
+    for (int h = 0; h < QCAP / kWave; ++h) {
+      const int i = h * kWave + lane;
+      const int pos = i < min(nq, QCAP) ? (int)F.qpos[w][i] : 0;
+      tv[h] = X.fix4(pos, FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n), n);
+    }
+    return nq;
+  };
+  // queued now against this wave's own maximum (m >= mx, so a superset of
+  // the lanes against the row's; the threshold lowered by 2^-12 more covers
+  // the roundings of R), the re-reads in flight while the other waves finish
+  // their loads; a wave whose superset overflows the queue scans again
+  // against the row's maximum after the barrier
+  int tq = -1;
+  if (tok && l2e_t > 0.0f) {
+    const float aw = fmaf(mx, -l2e_t, cw);
+    if (fabsf(aw) <= 64.0f) {
+      const int q0 = tqueue(__builtin_amdgcn_exp2f(aw), P.cand_theta * (1.0f - 0x1p-10f) * (1.0f - 0x1p-12f));
+      if (q0 <= QCAP) tq = q0;
+    }
+  }
   const bool wnan = bal64(nanf != 0u) != 0ull;
   if (lane == 0) {
     F.mw[w] = mx;
@@ -733,7 +792,14 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     F.done = 0;
     F.diag = 0;
   }
-  __syncthreads();
+  if constexpr (FASTLD) {
+    // every load of the row has landed (the register segments, issued after
+    // the LDS-resident ones, were consumed): the barrier orders LDS only, and
+    // a token-only row's re-reads stay in flight across it
+    lds_barrier();
+  } else {
+    __syncthreads();
+  }
   LLZ_STAMP(row, 1);
 
   // ---- phase M: row maximum, scale factors, binade prediction, first slots
@@ -767,48 +833,12 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       const float Rw_t = __builtin_amdgcn_exp2f(fmaf(m, -l2e_t, cw));
       const float theta_t = P.cand_theta;
       const float thr_e = theta_t * (1.0f - 0x1p-10f);
-      const uint64_t segm = bal64(lane < nseg_w && my_a * Rw_t >= thr_e);
-      const float thr_q = thr_e / Rw_t;  // q R_w ~ e
       if (t == 0) {
         F.tcand = 0u;
         F.tfail = 0u;
       }
-      // the lane's candidate segments as a bit mask, then its positions at
-      // its place in the wave's queue.  Positions outside the row hold q = 0,
-      // below thr_q > 0.  The register segments without a branch, the
-      // LDS-resident ones where the segment's sum passes
-      uint32_t lm_lo = 0u, lm_hi = 0u;
-      auto tflag = [&](const int k, const float4 q) {
-        const uint32_t c = max3_raw(max3_raw(q.x, q.y, q.z), q.w, q.w) >= thr_q ? 1u : 0u;
-        if (k < 32)
-          lm_lo |= c << k;
-        else
-          lm_hi |= c << (k - 32);
-      };
-#pragma unroll
-      for (int k = 0; k < KV; ++k) tflag(k, d[k]);
-      for (uint64_t rest = segm >> KV; rest != 0ull; rest &= rest - 1ull) {
-        const int k = KV + __ffsll((long long)rest) - 1;
-        const float4 q = *reinterpret_cast<const float4*>(&F.u.data[w][k - KV][lane * 4]);
-        const uint32_t c = max3_raw(max3_raw(q.x, q.y, q.z), q.w, q.w) >= thr_q ? 1u : 0u;
-        lm_hi |= c << (k - 32);  // k >= KV > 32
-      }
-      uint64_t lm = ((uint64_t)lm_hi << 32) | lm_lo;
+      if (tq < 0) tq = tqueue(Rw_t, thr_e);
       LLZ_STAMP(row, 39);
-      const uint32_t nb = (uint32_t)__popcll(lm);
-      const uint32_t nb_in = wave_incl_scan_op(nb, 0u, [](uint32_t a, uint32_t b) { return a + b; });
-      const int tq = (int)readlane_u32(nb_in, kWave - 1);
-      for (uint32_t slot = nb_in - nb; lm != 0ull; lm &= lm - 1ull, ++slot) {
-        const int k = __ffsll((long long)lm) - 1;
-        if (slot < (uint32_t)QCAP) F.qpos[w][slot] = (uint32_t)((w + W * k) * SEG + lane4);
-      }
-      float4 tv[QCAP / kWave];
-#pragma unroll
-      for (int h = 0; h < QCAP / kWave; ++h) {
-        const int i = h * kWave + lane;
-        const int pos = i < min(tq, QCAP) ? (int)F.qpos[w][i] : 0;
-        tv[h] = X.fix4(pos, FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n), n);
-      }
       lds_barrier();  // F.tcand / F.tfail cleared
       LLZ_STAMP(row, 32);
       if (tq > QCAP && lane == 0) atomicOr(&F.tfail, 1u);
