@@ -252,9 +252,12 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   P.src_stride = src_stride;
   P.orig_stride = row_stride;
   // the token alone: no probabilities and no row statistics asked for, and no
-  // typical-p (its entropy needs the exact normaliser)
+  // typical-p (its entropy needs the exact normaliser).  Only with a candidate
+  // threshold of at least 2^-10 (a min-p filter): below it the candidates
+  // (every term within 11 nats of the maximum, without min-p) rarely fit the
+  // token path's list, and a row that does not fit pays for the attempt
   const bool tok_only = !(extras && (extras->d_kept_probs || extras->d_row_stats)) &&
-                        !(cfg->typical_p > 0.0f && cfg->typical_p < 1.0f);
+                        !(cfg->typical_p > 0.0f && cfg->typical_p < 1.0f) && P.cand_theta >= 0x1p-10f;
   P.flags = (cfg->temperature == 1.0f ? kFlagTIsOne : 0u) | (vec ? kFlagVecSrc : 0u) | kFlagFallback |
             (tok_only ? kFlagTokenOnly : 0u);
   P.xf_src = xf_src;

@@ -754,11 +754,17 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       if (slot < (uint32_t)QCAP) F.qpos[w][slot] = (uint32_t)((w + W * k) * SEG + lane4);
     }
     __builtin_amdgcn_wave_barrier();  // this wave's own queue: LDS order suffices
+    // an overflowing queue fails the row: no re-reads for it
+    if (nq <= QCAP) {
 #pragma unroll
-    for (int h = 0; h < QCAP / kWave; ++h) {
-      const int i = h * kWave + lane;
-      const int pos = i < min(nq, QCAP) ? (int)F.qpos[w][i] : 0;
-      tv[h] = X.fix4(pos, FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n), n);
+      for (int h = 0; h < QCAP / kWave; ++h) {
+        const int i = h * kWave + lane;
+        const int pos = i < nq ? (int)F.qpos[w][i] : 0;
+        tv[h] = X.fix4(pos, FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n), n);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < QCAP / kWave; ++h) tv[h] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     return nq;
   };
@@ -846,7 +852,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
 #pragma unroll
       for (int h = 0; h < QCAP / kWave; ++h) {
         const int i = h * kWave + lane;
-        if (i < min(tq, QCAP)) {
+        if (tq <= QCAP && i < tq) {
           const int pos = (int)F.qpos[w][i];
           const float4 e = exact_terms4(tv[h], m, P.temperature, t1);  // sampler.zig:85
           const float es[4] = {e.x, e.y, e.z, e.w};

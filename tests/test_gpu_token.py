@@ -129,3 +129,25 @@ def test_token_only_kept_ids_without_cap(cuda):
     ot, oc, _ = O.sample_rows(x, w.params, u, threads=8)
     assert np.array_equal(tok, ot)
     assert np.array_equal(con, oc)
+
+
+@pytest.mark.parametrize("kind", ["flat", "many"])
+def test_token_only_overflow_falls_back(cuda, kind):
+    """Min-p rows whose candidates overflow the token path: a flat row (its
+    candidate lanes overflow every wave's queue) and 300 terms near the
+    maximum over a low floor (the lanes fit, the 256-entry list does not).
+    The exact phases follow, with the oracle's results."""
+    w = WORKLOADS["headline"]
+    rows = 4
+    rng = np.random.default_rng(7)
+    if kind == "flat":
+        x = rng.normal(0.0, 0.3, size=(rows, w.vocab)).astype(np.float32)
+    else:
+        x = rng.normal(-30.0, 1.0, size=(rows, w.vocab)).astype(np.float32)
+        for r in range(rows):
+            idx = rng.choice(w.vocab, 300, replace=False)
+            x[r, idx] = rng.uniform(-1.0, 0.0, 300).astype(np.float32)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    g = _run(cuda, x, w.params, u, cap=256)
+    assert not np.any(g["path"] & PATH_TOKEN_ONLY)
+    _check_oracle(x, w.params, u, g)
