@@ -849,18 +849,80 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       LLZ_STAMP(row, 32);
       if (tq > QCAP && lane == 0) atomicOr(&F.tfail, 1u);
       uint64_t* const tl = reinterpret_cast<uint64_t*>(&F.v);  // [kTokCap] collected, then [kTokCap] sorted
+      // The queued lanes' elements that may be candidates: the lane test
+      // (tqueue against the row's maximum) element by element, on the same
+      // estimates exp2(fma(v, l2e_t, -cw)) phase L computed.  When a wave
+      // has at most 64 of them, they are staged in its queue row as (logit,
+      // position) pairs and each lane evaluates one exact term; one LDS
+      // atomic per wave reserves its list slots.  Otherwise every queued
+      // lane evaluates its four terms.
+      constexpr int NH = QCAP / kWave;
+      int tpos[NH];
+      uint32_t tmk[NH];
+      uint32_t tcnt = 0u;
+      const float thr_q = thr_e / Rw_t;
 #pragma unroll
-      for (int h = 0; h < QCAP / kWave; ++h) {
+      for (int h = 0; h < NH; ++h) {
         const int i = h * kWave + lane;
-        if (tq <= QCAP && i < tq) {
-          const int pos = (int)F.qpos[w][i];
-          const float4 e = exact_terms4(tv[h], m, P.temperature, t1);  // sampler.zig:85
-          const float es[4] = {e.x, e.y, e.z, e.w};
+        const bool live = tq <= QCAP && i < tq;
+        tpos[h] = live ? (int)F.qpos[w][i] : 0;
+        const float vs[4] = {tv[h].x, tv[h].y, tv[h].z, tv[h].w};
+        uint32_t mk = 0u;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bool pass = live && tpos[h] + c < n && __builtin_amdgcn_exp2f(fmaf(vs[c], l2e_t, -cw)) >= thr_q;
+          mk |= pass ? (1u << c) : 0u;
+        }
+        tmk[h] = mk;
+        tcnt += (uint32_t)__popc(mk);
+      }
+      const uint32_t tinc = wave_incl_scan_op(tcnt, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+      const int ttot = (int)readlane_u32(tinc, kWave - 1);
+      if (ttot <= kWave) {
+        uint32_t* const sg = &F.qpos[w][0];  // [64][2]: this wave's row, read above (LDS order suffices)
+        __builtin_amdgcn_wave_barrier();
+        uint32_t o = tinc - tcnt;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+          const float vs[4] = {tv[h].x, tv[h].y, tv[h].z, tv[h].w};
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
-            if (pos + c < n && es[c] >= theta_t) {
-              const uint32_t slot = atomicAdd(&F.tcand, 1u);
-              if (slot < (uint32_t)kTokCap) tl[slot] = ((uint64_t)(~__float_as_uint(es[c])) << 32) | (uint32_t)(pos + c);
+            if ((tmk[h] >> c) & 1u) {
+              sg[2 * o] = __float_as_uint(vs[c]);
+              sg[2 * o + 1] = (uint32_t)(tpos[h] + c);
+              ++o;
+            }
+          }
+        }
+        __builtin_amdgcn_wave_barrier();
+        float e = 0.0f;
+        uint32_t id = 0u;
+        if (lane < ttot) {
+          id = sg[2 * lane + 1];
+          e = exact_term(__uint_as_float(sg[2 * lane]), m, P.temperature, t1);  // sampler.zig:85
+        }
+        const bool cand = lane < ttot && e >= theta_t;
+        const uint64_t cb = bal64(cand);
+        if (cb != 0ull) {
+          uint32_t base = 0u;
+          if (lane == 0) base = atomicAdd(&F.tcand, (uint32_t)__popcll(cb));
+          base = readlane_u32(base, 0);
+          const uint32_t slot = base + (uint32_t)__popcll(cb & lt_mask);
+          if (cand && slot < (uint32_t)kTokCap) tl[slot] = ((uint64_t)(~__float_as_uint(e)) << 32) | id;
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+          if (tmk[h] != 0u) {
+            const int pos = tpos[h];
+            const float4 e = exact_terms4(tv[h], m, P.temperature, t1);  // sampler.zig:85
+            const float es[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              if (pos + c < n && es[c] >= theta_t) {
+                const uint32_t slot = atomicAdd(&F.tcand, 1u);
+                if (slot < (uint32_t)kTokCap) tl[slot] = ((uint64_t)(~__float_as_uint(es[c])) << 32) | (uint32_t)(pos + c);
+              }
             }
           }
         }
