@@ -180,7 +180,7 @@ def run_workload(name: str, steps: int, warmup: int, args) -> dict:
     path_fracs = {"stream_norm": frac(llz.PATH_STREAM_NORM), "full_sort": frac(llz.PATH_FULL_SORT),
                   "entropy": frac(llz.PATH_ENTROPY), "sum_le0": frac(llz.PATH_SUM_LE0),
                   "walk_rounds": frac(llz.PATH_WALK_ROUNDS), "resolve_generic": frac(llz.PATH_RESOLVE_GENERIC),
-                  "buckets": frac(llz.PATH_BUCKETS),
+                  "buckets": frac(llz.PATH_BUCKETS), "token_only": frac(llz.PATH_TOKEN_ONLY),
                   "single_pass": round(float(np.mean((paths & (llz.PATH_STREAM_NORM | llz.PATH_FULL_SORT)) == 0)), 4)}
 
     # The timed region: K steps back to back on one stream, bracketed by HIP
