@@ -931,7 +931,8 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       LLZ_STAMP(row, 33);
       const int tc = (int)F.tcand;
       if (tc <= kTokCap && F.tfail == 0u) {
-        token_sort(tl, tl + kTokCap, reinterpret_cast<uint32_t*>(&F.qpos[0][0]), tc);
+        static_assert(sizeof(F.qpos) >= (size_t)(kNT / kWave) * kTokCap * sizeof(uint16_t), "partial ranks fit the queue rows");
+        token_sort(tl, tl + kTokCap, reinterpret_cast<uint16_t*>(&F.qpos[0][0]), tc);
         LLZ_STAMP(row, 34);
         if (w == 0) token_select(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, u_row, theta_t, &F.tfail);
       } else if (t == 0) {

@@ -34,23 +34,31 @@ namespace llz {
 
 constexpr int kTokCap = 256;  // candidates of a token-only row at most
 
-// Rank sort of c distinct keys (e desc as ~bits, id asc) by the whole
-// workgroup: wave w counts against its eighth of the list.
-__device__ __forceinline__ void token_sort(const uint64_t* in, uint64_t* out, uint32_t* rank, int c) {
+// Rank sort of c <= kTokCap distinct keys (e desc as ~bits, id asc) for
+// wave 0: wave w counts, for every key, the keys of its eighth of the list
+// below it (part[w][i], no clearing needed); after one barrier wave 0 adds
+// the eight counts and places each key.  Only wave 0 reads `out` (in LDS
+// order after its own writes).
+__device__ __forceinline__ void token_sort(const uint64_t* in, uint64_t* out, uint16_t* part, int c) {
   constexpr int NW = kNT / kWave;
-  const int t = (int)threadIdx.x, lane = lane_id(), w = wave_id();
-  for (int i = t; i < c; i += kNT) rank[i] = 0u;
-  lds_barrier();
+  const int lane = lane_id(), w = wave_id();
   const int j0 = (w * c) / NW, j1 = ((w + 1) * c) / NW;
   for (int i = lane; i < c; i += kWave) {
     const uint64_t ki = in[i];
     uint32_t r = 0;
     for (int j = j0; j < j1; ++j) r += in[j] < ki ? 1u : 0u;
-    if (r != 0u) atomicAdd(&rank[i], r);
+    part[w * kTokCap + i] = (uint16_t)r;
   }
   lds_barrier();
-  for (int i = t; i < c; i += kNT) out[rank[i]] = in[i];
-  lds_barrier();
+  if (w == 0) {
+    for (int i = lane; i < c; i += kWave) {
+      uint32_t r = 0;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) r += part[v * kTokCap + i];
+      out[r] = in[i];
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
 }
 
 __device__ __forceinline__ double readlane_f64(double v, int l) {
