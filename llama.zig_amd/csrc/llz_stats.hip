@@ -797,6 +797,8 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     F.s_run = 0.0f;
     F.done = 0;
     F.diag = 0;
+    F.tcand = 0u;  // the token-only list (ordered before its atomics by the barrier below)
+    F.tfail = 0u;
   }
   if constexpr (FASTLD) {
     // every load of the row has landed (the register segments, issued after
@@ -839,13 +841,8 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       const float Rw_t = __builtin_amdgcn_exp2f(fmaf(m, -l2e_t, cw));
       const float theta_t = P.cand_theta;
       const float thr_e = theta_t * (1.0f - 0x1p-10f);
-      if (t == 0) {
-        F.tcand = 0u;
-        F.tfail = 0u;
-      }
       if (tq < 0) tq = tqueue(Rw_t, thr_e);
       LLZ_STAMP(row, 39);
-      lds_barrier();  // F.tcand / F.tfail cleared
       LLZ_STAMP(row, 32);
       if (tq > QCAP && lane == 0) atomicOr(&F.tfail, 1u);
       uint64_t* const tl = reinterpret_cast<uint64_t*>(&F.v);  // [kTokCap] collected, then [kTokCap] sorted
