@@ -151,3 +151,25 @@ def test_token_only_overflow_falls_back(cuda, kind):
     g = _run(cuda, x, w.params, u, cap=256)
     assert not np.any(g["path"] & PATH_TOKEN_ONLY)
     _check_oracle(x, w.params, u, g)
+
+
+def test_token_only_wave_with_many_candidates(cuda):
+    """About 100 terms near the maximum, all in one wave's segments (segment
+    g belongs to wave g mod 8), over a low floor: that wave has more than 64
+    candidate elements, so it evaluates its queued lanes' four terms each
+    instead of staging one element per lane.  The list (100 terms) fits and
+    the rows still certify on the token path."""
+    w = WORKLOADS["headline"]
+    rows = 6
+    rng = np.random.default_rng(11)
+    x = rng.normal(-30.0, 1.0, size=(rows, w.vocab)).astype(np.float32)
+    pos = np.arange(w.vocab)
+    for r in range(rows):
+        wave = r % 8
+        own = pos[((pos // 256) % 8) == wave]
+        idx = rng.choice(own, 90 + 5 * r, replace=False)
+        x[r, idx] = rng.uniform(-1.0, 0.0, idx.size).astype(np.float32)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    g = _run(cuda, x, w.params, u)
+    assert np.all(g["path"] & PATH_TOKEN_ONLY), f"rows off the token path: {g['path']}"
+    _check_oracle(x, w.params, u, g)
