@@ -162,10 +162,6 @@ def run_workload(name: str, steps: int, warmup: int, args) -> dict:
         b = i % nbuf
         llz.sample_rows(xs[b], cfg, us[b], workspace=ws, stream=stream, out=(tokens, consumed))
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-
     # parity spot check of the timed configuration against the oracle, and
     # the path each row of every buffer takes
     res = llz.sample_rows(xs[0], cfg, us[0], path=True, workspace=ws, stream=stream)
@@ -183,20 +179,29 @@ def run_workload(name: str, steps: int, warmup: int, args) -> dict:
                   "buckets": frac(llz.PATH_BUCKETS), "token_only": frac(llz.PATH_TOKEN_ONLY),
                   "single_pass": round(float(np.mean((paths & (llz.PATH_STREAM_NORM | llz.PATH_FULL_SORT)) == 0)), 4)}
 
-    # The timed region: K steps back to back on one stream, bracketed by HIP
+    # W untimed warmup steps right before the timed region (after the spot
+    # check, whose host work leaves the GPU idle), a synchronisation, then the
+    # timed region: K steps back to back on one stream, bracketed by HIP
     # events on that stream.  k_stats is the only kernel of a step, so the
     # events' interval over K is its average launch duration (the host
     # enqueues faster than the GPU runs, so launches follow each other with
-    # no idle gap).
+    # no idle gap).  The first dispatch after the synchronisation's idle gap
+    # runs about 12 us longer than the others (kernel trace of this command),
+    # so one untimed lead-in step goes ahead of the start event: the events
+    # time exactly the K steps, and the wall clock (from the synchronisation
+    # on) includes the lead-in, so ms_per_step and value err on the slow side.
     cb = torch.cuda.Event(enable_timing=True)
     ce = torch.cuda.Event(enable_timing=True)
     for ev in (cb, ce):  # materialise the underlying HIP events
         ev.record(stream)
+    for i in range(warmup):
+        step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    step(warmup)  # the lead-in (untimed by the events)
     cb.record(stream)
     for i in range(steps):
-        step(warmup + i)
+        step(warmup + 1 + i)
     ce.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()

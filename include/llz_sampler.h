@@ -91,14 +91,25 @@ typedef struct llz_sample_extras {
     uint32_t *d_row_path;       /* [rows] the path each row took (LLZ_PATH_* bits)           */
 } llz_sample_extras;
 
-/* Bits of d_row_path (diagnostics; a row with none took the single-pass path). */
+/* Bits of d_row_path (diagnostics).  A row with none of the bits 0-7 and 16
+ * took the single-pass exact path (the exact normaliser in one read, then the
+ * selection on its candidate list).  Bits 8-15 hold a number, not flags: with
+ * LLZ_PATH_FULL_SORT set, why the bucket path declined the row (0: it was not
+ * tried; 1 .. 255: a reason code of the bucket path, for diagnostics only). */
 enum {
     LLZ_PATH_SUM_LE0 = 1,        /* sum <= 0 exit (sampler.zig:89)                         */
     LLZ_PATH_ENTROPY = 2,        /* typical-p entropy pass ran (sampler.zig:128-154)       */
-    LLZ_PATH_FULL_SORT = 4,      /* kept set beyond the candidate list: full-row sort      */
+    LLZ_PATH_FULL_SORT = 4,      /* kept set beyond the candidate list: full-row fallback  */
     LLZ_PATH_STREAM_NORM = 8,    /* normaliser not certified in one pass: streaming pass   */
     LLZ_PATH_WALK_ROUNDS = 16,   /* diagnostic: more EXACT segments than one round's slots  */
     LLZ_PATH_RESOLVE_GENERIC = 32, /* diagnostic: a crossing beyond the tabulated binades   */
+    LLZ_PATH_BUCKETS = 64,       /* full row without a sort: kept prefix, total, draw from   */
+                                 /*   p-key buckets (with LLZ_PATH_FULL_SORT)              */
+    LLZ_PATH_TOKEN_ONLY = 128,   /* the token decided without the exact normaliser (calls    */
+                                 /*   asking for neither probabilities nor row statistics)  */
+    LLZ_PATH_DECLINE_SHIFT = 8,  /* bits 8-15: the bucket path's decline reason (see above)  */
+    LLZ_PATH_RECOLLECT = 1 << 16, /* a flooded candidate list collected again, its largest  */
+                                 /*   terms only, so the selection ran on a list            */
     LLZ_PATH_ERROR = (int)0x80000000u
 };
 

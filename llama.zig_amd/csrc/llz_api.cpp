@@ -47,11 +47,11 @@ uint32_t post_bits(const llz_logit_post* post) {
   return b;
 }
 
-// Workspace layout of one llz_sample_rows call: per row, its status word,
-// candidate list and special-queue overflow (32 KB); per call, a pool of
-// min(rows, kFbSlots) full-row fallback buffer sets (25 B per logit each)
-// with their owner words; the penalised copy only for windows too long to
-// fuse.
+// Workspace layout of one llz_sample_rows call: per row, its status word and
+// candidate list (16 KB); per workgroup of the grid (min(rows, kMaxGrid)),
+// a special-queue overflow block (128 KB); per call, a pool of full-row
+// fallback buffer sets (25 B per logit each) with their owner words; the
+// penalised copy only for windows too long to fuse.
 struct Layout {
   size_t status, claim, cand, qovf, owner, fb, fb_mask, penal, total;
   int fb_slots;
@@ -68,7 +68,7 @@ Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int
   L.status = off;  off = align_up(off + r * sizeof(uint32_t));
   L.claim = off;   off = align_up(off + sizeof(uint64_t));
   L.cand = off;    off = align_up(off + r * (size_t)kCandCap * sizeof(uint64_t));
-  L.qovf = off;    off = align_up(off + r * (size_t)kQovfRow * sizeof(uint32_t));
+  L.qovf = off;    off = align_up(off + (size_t)std::min(rows, kMaxGrid) * (size_t)kQovfRow * sizeof(uint32_t));
   L.owner = off;   off = align_up(off + ns * sizeof(uint64_t));
   L.fb = off;      off = align_up(off + 6 * ns * n * sizeof(uint32_t));
   L.fb_mask = off; off = align_up(off + ns * n);
@@ -252,12 +252,18 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   P.src_stride = src_stride;
   P.orig_stride = row_stride;
   // the token alone: no probabilities and no row statistics asked for, and no
-  // typical-p (its entropy needs the exact normaliser).  Only with a candidate
-  // threshold of at least 2^-10 (a min-p filter): below it the candidates
-  // (every term within 11 nats of the maximum, without min-p) rarely fit the
-  // token path's list, and a row that does not fit pays for the attempt
+  // typical-p (its entropy needs the exact normaliser).  The token path's list
+  // holds the terms e >= tok_theta: min-p's candidate threshold when it is at
+  // least 2^-10; without min-p (the reference's default chain), 2^-10 with
+  // top-p, whose cut must then fall inside the list.  Below 2^-10 the list
+  // (every term within 7 nats of the maximum) rarely fits, and a row that does
+  // not fit pays for the attempt
+  const bool tok_minp = P.cand_theta >= 0x1p-10f;
+  const bool tok_topp = !tok_minp && !(cfg->min_p > 0.0f) && cfg->top_p > 0.0f && cfg->top_p < 1.0f &&
+                        vocab > kCandCap;
+  P.tok_theta = tok_minp ? P.cand_theta : (tok_topp ? 0x1p-10f : 0.0f);
   const bool tok_only = !(extras && (extras->d_kept_probs || extras->d_row_stats)) &&
-                        !(cfg->typical_p > 0.0f && cfg->typical_p < 1.0f) && P.cand_theta >= 0x1p-10f;
+                        !(cfg->typical_p > 0.0f && cfg->typical_p < 1.0f) && (tok_minp || tok_topp);
   P.flags = (cfg->temperature == 1.0f ? kFlagTIsOne : 0u) | (vec ? kFlagVecSrc : 0u) | kFlagFallback |
             (tok_only ? kFlagTokenOnly : 0u);
   P.xf_src = xf_src;
@@ -273,7 +279,7 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
     // all resident at once; rows beyond them are claimed
     const int cus = device_cus(st);
     if (cus <= 0) return LLZ_E_HIP;
-    P.grid = rows < cus ? rows : cus;
+    P.grid = std::min(std::min(rows, cus), kMaxGrid);
   }
   P.epoch = g_epoch.fetch_add(1, std::memory_order_relaxed) & ((1ull << 62) - 1);
   // LLZ_TEST_QUEUE_CAP: a smaller special-queue chunk, so that tests reach

@@ -8,8 +8,12 @@ namespace llz {
 
 constexpr int kCandCap = 2048;  // candidate list capacity per row (power of two)
 constexpr int kPenMax = 64;     // fused repetition penalty: window entries at most (one per lane)
-constexpr int kQovfWave = 512;  // k_stats special-queue overflow entries per wave (four chunks)
-constexpr int kQovfRow = 8 * kQovfWave;  // ... per row (eight waves)
+constexpr int kQovfWave = 4096;  // k_stats special-queue overflow entries per wave
+constexpr int kQovfRow = 8 * kQovfWave;  // ... per workgroup (eight waves)
+// k_stats workgroups per launch at most (the grid: one per CU, rows beyond
+// claimed); the special-queue overflow area has one kQovfRow block per
+// workgroup, which samples one row at a time
+constexpr int kMaxGrid = 256;
 // Full-row fallback buffer sets per call at most (rows beyond wait for one):
 // the number of CUs, since k_stats's LDS holds one row-workgroup per CU, so
 // no more rows than this can be inside the fallback at once.
@@ -35,6 +39,7 @@ constexpr uint32_t kPathWalkRounds = 16u;    // diagnostic: the walk took more t
 constexpr uint32_t kPathResolveGeneric = 32u;  // diagnostic: an event beyond a segment's tabulated grids
 constexpr uint32_t kPathTokenOnly = 128u;     // the token certified without the exact normaliser
 constexpr uint32_t kPathBuckets = 64u;        // full row without a sort: kept prefix, total and draw by p-key buckets
+constexpr uint32_t kPathRecollect = 1u << 16;  // a flooded candidate list collected again (its largest terms)
 constexpr uint32_t kPathError = 0x80000000u;
 
 // Phase timestamps (measurement builds only, -DLLZ_PHASE_STAMPS): thread 0
@@ -63,6 +68,7 @@ struct RowParams {
   float typical_p;
   uint32_t top_k;
   float cand_theta;   // e >= cand_theta enters the candidate list
+  float tok_theta;    // token-only rows: e >= tok_theta enters their list (cand_theta, or 2^-10 without min-p)
   float l2e_t;        // RN(log2(e) / temperature)
   int32_t n;          // vocab
   int32_t rows;
@@ -98,7 +104,7 @@ struct RowPtrs {
   uint32_t* fb;           // 6 x [fb_slots][n] u32 (full-row fallback sort buffers)
   uint8_t* fb_mask;       // [fb_slots][n]
   unsigned long long* fb_owner;  // [fb_slots] epoch of the row using each slot
-  uint32_t* qovf;         // [rows][kQovfRow] k_stats special-queue overflow
+  uint32_t* qovf;         // [min(rows, kMaxGrid)][kQovfRow] k_stats special-queue overflow, per workgroup
   unsigned long long* claim;  // rows claimed beyond the grid: (epoch tag << 24) | count
   const uint32_t* prev_win;  // kXfPen: row 0's window (its last pen_w history tokens)
 };

@@ -722,6 +722,133 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
 
 constexpr int kShortMax = 256;  // longest candidate list of the short path
 
+// A flooded candidate list (more than kCap elements with e >= cand_theta) is
+// collected again from the row, keeping only its largest terms, so that the
+// selection still runs on a list whenever the kept prefix is short: the
+// reference's default chain (top-p 0.9, no min-p) on peaked rows keeps tens
+// to hundreds of terms of the thousands above 2^-16.  e is monotone in v, so
+// the largest terms are the largest logits:
+//  1. a histogram of d = m - v over [0, D), D = T ln(1 / cand_theta) (1 +
+//     2^-10) (every candidate), kRecBins bins of width w, with the count and
+//     the estimated terms' sum of each;
+//  2. the cut b: the first bin where the running estimated mass reaches
+//     top_p S (1 + 2^-8) (the estimates are within 2^-16 of the terms), one
+//     bin more, or else the end; and no further than the bins whose elements
+//     fit the list with a quarter of it to spare;
+//  3. every element with v > v_t = m - b w, with its exact term (sampler.zig:85).
+// Every element left out has v <= v_t, so e <= e(v_t) (1 + 2^-21.9): the
+// reference's argument RN(RN(v - m) / T) is monotone in v and its exp is
+// within one ulp of exp.  Returns e(v_t) (1 + 2^-21), the bound the
+// selection's certified prefix takes in place of cand_theta, or -1 when the
+// list cannot be made to fit (the full-row fallback follows).
+constexpr int kRecBins = 2048;
+
+template <class Src>
+__device__ __noinline__ float recollect_top(const Src X, int n, float m, float S, float T, float theta,
+                                            float l2e_t, float top_p, uint32_t top_k, uint32_t flags,
+                                            SampleShared& sh, int bank) {
+  constexpr int EV = RowTiles8::V;
+  constexpr int ET = kNT * EV;
+  constexpr int HB = kRecBins;
+  static_assert(sizeof(sh.u.post.radix.stage_k) >= HB * sizeof(uint32_t), "histogram counts fit");
+  static_assert(sizeof(sh.u.post.radix.stage_v) >= HB * sizeof(float), "histogram sums fit");
+  uint32_t* hcnt = sh.u.post.radix.stage_k;
+  float* hsum = reinterpret_cast<float*>(sh.u.post.radix.stage_v);
+  const int t = (int)threadIdx.x;
+  const bool t1 = (flags & kFlagTIsOne) != 0;
+  const bool vec = (flags & kFlagVecSrc) != 0;
+  // D: T ln(1/theta) from the hardware log2 (within an ulp), with 2^-10 to spare
+  const float D = T * (-__builtin_amdgcn_logf(theta)) * 0.693147182f * (1.0f + 0x1p-10f);
+  if (!(D > 0.0f) || !(D < 3.0e38f)) return -1.0f;
+  const float w = D / (float)HB, iw = (float)HB / D;
+  for (int b = t; b < HB; b += kNT) {
+    hcnt[b] = 0u;
+    hsum[b] = 0.0f;
+  }
+  lds_barrier();
+  const RowTiles8 rt(X.x, n, vec);
+  float raw[EV];
+  // ---- 1. the histogram (d < D: NaN and -inf logits never enter)
+  rt.load(t * EV, raw);
+  for (int base = 0; base < n; base += ET) {
+    const int pos = base + t * EV;
+    rt.fix_tail(pos, raw);
+    float d[EV];
+#pragma unroll
+    for (int k = 0; k < EV; ++k) d[k] = pos + k < n ? m - X.fix(pos + k, raw[k]) : kInf;
+    if (base + ET < n) rt.load(pos + ET, raw);
+#pragma unroll
+    for (int k = 0; k < EV; ++k) {
+      if (d[k] < D) {
+        const int b = min(HB - 1, (int)(d[k] * iw));
+        atomicAdd(&hcnt[b], 1u);
+        atomicAdd(&hsum[b], __builtin_amdgcn_exp2f(-d[k] * l2e_t));
+      }
+    }
+  }
+  lds_barrier();
+  // ---- 2. the cut: wave 0, lane l holding bins 32 l .. 32 l + 31
+  if (wave_id() == 0) {
+    constexpr int PB = HB / kWave;
+    const int lane = lane_id();
+    uint32_t cnt_l = 0u;
+    float mass_l = 0.0f;
+    for (int j = 0; j < PB; ++j) {
+      cnt_l += hcnt[lane * PB + j];
+      mass_l += hsum[lane * PB + j];
+    }
+    const uint32_t cinc = wave_incl_scan_op(cnt_l, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+    const float minc = __uint_as_float(wave_incl_scan_op(__float_as_uint(mass_l), 0u, [](uint32_t a, uint32_t b) {
+      return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+    }));
+    const uint32_t cap_fit = (uint32_t)(kCap - kCap / 4);
+    const bool topk_fit = top_k > 0u && top_k <= cap_fit / 2u;  // top-k ends the prefix inside a full list
+    const bool topp = top_p > 0.0f && top_p < 1.0f;
+    const float mass_target = topp ? top_p * S * (1.0f + 0x1p-8f) : kInf;
+    // the first bin where the list would be full, and the first where the
+    // running mass reaches top-p's target (then one bin more)
+    uint32_t c = cinc - cnt_l;
+    float s = minc - mass_l;
+    int cut_full = HB, mass_bin = HB;
+    for (int j = 0; j < PB; ++j) {
+      const int b = lane * PB + j;
+      c += hcnt[b];
+      s += hsum[b];
+      if (c > cap_fit && cut_full == HB) cut_full = b;  // bins before b fit the list
+      if (s >= mass_target && mass_bin == HB) mass_bin = b;
+    }
+    const int full_at = (int)wave_min_u32((uint32_t)cut_full);
+    const int mass_at = (int)wave_min_u32((uint32_t)mass_bin);
+    // a list filled at or before the bin where top-p's mass is reached,
+    // without a top-k inside it, cannot hold the kept prefix: not worth the
+    // second pass
+    const bool hopeless = full_at < HB && full_at <= mass_at && !topk_fit;
+    if (lane == 0) sh.misc[2] = hopeless ? 0u : (uint32_t)min(full_at, min(HB, mass_at + 2));
+  }
+  lds_barrier();
+  const int cut = (int)sh.misc[2];
+  if (cut <= 0) return -1.0f;  // the top bin alone does not fit
+  const float v_t = m - (float)cut * w;
+  if (t == 0) sh.cand_count = 0u;
+  lds_barrier();
+  // ---- 3. every element above v_t, with its exact term
+  rt.load(t * EV, raw);
+  for (int base = 0; base < n; base += ET) {
+    const int pos = base + t * EV;
+    rt.fix_tail(pos, raw);
+    float v[EV];
+#pragma unroll
+    for (int k = 0; k < EV; ++k) v[k] = pos + k < n ? X.fix(pos + k, raw[k]) : -kInf;
+    if (base + ET < n) rt.load(pos + ET, raw);
+#pragma unroll
+    for (int k = 0; k < EV; ++k)
+      if (v[k] > v_t) push_candidate(sh, exact_term(v[k], m, T, t1), (uint32_t)(pos + k));
+  }
+  lds_barrier();
+  if (sh.cand_count > (uint32_t)kCap) return -1.0f;
+  return exact_term(v_t, m, T, t1) * (1.0f + 0x1p-21f);
+}
+
 // The selection for a short candidate list without typical-p (the common
 // case): a rank sort by every wave, then filters, total and draw by wave 0
 // alone (sampler.zig:92-126, 156-168), with the same certified-prefix rules
@@ -941,11 +1068,28 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
 
   // ---- 4. candidates -> probabilities -> (p desc, id asc) (:90-100)
   lds_barrier();
-  const uint32_t cc = sh.cand_count;
+  uint32_t cc = sh.cand_count;
+  // the list's threshold for the certified prefix: cand_theta, or the bound
+  // of a list collected again (recollect_top) after it flooded
+  RowParams Pl = P;
+  // only where a filter can end the kept prefix inside the list: top-p, or a
+  // top-k within three quarters of it (min-p alone keeps every flooded term)
+  const bool bounded = (P.top_p > 0.0f && P.top_p < 1.0f) || (P.top_k > 0u && P.top_k <= (uint32_t)(kCap - kCap / 4) / 2u);
+  if (cc > (uint32_t)kCap && n > kCap && P.cand_theta > 0.0f && bounded) {
+    const float th =
+        recollect_top<Src>(X, n, m, S, P.temperature, P.cand_theta, P.l2e_t, P.top_p, P.top_k, P.flags, sh, bank);
+    cc = sh.cand_count;
+    if (th >= 0.0f) {
+      Pl.cand_theta = th;
+      path |= kPathRecollect;
+    } else {
+      cc = (uint32_t)kCap + 1u;
+    }
+  }
   const bool ovf = cc > (uint32_t)kCap;
   const int c = ovf ? kCap : (int)cc;
   if (!ovf && c <= kShortMax && !(P.typical_p > 0.0f && P.typical_p < 1.0f)) {
-    if (!select_short(P, Q, row, sh, c, m, S, path, u_row)) select_full_row<Src>(A, row, pen, sh, bank, m, S, path);
+    if (!select_short(Pl, Q, row, sh, c, m, S, path, u_row)) select_full_row<Src>(A, row, pen, sh, bank, m, S, path);
     return;
   }
   const int csort = next_pow2(c);
@@ -964,10 +1108,10 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   // certified prefix: every element outside the list has p <= theta / S
   int M = 0;
   if (!ovf) {
-    if (P.cand_theta <= 0.0f) {
+    if (Pl.cand_theta <= 0.0f) {
       M = c;  // every element was collected
     } else {
-      const float p_nc = P.cand_theta / S;
+      const float p_nc = Pl.cand_theta / S;
       uint32_t cnt = 0;
       for (int q = t; q < c; q += kNT) cnt += __uint_as_float(~(uint32_t)(sh.cand[q] >> 32)) > p_nc ? 1u : 0u;
       M = (int)wg_sum_sat<kNT>(cnt, 0x7fffffffu, sh.wg, bank);
@@ -976,7 +1120,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
 
   const LdsList LL{sh.cand};
   // a complete list bounds everything outside it: e < theta, p <= theta / S
-  const float p_nc = ovf ? kInf : P.cand_theta / S;
+  const float p_nc = ovf ? kInf : Pl.cand_theta / S;
   K = prefix_filters(LL, M, p_nc, n, P, S, sh, bank);
   const bool typical = P.typical_p > 0.0f && P.typical_p < 1.0f;
   const float u = u_row;

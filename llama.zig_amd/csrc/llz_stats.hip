@@ -777,7 +777,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   if (tok && l2e_t > 0.0f) {
     const float aw = fmaf(mx, -l2e_t, cw);
     if (fabsf(aw) <= 64.0f) {
-      const int q0 = tqueue(__builtin_amdgcn_exp2f(aw), P.cand_theta * (1.0f - 0x1p-10f) * (1.0f - 0x1p-12f));
+      const int q0 = tqueue(__builtin_amdgcn_exp2f(aw), P.tok_theta * (1.0f - 0x1p-10f) * (1.0f - 0x1p-12f));
       if (q0 <= QCAP) tq = q0;
     }
   }
@@ -827,7 +827,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   // estimate does (estimates are within 2^-16 of the terms, and no term
   // exceeds its segment's sum), re-read and evaluated exactly; the list lies
   // in F.v, free once every wave has read the segment sums below.
-  if (tok && !nanrow && fabsf(m) <= 3.0e38f && P.cand_theta > 0.0f) {
+  if (tok && !nanrow && fabsf(m) <= 3.0e38f && P.tok_theta > 0.0f) {
     LLZ_STAMP(row, 38);
     float s_est = 0.0f;
     bool tbad = false;
@@ -839,7 +839,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     }
     if (!tbad) {
       const float Rw_t = __builtin_amdgcn_exp2f(fmaf(m, -l2e_t, cw));
-      const float theta_t = P.cand_theta;
+      const float theta_t = P.tok_theta;
       const float thr_e = theta_t * (1.0f - 0x1p-10f);
       if (tq < 0) tq = tqueue(Rw_t, thr_e);
       LLZ_STAMP(row, 39);
@@ -1094,7 +1094,8 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     // entries per wave.  All are settled in phase F+X: phase S never
     // settles.  qch: current chunk,
     // qn: its entries, lane c of ccnt: the entries of an earlier chunk c.
-    uint32_t* const ovp = Q.qovf + (int64_t)row * kQovfRow + (int64_t)w * kQovfWave;
+    // (one block per workgroup: a workgroup samples one row at a time)
+    uint32_t* const ovp = Q.qovf + (int64_t)blockIdx.x * kQovfRow + (int64_t)w * kQovfWave;
     const int qcap = (P.qcap > 0u && P.qcap < (uint32_t)QCAP) ? (int)P.qcap : QCAP;  // entries per chunk
     int qch = 0;
     uint32_t ccnt = 0;
@@ -1558,11 +1559,17 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
   if (ev_begin && hipEventRecord(ev_begin, st) != hipSuccess) return hipErrorUnknown;
   const bool fastld = (P.flags & kFlagVecSrc) != 0 && (P.n % 4) == 0;
   const bool xf = P.xf_src != 0u || P.xf_orig != 0u;
-  if (P.grid < P.rows && fastld) {
-    if (!xf)
+  // more rows than workgroups: the grid's workgroups claim rows (the
+  // special-queue overflow area has one block per workgroup of the grid)
+  if (P.grid < P.rows) {
+    if (fastld && !xf)
       hipLaunchKernelGGL((k_stats_rows<true, false>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
-    else
+    else if (fastld)
       hipLaunchKernelGGL((k_stats_rows<true, true>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
+    else if (!xf)
+      hipLaunchKernelGGL((k_stats_rows<false, false>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
+    else
+      hipLaunchKernelGGL((k_stats_rows<false, true>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
   } else if (fastld && !xf)
     hipLaunchKernelGGL((k_stats<true, false>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
   else if (fastld)

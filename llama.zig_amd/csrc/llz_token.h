@@ -131,7 +131,12 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   LLZ_STAMP(row, 35);
   const int Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
   const int L = min(Kk, Km);
-  if (L > M) ok = false;
+  // a kept prefix that may reach past the certified prefix (no min-p, and
+  // no top-k inside it) is decided only by a top-p cut inside the prefix:
+  // the terms outside the list come after every position below M, and
+  // top-p, applied before min-p, drops each of them once it has cut
+  const bool open_end = L > M;
+  const int Lc = open_end ? M : L;
   // the interval of the reference's normaliser
   const double g = (double)(n - 1) * 0x1p-24;
   const double gr = g / (1.0 - g) + 0x1p-14;
@@ -140,22 +145,22 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   // 1/S at the interval's ends, rounded outwards (one rounding of 2^-53 each)
   const double iS_hi = (1.0 / S_hi) * (1.0 - 0x1p-50), iS_lo = (1.0 / S_lo) * (1.0 + 0x1p-50);
   const bool topp = P.top_p > 0.0f && P.top_p < 1.0f;
-  // one pass over positions [0, L): the running sums C_q of the terms
+  // one pass over positions [0, Lc): the running sums C_q of the terms
   // (double), top-p's cut (sampler.zig:111-118), and the order: adjacent terms
   // up to max(L, 1) equal (then ordered by id) or apart by more than 2^-21
   const int pe = min(max(L, 1), M - 1);
-  const int span = max(L, pe);
+  const int span = max(Lc, pe);
   double carry = 0.0, C0 = 0.0;  // C0: lane q's C_q for q < 64
   int cut = -1;
   for (int b = 0; b < span && ok && cut < 0; b += kWave) {
     const int q = b + lane;
     const float e = q < c ? e_at(q) : 0.0f;
-    const double C = carry + wave_incl_scan_f64(q < L ? (double)e : 0.0);
+    const double C = carry + wave_incl_scan_f64(q < Lc ? (double)e : 0.0);
     if (b == 0) C0 = C;
     if (topp) {
       const double rel = (2.0 * q + 4.0) * 0x1p-24;
-      const bool lo_over = q < L && C * iS_hi * (1.0 - rel) > (double)P.top_p;
-      const bool hi_over = q < L && C * iS_lo * (1.0 + rel) > (double)P.top_p;
+      const bool lo_over = q < Lc && C * iS_hi * (1.0 - rel) > (double)P.top_p;
+      const bool hi_over = q < Lc && C * iS_lo * (1.0 + rel) > (double)P.top_p;
       const uint64_t mh = bal64(hi_over);
       if (mh != 0ull) {
         const int fq = __ffsll((long long)mh) - 1;
@@ -173,6 +178,7 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
     if (bal64(unc) != 0ull) ok = false;
     carry = readlane_f64(C, kWave - 1);
   }
+  if (open_end && cut < 0) ok = false;  // the kept prefix may reach past the list
   const int K = cut >= 0 ? min(L, cut) : L;
   LLZ_STAMP(row, 36);
   uint32_t token = c >= 1 ? readlane_u32((uint32_t)k0, 0) : 0u, consumed = 0;  // indices[0]

@@ -240,6 +240,8 @@ PATH_SUM_LE0, PATH_ENTROPY, PATH_FULL_SORT, PATH_STREAM_NORM = 1, 2, 4, 8
 PATH_WALK_ROUNDS, PATH_RESOLVE_GENERIC = 16, 32  # diagnostics of the single pass's walk
 PATH_BUCKETS = 64  # full row without a sort: kept prefix, total and draw from p-key buckets
 PATH_TOKEN_ONLY = 128  # the token decided without the exact normaliser (calls asking for the token alone)
+PATH_DECLINE_SHIFT = 8  # bits 8-15: why the bucket path declined a full-row row (a number, not flags)
+PATH_RECOLLECT = 1 << 16  # a flooded candidate list collected again (its largest terms)
 
 
 def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, post: Optional[LogitPost] = None,

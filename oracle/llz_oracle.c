@@ -619,6 +619,7 @@ typedef struct {
     uint32_t *tokens;
     uint8_t *consumed;
     uint32_t *kept;
+    float *stats;
     int64_t row_begin, row_end;
     int rc;
 } rows_job;
@@ -636,6 +637,13 @@ static void *rows_worker(void *arg)
         j->tokens[r] = o.token;
         if (j->consumed) j->consumed[r] = (uint8_t)o.consumed;
         if (j->kept) j->kept[r] = o.kept_count;
+        if (j->stats) {
+            float *st = j->stats + 4 * r;
+            st[0] = o.max_logit;
+            st[1] = o.sum;
+            st[2] = o.entropy;
+            st[3] = o.total;
+        }
     }
     return NULL;
 }
@@ -645,6 +653,17 @@ int llz_oracle_sample_rows(const float *logits, int64_t rows, int64_t n, int64_t
                            int64_t n_prev, int64_t prev_stride, const float *uniforms,
                            uint32_t *tokens, uint8_t *consumed, uint32_t *kept_count,
                            int threads)
+{
+    return llz_oracle_sample_rows_stats(logits, rows, n, row_stride, cfg, prev_tokens, n_prev,
+                                        prev_stride, uniforms, tokens, consumed, kept_count, NULL,
+                                        threads);
+}
+
+int llz_oracle_sample_rows_stats(const float *logits, int64_t rows, int64_t n, int64_t row_stride,
+                                 const llz_oracle_cfg *cfg, const uint32_t *prev_tokens,
+                                 int64_t n_prev, int64_t prev_stride, const float *uniforms,
+                                 uint32_t *tokens, uint8_t *consumed, uint32_t *kept_count,
+                                 float *stats, int threads)
 {
     if (threads < 1) threads = 1;
     if (threads > rows) threads = (int)(rows > 0 ? rows : 1);
@@ -657,6 +676,7 @@ int llz_oracle_sample_rows(const float *logits, int64_t rows, int64_t n, int64_t
         j->logits = logits; j->n = n; j->row_stride = row_stride; j->cfg = cfg;
         j->prev = prev_tokens; j->n_prev = n_prev; j->prev_stride = prev_stride;
         j->uniforms = uniforms; j->tokens = tokens; j->consumed = consumed; j->kept = kept_count;
+        j->stats = stats;
         j->row_begin = t * per;
         j->row_end = (t + 1) * per < rows ? (t + 1) * per : rows;
         j->rc = 0;

@@ -122,6 +122,14 @@ int llz_oracle_sample_rows(const float *logits, int64_t rows, int64_t n, int64_t
                            uint32_t *tokens, uint8_t *consumed, uint32_t *kept_count,
                            int threads);
 
+/* The same, plus per row (when stats is not NULL) the maximum logit, the
+ * normaliser, the entropy and the kept total: stats[4 r + 0 .. 3]. */
+int llz_oracle_sample_rows_stats(const float *logits, int64_t rows, int64_t n, int64_t row_stride,
+                                 const llz_oracle_cfg *cfg, const uint32_t *prev_tokens,
+                                 int64_t n_prev, int64_t prev_stride, const float *uniforms,
+                                 uint32_t *tokens, uint8_t *consumed, uint32_t *kept_count,
+                                 float *stats, int threads);
+
 /* Sampler object with the reference's RNG lifecycle (sampler.zig:15-28). */
 typedef struct {
     llz_oracle_cfg cfg;

@@ -104,6 +104,10 @@ def lib():
         L.llz_oracle_sample_rows.argtypes = [fp, i64, i64, i64, C.POINTER(OracleCfg),
                                              C.POINTER(u32), i64, i64, fp, C.POINTER(u32),
                                              C.POINTER(C.c_uint8), C.POINTER(u32), C.c_int]
+        L.llz_oracle_sample_rows_stats.restype = C.c_int
+        L.llz_oracle_sample_rows_stats.argtypes = [fp, i64, i64, i64, C.POINTER(OracleCfg),
+                                                   C.POINTER(u32), i64, i64, fp, C.POINTER(u32),
+                                                   C.POINTER(C.c_uint8), C.POINTER(u32), fp, C.c_int]
         L.llz_oracle_sampler_init.argtypes = [C.POINTER(OracleSampler), C.POINTER(OracleCfg)]
         L.llz_oracle_sampler_sample.restype = C.c_int
         L.llz_oracle_sampler_sample.argtypes = [C.POINTER(OracleSampler), fp, i64, C.POINTER(u32),
@@ -199,6 +203,28 @@ def sample_rows(logits: np.ndarray, params, uniforms: np.ndarray, prev_tokens=No
     if rc != 0:
         raise MemoryError("oracle allocation failed")
     return tokens, consumed, kept
+
+
+def sample_rows_stats(logits: np.ndarray, params, uniforms: np.ndarray, threads: int = 1):
+    """Token, consumed flag, kept count and [max, normaliser, entropy, total]
+    per row, no repetition history."""
+    L = lib()
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, n = x.shape
+    u = np.ascontiguousarray(uniforms, dtype=np.float32)
+    assert u.shape[0] >= rows
+    tokens = np.empty(rows, np.uint32)
+    consumed = np.empty(rows, np.uint8)
+    kept = np.empty(rows, np.uint32)
+    stats = np.empty((rows, 4), np.float32)
+    prev = np.zeros(0, np.uint32)
+    cfg = make_cfg(params)
+    rc = L.llz_oracle_sample_rows_stats(_fptr(x), rows, n, n, C.byref(cfg), _uptr(prev), 0, 0, _fptr(u),
+                                        _uptr(tokens), consumed.ctypes.data_as(C.POINTER(C.c_uint8)),
+                                        _uptr(kept), _fptr(stats), int(threads))
+    if rc != 0:
+        raise MemoryError("oracle allocation failed")
+    return tokens, consumed, kept, stats
 
 
 def expf(x: float) -> np.float32:

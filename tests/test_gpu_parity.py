@@ -321,6 +321,34 @@ def test_strided_and_unaligned_rows(cuda):
     compare_rows(x, p, u, g)
 
 
+@pytest.mark.parametrize("post", [None, "softcap"])
+def test_unaligned_rows_beyond_the_grid(cuda, post):
+    """More rows than the grid's workgroups (300 > 256) on rows that are only
+    4-byte aligned: the workgroups claim rows (k_stats_rows's element-load
+    instantiations), each with its own special-queue overflow block; with
+    and without the logit post-processing.  Every row against the oracle."""
+    import torch
+
+    n, rows, stride = 3001, 300, 3007
+    base = np.random.default_rng(8).normal(0, 2, rows * stride + 1).astype(np.float32)
+    p = Params(temperature=0.8, top_k=30, top_p=0.9, min_p=0.02, repetition_penalty=1.0)
+    u = llz.rng_uniforms(19, rows)
+    cfg = llz.SamplerConfig.of(p)
+    lp = llz.LogitPost(final_logit_softcapping=20.0, logit_scale=0.5) if post else None
+    full = torch.from_numpy(base).to(cuda)
+    view = full[1:1 + rows * stride].view(rows, stride)[:, :n]   # 4-byte aligned only
+    res = llz.sample_rows(view, cfg, torch.from_numpy(u).to(cuda), post=lp, kept_cap=64, stats=True)
+    torch.cuda.synchronize()
+    x = base[1:1 + rows * stride].reshape(rows, stride)[:, :n].copy()
+    if post:
+        x = O.logit_post(x, softcap=20.0, logit_scale=0.5)
+    g = dict(tokens=res.tokens.cpu().numpy().view(np.uint32), consumed=res.consumed.cpu().numpy(),
+             kept_count=res.kept_count.cpu().numpy().view(np.uint32),
+             kept_ids=res.kept_ids.cpu().numpy().view(np.uint32),
+             kept_probs=res.kept_probs.cpu().numpy(), stats=res.row_stats.cpu().numpy(), cap=64)
+    compare_rows(x, p, u, g, rows=range(0, rows, 7))
+
+
 def test_argmax_rows(cuda):
     import torch
 

@@ -105,12 +105,88 @@ def test_token_only_undecidable_rows_fall_back(cuda):
     probs = o1.probs[o1.kept_ids()[:k1]].astype(np.float64)
     u[1] = np.float32(probs[0] / probs.sum())
     g = _run(cuda, x, p, u)
-    assert not (g["path"][0] & PATH_TOKEN_ONLY) or True  # the min-p term may round clear of the band
+    # row 0's min-p term may round clear of the band: only the oracle decides it.
+    # Row 1's draw lands on a CDF boundary, inside the draw's margin: the row
+    # must leave the token path
+    assert not (g["path"][1] & PATH_TOKEN_ONLY), f"row 1 certified a boundary draw (path {g['path'][1]:#x})"
     _check_oracle(x, p, u, g)
     # top-p binding: configuration 2's logits with top-p 0.3
     p2 = dataclasses.replace(p, top_p=0.3)
     g2 = _run(cuda, x, p2, u)
     _check_oracle(x, p2, u, g2)
+
+
+def test_token_only_top_p_cut_inside_interval_falls_back(cuda):
+    """Ten equal terms over a low floor with top-p 0.3: the running sum after
+    three terms is 3/S with S close to 10, and the reference's S is known
+    only to (n - 1) 2^-24 (the recursive-summation bound), about 0.8%, so
+    the cut cannot be decided without the exact normaliser.  The row leaves
+    the token path and matches the oracle; the same logits with top-p 0.5
+    (a cut clear of the interval) stay on it."""
+    w = WORKLOADS["headline"]
+    rows = 2
+    rng = np.random.default_rng(5)
+    x = rng.normal(-30.0, 1.0, size=(rows, w.vocab)).astype(np.float32)
+    for r in range(rows):
+        x[r, rng.choice(w.vocab, 10, replace=False)] = 0.0
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    p = dataclasses.replace(w.params, top_k=0, top_p=0.3)
+    g = _run(cuda, x, p, u)
+    assert not np.any(g["path"] & PATH_TOKEN_ONLY), f"paths {g['path']}"
+    _check_oracle(x, p, u, g)
+    p5 = dataclasses.replace(p, top_p=0.45)
+    g5 = _run(cuda, x, p5, u)
+    assert np.all(g5["path"] & PATH_TOKEN_ONLY), f"paths {g5['path']}"
+    _check_oracle(x, p5, u, g5)
+
+
+def test_token_only_top_p_without_min_p(cuda):
+    """The reference's default chain (no min-p; top-p 0.9, T 0.8): the token
+    path's list holds the terms e >= 2^-10, and a row certifies when its
+    top-p cut falls inside the list and clear of the normaliser's interval
+    (about 0.8% at 128k terms).  Configuration 1's rows 1-3 do (their cuts
+    lie 2% or more from 0.9); row 0's running sum stops 0.04% short of 0.9,
+    so it takes the exact phases.  On the headline's logits the nuclei are
+    long and fine-grained, so most rows take the exact phases too.  Every row
+    matches the oracle."""
+    c1 = WORKLOADS["c1"]
+    x1 = c1.logits(4)
+    u1 = llz.rng_uniforms(c1.uniform_seed, 4)
+    g1 = _run(cuda, x1, c1.params, u1)
+    assert np.all(g1["path"][1:] & PATH_TOKEN_ONLY), f"paths {g1['path']}"
+    assert not (g1["path"][0] & PATH_TOKEN_ONLY), f"path {g1['path'][0]:#x}"
+    _check_oracle(x1, c1.params, u1, g1)
+    w = WORKLOADS["headline"]
+    rows = 48
+    x = w.logits(rows)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    p = dataclasses.replace(w.params, temperature=0.8, top_k=0, top_p=0.9, min_p=0.0)
+    g = _run(cuda, x, p, u)
+    _check_oracle(x, p, u, g)
+    # with top-k inside the list as well
+    pk = dataclasses.replace(p, top_k=20)
+    gk = _run(cuda, x, pk, u)
+    _check_oracle(x, pk, u, gk)
+
+
+@pytest.mark.parametrize("kind", ["flat", "wide-nucleus"])
+def test_token_only_top_p_without_min_p_falls_back(cuda, kind):
+    """Top-p without min-p where the cut is not inside the list: a near-flat
+    row (every term past the list's reach) and top-p 0.999 on peaked rows
+    (the list holds less than 0.999 of the mass).  The rows take the exact
+    phases and match the oracle."""
+    w = WORKLOADS["headline"]
+    rows = 4
+    if kind == "flat":
+        x = np.random.default_rng(3).normal(0.0, 0.3, size=(rows, 100000)).astype(np.float32)
+        p = dataclasses.replace(w.params, temperature=1.2, top_k=0, top_p=0.9, min_p=0.0)
+    else:
+        x = WORKLOADS["c1"].logits(rows)
+        p = dataclasses.replace(WORKLOADS["c1"].params, top_p=0.999)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    g = _run(cuda, x, p, u, cap=256)
+    assert not np.any(g["path"] & PATH_TOKEN_ONLY), f"paths {g['path']}"
+    _check_oracle(x, p, u, g)
 
 
 def test_token_only_kept_ids_without_cap(cuda):
