@@ -89,8 +89,9 @@ def calibrate_copy(mib: int) -> int:
 
 def c1_latency(w, x_host, u_host, reps: int) -> dict:
     """Configuration 1 is one row per decode step (main.zig:667): its latency
-    per call, for the device-resident batched entry point and for the host
-    Sampler that takes host logits (H2D copy, sampling, D2H, synchronisation)."""
+    per call, rotating over the given rows, for the device-resident batched
+    entry point and for the host Sampler that takes host logits (H2D copy,
+    sampling, D2H, synchronisation)."""
     import numpy as np
     import torch
 
@@ -98,37 +99,56 @@ def c1_latency(w, x_host, u_host, reps: int) -> dict:
 
     dev = torch.device("cuda:0")
     cfg = llz.SamplerConfig.of(w.params)
-    x = torch.from_numpy(x_host[:1]).to(dev)
-    u = torch.from_numpy(u_host[:1].copy()).to(dev)
-    ws = torch.empty(llz.workspace_bytes(1, w.vocab, cfg), dtype=torch.uint8, device=dev)
-    tok = torch.empty(1, dtype=torch.int32, device=dev)
-    con = torch.empty(1, dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream()
-    for _ in range(20):
-        llz.sample_rows(x, cfg, u, workspace=ws, stream=stream, out=(tok, con))
+    nr = x_host.shape[0]
+    xs = [torch.from_numpy(x_host[b:b + 1].copy()).to(dev) for b in range(nr)]
+    us = [torch.from_numpy(u_host[b:b + 1].copy()).to(dev) for b in range(nr)]
+    call = llz.PreparedCall(1, w.vocab, cfg, dev)
+    for i in range(20):
+        call(xs[i % nr], us[i % nr])
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        llz.sample_rows(x, cfg, u, workspace=ws, stream=stream, out=(tok, con))
+    per_row = np.zeros(nr)
+    for i in range(reps * nr):
+        t0 = time.perf_counter()
+        call(xs[i % nr], us[i % nr])
         torch.cuda.synchronize()
-    dev_us = (time.perf_counter() - t0) * 1e6 / reps
+        per_row[i % nr] += time.perf_counter() - t0
+    per_row *= 1e6 / reps
 
     s = llz.Sampler(llz.SamplerConfig.of(w.params, seed=0))
-    row = np.ascontiguousarray(x_host[0])
-    for _ in range(20):
-        s.sample(row)
+    rows = [np.ascontiguousarray(x_host[b]) for b in range(nr)]
+    for i in range(20):
+        s.sample(rows[i % nr])
     t0 = time.perf_counter()
-    for _ in range(reps):
-        s.sample(row)
-    host_us = (time.perf_counter() - t0) * 1e6 / reps
+    for i in range(reps * nr):
+        s.sample(rows[i % nr])
+    host_us = (time.perf_counter() - t0) * 1e6 / (reps * nr)
     s.close()
-    return {"device_rows_us_per_call": round(dev_us, 2), "host_sampler_us_per_call": round(host_us, 2),
-            "reps": reps,
-            "note": "one row per call, each call synchronised: llz_sample_rows on device logits, and "
-                    "llz_sampler_sample on host logits (513 KB H2D copy + sampling + token D2H)"}
+    return {"device_rows_us_per_call": round(float(per_row.mean()), 2),
+            "device_rows_us_per_row": [round(float(v), 1) for v in per_row],
+            "host_sampler_us_per_call": round(host_us, 2), "reps_per_row": reps, "rows": nr,
+            "note": "one row per call, each call synchronised, rotating over the configuration's first rows: "
+                    "llz_sample_rows on device logits, and llz_sampler_sample on host logits (513 KB H2D copy + "
+                    "sampling + token D2H)"}
 
 
-def run_workload(name: str, steps: int, warmup: int, args) -> dict:
+# bench lines: (workload, mode).  "token": the call asks for the token alone
+# (the reference's Sampler.sample returns only the token, sampler.zig:26-28);
+# "exact": it also asks for the kept probabilities and the row statistics
+# (the exact normaliser on every row).
+LINES = {
+    "headline": ("headline", "token"),
+    "headline-exact": ("headline", "exact"),
+    "headline-default": ("headline-default", "token"),
+    "c1": ("c1", "token"),
+    "c2": ("c2", "token"),
+    "c3": ("c3", "token"),
+    "c4": ("c4", "token"),
+    "c5": ("c5", "token"),
+}
+C1_ROWS = 8  # configuration 1 is one row per call: the steps rotate over this many rows of its generator
+
+
+def run_workload(line: str, steps: int, warmup: int, args) -> dict:
     import numpy as np
     import torch
 
@@ -136,48 +156,65 @@ def run_workload(name: str, steps: int, warmup: int, args) -> dict:
     import oracle_lib as O
     from llz.workloads import WORKLOADS, algorithmic_bytes
 
+    name, mode = LINES[line]
     w = WORKLOADS[name]
     dev = torch.device("cuda:0")
     rows, vocab = w.rows, w.vocab
     batch_bytes = rows * vocab * 4
     cfg = llz.SamplerConfig.of(w.params)
-
-    # one batch generated on the host; the other buffers hold its rows rotated
-    # (same data, other addresses: each step reads memory the previous steps
-    # did not leave in the Infinity Cache)
-    nbuf = max(2, -(-2 * MALL_BYTES // batch_bytes) + 1)
-    x_host = w.logits(rows)
-    u_host = llz.rng_uniforms(w.uniform_seed, rows)
-    x0 = torch.from_numpy(x_host).to(dev)
-    u0 = torch.from_numpy(u_host).to(dev)
-    xs = [torch.roll(x0, shifts=b * max(1, rows // nbuf), dims=0).contiguous() for b in range(nbuf)]
-    us = [torch.roll(u0, shifts=b * max(1, rows // nbuf), dims=0).contiguous() for b in range(nbuf)]
-    del x0
-    ws = torch.empty(llz.workspace_bytes(rows, vocab, cfg), dtype=torch.uint8, device=dev)
-    tokens = torch.empty(rows, dtype=torch.int32, device=dev)
-    consumed = torch.empty(rows, dtype=torch.uint8, device=dev)
+    exact = mode == "exact"
     stream = torch.cuda.current_stream()
+
+    if name == "c1":
+        # one row per call, rotating over C1_ROWS rows of the generator (each
+        # step reads a row the previous steps did not)
+        nbuf = C1_ROWS
+        x_host = w.logits(nbuf)
+        u_host = llz.rng_uniforms(w.uniform_seed, nbuf)
+        xs = [torch.from_numpy(x_host[b:b + 1].copy()).to(dev) for b in range(nbuf)]
+        us = [torch.from_numpy(u_host[b:b + 1].copy()).to(dev) for b in range(nbuf)]
+    else:
+        # one batch generated on the host; the other buffers hold its rows
+        # rotated (same data, other addresses: each step reads memory the
+        # previous steps did not leave in the Infinity Cache)
+        nbuf = max(2, -(-2 * MALL_BYTES // batch_bytes) + 1)
+        x_host = w.logits(rows)
+        u_host = llz.rng_uniforms(w.uniform_seed, rows)
+        x0 = torch.from_numpy(x_host).to(dev)
+        u0 = torch.from_numpy(u_host).to(dev)
+        xs = [torch.roll(x0, shifts=b * max(1, rows // nbuf), dims=0).contiguous() for b in range(nbuf)]
+        us = [torch.roll(u0, shifts=b * max(1, rows // nbuf), dims=0).contiguous() for b in range(nbuf)]
+        del x0
+    call = llz.PreparedCall(rows, vocab, cfg, dev, kept_cap=64 if exact else 0, probs=exact, stats=exact,
+                            stream=stream)
 
     def step(i):
         b = i % nbuf
-        llz.sample_rows(xs[b], cfg, us[b], workspace=ws, stream=stream, out=(tokens, consumed))
+        call(xs[b], us[b])
 
-    # parity spot check of the timed configuration against the oracle, and
-    # the path each row of every buffer takes
-    res = llz.sample_rows(xs[0], cfg, us[0], path=True, workspace=ws, stream=stream)
-    torch.cuda.synchronize()
-    tok0 = res.tokens.cpu().numpy().view(np.uint32)
-    con0 = res.consumed.cpu().numpy()
-    nchk = min(8, rows)
+    # parity spot check of the timed call against the oracle, and the path
+    # each row takes (the same call with the path bits asked for)
+    probe = llz.PreparedCall(rows, vocab, cfg, dev, kept_cap=64 if exact else 0, probs=exact, stats=exact,
+                             path=True, stream=stream)
+    tok0, con0, paths = [], [], []
+    for b in range(nbuf if name == "c1" else 1):
+        r = probe(xs[b], us[b])
+        torch.cuda.synchronize()
+        tok0.append(r.tokens.cpu().numpy().view(np.uint32).copy())
+        con0.append(r.consumed.cpu().numpy().copy())
+        paths.append(r.row_path.cpu().numpy().view(np.uint32).copy())
+    tok0, con0, paths = np.concatenate(tok0), np.concatenate(con0), np.concatenate(paths)
+    nchk = min(8, tok0.shape[0])
     o_tok, o_con, _ = O.sample_rows(x_host[:nchk], w.params, u_host[:nchk], threads=HOST_THREADS)
     parity_ok = bool(np.array_equal(tok0[:nchk], o_tok) and np.array_equal(con0[:nchk], o_con))
-    paths = res.row_path.cpu().numpy().view(np.uint32)
     frac = lambda bit: round(float(np.mean((paths & bit) != 0)), 4)  # noqa: E731
     path_fracs = {"stream_norm": frac(llz.PATH_STREAM_NORM), "full_sort": frac(llz.PATH_FULL_SORT),
                   "entropy": frac(llz.PATH_ENTROPY), "sum_le0": frac(llz.PATH_SUM_LE0),
                   "walk_rounds": frac(llz.PATH_WALK_ROUNDS), "resolve_generic": frac(llz.PATH_RESOLVE_GENERIC),
                   "buckets": frac(llz.PATH_BUCKETS), "token_only": frac(llz.PATH_TOKEN_ONLY),
+                  "recollect": frac(llz.PATH_RECOLLECT),
                   "single_pass": round(float(np.mean((paths & (llz.PATH_STREAM_NORM | llz.PATH_FULL_SORT)) == 0)), 4)}
+    del probe
 
     # W untimed warmup steps right before the timed region (after the spot
     # check, whose host work leaves the GPU idle), a synchronisation, then the
@@ -210,10 +247,13 @@ def run_workload(name: str, steps: int, warmup: int, args) -> dict:
     ms_events = cb.elapsed_time(ce) / steps
     alg = algorithmic_bytes(rows, vocab)
     achieved = alg / (ms_events * 1e-3) / 1e9
+    # HBM bytes per launch from the committed counter runs of this line
+    # (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, scaled by a device copy),
+    # not measured by this run
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"k_stats_{name}_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
+    traffic_src = os.path.join("profiles", f"k_stats_{line}_traffic.json")
+    if os.path.exists(os.path.join(ROOT, traffic_src)):
+        with open(os.path.join(ROOT, traffic_src)) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
     out = {
@@ -230,21 +270,24 @@ def run_workload(name: str, steps: int, warmup: int, args) -> dict:
         "dtype": "f32",
         "data": f"synthetic ({w.text}); numpy default_rng per row; inputs resident in HBM, "
                 f"{nbuf} rotating buffers ({nbuf * batch_bytes / 2**20:.0f} MiB) to defeat the Infinity Cache",
-        "config": {"workload": w.name, "rows": rows, "vocab": vocab, "temperature": w.params.temperature,
+        "config": {"workload": line, "rows": rows, "vocab": vocab, "temperature": w.params.temperature,
                    "top_k": w.params.top_k, "top_p": w.params.top_p, "min_p": w.params.min_p,
-                   "typical_p": w.params.typical_p, "parallelism": "none (1 GPU)"},
+                   "typical_p": w.params.typical_p,
+                   "call": ("token, kept probabilities (64) and row statistics" if exact else "token alone"),
+                   "parallelism": "none (1 GPU)"},
         "gbps": round(alg / (ms_per_step * 1e-3) / 1e9, 1),
         "ms_per_step_events": round(ms_events, 5),
         "roofline": {"bound": "hbm", "kernel": "k_stats", "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
-                     "traffic": traffic, "kernel_ms": round(ms_events, 5),
+                     "traffic": traffic, "traffic_source": traffic_src if traffic is not None else None,
+                     "kernel_ms": round(ms_events, 5),
                      "algorithmic_bytes": alg},
         "paths": path_fracs,
         "parity_spot_check": {"rows": nchk, "ok": parity_ok},
     }
     if name == "c1":
-        out["latency"] = c1_latency(w, x_host, u_host, reps=200)
-    del xs, us, ws
+        out["latency"] = c1_latency(w, x_host, u_host, reps=50)
+    del xs, us, call
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         # 64 rows (a batch of fewer rows is repeated), so that every thread has rows
@@ -263,7 +306,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--workload", default="headline",
-                    help="headline (default), c1 .. c5, or all (one JSON line each)")
+                    help="headline (default), headline-exact, headline-default, c1 .. c5, or all (one JSON line each)")
     ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="wall-clock budget of each CPU baseline mode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -283,11 +326,11 @@ def main() -> int:
 
     from llz.workloads import WORKLOADS
 
-    names = ["headline", "c1", "c2", "c3", "c4", "c5"] if args.workload == "all" else [args.workload]
+    names = list(LINES) if args.workload == "all" else [args.workload]
     head_rows = WORKLOADS["headline"].rows * WORKLOADS["headline"].vocab
     ok = True
     for name in names:
-        w = WORKLOADS[name]
+        w = WORKLOADS[LINES[name][0]]
         # the headline takes the given K; the others scale K by their batch size
         # (at least 10 steps), so each line times a comparable amount of work
         steps = args.steps if name == "headline" else max(10, args.steps * head_rows // (w.rows * w.vocab))

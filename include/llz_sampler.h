@@ -239,6 +239,13 @@ int llz_debug_hw_error(int32_t op, uint32_t first_bits, uint32_t count, uint32_t
  * time, so throughput runs leave it cleared). */
 int llz_debug_kernel_events(void *begin_event, void *end_event);
 
+/* Test hook (no counterpart in the reference): the special-queue chunk of
+ * the single-pass statistics (entries per wave and chunk, 1 .. 127) for the
+ * following llz_sample_rows calls, so that tests reach the queue's chunks
+ * in the workspace on ordinary rows; 0 restores the kernel's own.  Results
+ * do not depend on it.  Process-wide. */
+int llz_debug_set_queue_cap(uint32_t cap);
+
 /* Name of a return code. */
 const char *llz_strerror(int code);
 

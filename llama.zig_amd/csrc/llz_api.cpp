@@ -22,6 +22,8 @@ size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 // measurement hook: events recorded around the fused sampling kernel (see llz_debug_kernel_events)
 hipEvent_t g_ev_begin = nullptr;
 hipEvent_t g_ev_end = nullptr;
+// test hook: a smaller special-queue chunk (see llz_debug_set_queue_cap)
+std::atomic<uint32_t> g_queue_cap{0u};
 
 bool penalty_active(const llz_sampler_config* cfg, int32_t n_prev) {
   return cfg->repetition_penalty != 1.0f && n_prev > 0 && cfg->repetition_window > 0;
@@ -282,12 +284,8 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
     P.grid = std::min(std::min(rows, cus), kMaxGrid);
   }
   P.epoch = g_epoch.fetch_add(1, std::memory_order_relaxed) & ((1ull << 62) - 1);
-  // LLZ_TEST_QUEUE_CAP: a smaller special-queue chunk, so that tests reach
-  // the chunked queue on ordinary rows (the kernel clamps it to its own)
-  {
-    const char* qc = std::getenv("LLZ_TEST_QUEUE_CAP");
-    P.qcap = qc ? (uint32_t)std::strtoul(qc, nullptr, 10) : 0u;
-  }
+  // the test hook's special-queue chunk (0: the kernel's own)
+  P.qcap = g_queue_cap.load(std::memory_order_relaxed);
 
   RowPtrs Q{};
   Q.src = src;
@@ -387,6 +385,11 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
   return sample_rows_impl(d_logits, row_stride, rows, vocab, cfg, post, d_prev_tokens, n_prev, prev_stride,
                           d_uniforms, d_tokens, d_consumed, extras, d_workspace, workspace_bytes, kFbSlots,
                           LLZ_E_WORKSPACE, stream);
+}
+
+int llz_debug_set_queue_cap(uint32_t cap) {
+  g_queue_cap.store(cap, std::memory_order_relaxed);
+  return LLZ_OK;
 }
 
 int llz_debug_kernel_events(void* begin_event, void* end_event) {

@@ -746,7 +746,7 @@ constexpr int kRecBins = 2048;
 template <class Src>
 __device__ __noinline__ float recollect_top(const Src X, int n, float m, float S, float T, float theta,
                                             float l2e_t, float top_p, uint32_t top_k, uint32_t flags,
-                                            SampleShared& sh, int bank) {
+                                            SampleShared& sh, int bank, int row) {
   constexpr int EV = RowTiles8::V;
   constexpr int ET = kNT * EV;
   constexpr int HB = kRecBins;
@@ -787,6 +787,7 @@ __device__ __noinline__ float recollect_top(const Src X, int n, float m, float S
     }
   }
   lds_barrier();
+  LLZ_STAMP(row, 40);
   // ---- 2. the cut: wave 0, lane l holding bins 32 l .. 32 l + 31
   if (wave_id() == 0) {
     constexpr int PB = HB / kWave;
@@ -831,6 +832,7 @@ __device__ __noinline__ float recollect_top(const Src X, int n, float m, float S
   const float v_t = m - (float)cut * w;
   if (t == 0) sh.cand_count = 0u;
   lds_barrier();
+  LLZ_STAMP(row, 41);
   // ---- 3. every element above v_t, with its exact term
   rt.load(t * EV, raw);
   for (int base = 0; base < n; base += ET) {
@@ -845,6 +847,7 @@ __device__ __noinline__ float recollect_top(const Src X, int n, float m, float S
       if (v[k] > v_t) push_candidate(sh, exact_term(v[k], m, T, t1), (uint32_t)(pos + k));
   }
   lds_barrier();
+  LLZ_STAMP(row, 42);
   if (sh.cand_count > (uint32_t)kCap) return -1.0f;
   return exact_term(v_t, m, T, t1) * (1.0f + 0x1p-21f);
 }
@@ -1075,9 +1078,13 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
   // only where a filter can end the kept prefix inside the list: top-p, or a
   // top-k within three quarters of it (min-p alone keeps every flooded term)
   const bool bounded = (P.top_p > 0.0f && P.top_p < 1.0f) || (P.top_k > 0u && P.top_k <= (uint32_t)(kCap - kCap / 4) / 2u);
-  if (cc > (uint32_t)kCap && n > kCap && P.cand_theta > 0.0f && bounded) {
+  // (each term is at most 1, so a kept prefix that top-p alone ends inside
+  // the list needs top_p S <= the list's length: near-flat rows skip it)
+  const bool topk_in = P.top_k > 0u && P.top_k <= (uint32_t)(kCap - kCap / 4) / 2u;
+  const bool reachable = topk_in || P.top_p * S <= (float)(kCap - kCap / 4);
+  if (cc > (uint32_t)kCap && n > kCap && P.cand_theta > 0.0f && bounded && reachable) {
     const float th =
-        recollect_top<Src>(X, n, m, S, P.temperature, P.cand_theta, P.l2e_t, P.top_p, P.top_k, P.flags, sh, bank);
+        recollect_top<Src>(X, n, m, S, P.temperature, P.cand_theta, P.l2e_t, P.top_p, P.top_k, P.flags, sh, bank, row);
     cc = sh.cand_count;
     if (th >= 0.0f) {
       Pl.cand_theta = th;

@@ -41,7 +41,7 @@ EXPORTED = (
     "llz_argmax_rows", "llz_rng_seed", "llz_rng_next", "llz_rng_float", "llz_rng_uniforms",
     "llz_sampler_create", "llz_sampler_destroy", "llz_sampler_sample", "llz_sampler_sample_uniform",
     "llz_sampler_get_state",
-    "llz_sampler_set_state", "llz_debug_math", "llz_debug_hw_error", "llz_debug_kernel_events", "llz_strerror",
+    "llz_sampler_set_state", "llz_debug_math", "llz_debug_hw_error", "llz_debug_kernel_events", "llz_debug_set_queue_cap", "llz_strerror",
 )
 
 
@@ -163,6 +163,8 @@ def _lib():
         L.llz_debug_hw_error.restype = C.c_int
         L.llz_debug_kernel_events.argtypes = [vp, vp]
         L.llz_debug_kernel_events.restype = C.c_int
+        L.llz_debug_set_queue_cap.argtypes = [C.c_uint32]
+        L.llz_debug_set_queue_cap.restype = C.c_int
         L.llz_strerror.argtypes = [C.c_int]
         L.llz_strerror.restype = C.c_char_p
         _LIB = L
@@ -320,6 +322,59 @@ def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, post:
     return res
 
 
+class PreparedCall:
+    """llz_sample_rows for a fixed shape and configuration with its outputs
+    and workspace allocated once (serving loops, benchmarks): each call runs
+    the C entry point on the given rows and uniforms and fills the same
+    output tensors, with no allocation.  kept_cap > 0 asks for the kept ids
+    (and with probs their probabilities); stats for the row statistics; path
+    for the path bits.  A call asking for neither probabilities nor row
+    statistics may finish rows without the exact normaliser."""
+
+    def __init__(self, rows: int, vocab: int, cfg: SamplerConfig, device, *, kept_cap: int = 0,
+                 probs: bool = False, stats: bool = False, path: bool = False, stream=None):
+        torch = _torch()
+        self.rows, self.vocab = rows, vocab
+        self._c = cfg.to_c()
+        self._stream = _stream_ptr(stream)
+        self.result = SampleResult(torch.empty(rows, dtype=torch.int32, device=device),
+                                   torch.empty(rows, dtype=torch.uint8, device=device))
+        self._ex = None
+        if kept_cap > 0 or stats or path:
+            ex = CExtras()
+            r = self.result
+            r.kept_count = torch.empty(rows, dtype=torch.int32, device=device)
+            ex.d_kept_count = r.kept_count.data_ptr()
+            if kept_cap > 0:
+                r.kept_ids = torch.full((rows, kept_cap), -1, dtype=torch.int32, device=device)
+                ex.d_kept_ids = r.kept_ids.data_ptr()
+                if probs:
+                    r.kept_probs = torch.full((rows, kept_cap), float("nan"), dtype=torch.float32, device=device)
+                    ex.d_kept_probs = r.kept_probs.data_ptr()
+                ex.kept_cap = kept_cap
+            if stats:
+                r.row_stats = torch.zeros((rows, 4), dtype=torch.float32, device=device)
+                ex.d_row_stats = r.row_stats.data_ptr()
+            if path:
+                r.row_path = torch.empty(rows, dtype=torch.int32, device=device)
+                ex.d_row_path = r.row_path.data_ptr()
+            self._ex = ex
+        need = int(_lib().llz_sample_workspace_bytes(rows, vocab, C.byref(self._c), 0))
+        self.workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+
+    def __call__(self, logits, uniforms) -> SampleResult:
+        if tuple(logits.shape) != (self.rows, self.vocab) or logits.stride(1) != 1:
+            raise ValueError("logits must have the prepared shape with contiguous rows")
+        r = self.result
+        rc = _lib().llz_sample_rows(
+            logits.data_ptr(), logits.stride(0), self.rows, self.vocab, C.byref(self._c), None, None, 0, 0,
+            uniforms.data_ptr(), r.tokens.data_ptr(), r.consumed.data_ptr(),
+            C.byref(self._ex) if self._ex is not None else None, self.workspace.data_ptr(), self.workspace.numel(),
+            self._stream)
+        _check(rc, "llz_sample_rows")
+        return r
+
+
 def argmax_rows(logits, post: Optional[LogitPost] = None, stream=None):
     """sampleArgmax per row (sampler.zig:31-41) of the post-processed logits
     (main.zig:653-666) on a 2-D float32 CUDA tensor."""
@@ -357,6 +412,12 @@ def debug_hw_error(op: int, first_bits: int, count: int) -> float:
     rc = _lib().llz_debug_hw_error(op, first_bits, count, out.data_ptr(), _stream_ptr(None))
     _check(rc, "llz_debug_hw_error")
     return float(int(out.cpu().numpy().view("uint32")[0])) / 2.0 ** 20
+
+
+def debug_set_queue_cap(cap: int) -> None:
+    """The single pass's special-queue chunk for following calls (0: the
+    kernel's own); a test hook, results do not depend on it."""
+    _check(_lib().llz_debug_set_queue_cap(int(cap)), "llz_debug_set_queue_cap")
 
 
 def set_kernel_events(begin=None, end=None) -> None:

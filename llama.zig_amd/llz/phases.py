@@ -35,6 +35,7 @@ SLOTS = {
     32: "token-only: candidate lanes queued", 33: "token-only: candidates evaluated", 34: "token-only: sorted",
     38: "token-only: row maximum read", 39: "token-only: candidate segments scanned",
     35: "token-only: prefix and min-p counted", 36: "token-only: top-p and order checked", 37: "token-only: drawn",
+    40: "recollect: histogram", 41: "recollect: cut", 42: "recollect: collected",
 }
 # phases as (name, from slot, to slot)
 PHASES = [
@@ -55,6 +56,8 @@ PHASES = [
     ("token: queue + loads issued + barrier", 39, 32), ("token-only: re-read and exact terms", 32, 33), ("token-only: sort", 33, 34),
     ("token-only: decisions", 34, 15), ("decisions: entry + counts", 34, 35), ("decisions: top-p + order", 35, 36),
     ("decisions: draw", 36, 37), ("decisions: outputs + barrier", 37, 15),
+    ("recollect: histogram pass", 6, 40), ("recollect: cut", 40, 41), ("recollect: collect pass", 41, 42),
+    ("after recollect: sort, filters, draw", 42, 15),
 ]
 
 
@@ -64,6 +67,7 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=0, help="rows (default: the workload's batch)")
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--exact", action="store_true", help="ask for row statistics (the exact phases on every row)")
+    ap.add_argument("--chain-params", default="", help="override the workload's chain, e.g. T=0.8,top_p=0.9,min_p=0,top_k=0")
     ap.add_argument("--dump", default="", help="also save every row's raw timestamps (.npy)")
     ap.add_argument("--chain", type=int, default=1,
                     help="launches back to back before reading (the last one's stamps, as in a benchmark loop)")
@@ -82,10 +86,17 @@ def main() -> int:
     L.llz_debug_phase_stamps.argtypes = [C.c_void_p, C.c_int, C.c_int]
     L.llz_debug_phase_stamps.restype = C.c_int
     rows_st = min(rows, 4096)
-    buf = np.zeros((rows_st, 40), np.uint64)
+    buf = np.zeros((rows_st, 44), np.uint64)
     x = torch.from_numpy(w.logits(rows)).cuda()
     u = torch.from_numpy(llz.rng_uniforms(w.uniform_seed, rows)).cuda()
-    cfg = llz.SamplerConfig.of(w.params)
+    params = w.params
+    if a.chain_params:
+        import dataclasses
+
+        names = {"T": "temperature", "top_p": "top_p", "min_p": "min_p", "top_k": "top_k", "typical_p": "typical_p"}
+        kv = dict(item.split("=") for item in a.chain_params.split(","))
+        params = dataclasses.replace(params, **{names[k]: (int(v) if k == "top_k" else float(v)) for k, v in kv.items()})
+    cfg = llz.SamplerConfig.of(params)
     res = None
     for _ in range(a.reps):
         assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 1) == 0

@@ -127,6 +127,13 @@ WORKLOADS: Dict[str, Workload] = {
         Params(temperature=1.0, top_k=40, top_p=0.95, min_p=0.05, typical_p=1.0, **_NO_REP),
         data_seed=7, uniform_seed=7, gen_row=_zipf_row,
         text="256 x 128256, configuration 2's logits and chain (T 1.0, k 40, p 0.95, min-p 0.05)"),
+    # The headline's logits with the reference's default chain (SamplerConfig
+    # defaults, sampler.zig:4-13, without the repetition penalty).
+    "headline-default": Workload(
+        "headline-default", 256, 128256,
+        Params(temperature=0.8, top_k=0, top_p=0.9, min_p=0.0, typical_p=1.0, **_NO_REP),
+        data_seed=7, uniform_seed=7, gen_row=_zipf_row,
+        text="256 x 128256, the headline's logits with the reference's default chain (T 0.8, top-p 0.9)"),
 }
 
 

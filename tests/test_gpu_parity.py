@@ -506,16 +506,23 @@ def test_headline_rows_take_fast_path(cuda):
 # the special queue's chunks past the LDS queue
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("qcap", [8, 32, 64])
-def test_special_queue_chunks(cuda, monkeypatch, qcap):
-    """LLZ_TEST_QUEUE_CAP shrinks the special-queue chunk, so ordinary rows fill
-    several chunks (kept in the workspace's fallback buffers); a batch with
-    more specials than a chunk holds (the row's first segments have many
-    large terms) sends its row to the streaming normaliser.  Results stay
-    bit-exact; at 32 and 64 some rows (each with over 64 specials per wave,
-    so several chunks) still take the fast path."""
+def test_special_queue_chunks(cuda, qcap):
+    """llz_debug_set_queue_cap shrinks the special-queue chunk, so ordinary rows fill
+    several chunks (kept in the workgroup's overflow block of the workspace);
+    a batch with more specials than a chunk holds (the row's first segments
+    have many large terms) sends its row to the streaming normaliser.
+    Results stay bit-exact; at 32 and 64 some rows (each with over 64
+    specials per wave, so several chunks) still take the fast path."""
+    llz.debug_set_queue_cap(qcap)
+    try:
+        _queue_chunk_rows(cuda, qcap)
+    finally:
+        llz.debug_set_queue_cap(0)
+
+
+def _queue_chunk_rows(cuda, qcap):
     import torch
 
-    monkeypatch.setenv("LLZ_TEST_QUEUE_CAP", str(qcap))
     for name, rows in [("headline", 8), ("c2", 6)]:
         w = WORKLOADS[name]
         x = w.logits(rows)
