@@ -52,19 +52,34 @@ uint32_t post_bits(const llz_logit_post* post) {
 // Workspace layout of one llz_sample_rows call: per row, its status word and
 // candidate list (16 KB); per workgroup of the grid (min(rows, kMaxGrid)),
 // a special-queue overflow block (128 KB); per call, a pool of full-row
-// fallback buffer sets (25 B per logit each) with their owner words; the
-// penalised copy only for windows too long to fuse.
+// fallback buffer sets (25 B per logit each, fb_slots_for) with their owner
+// words; the penalised copy only for windows too long to fuse.
 struct Layout {
   size_t status, claim, cand, qovf, owner, fb, fb_mask, penal, total;
   int fb_slots;
   bool has_penal;
 };
 
+float candidate_theta(const llz_sampler_config* cfg, int32_t vocab);
+
+// Full-row fallback buffer sets for a call: a row needs one only when its
+// kept set can outgrow the candidate list.  With a min-p of at least 2^-10
+// every kept term passes the candidate threshold, so only rows with more
+// than kCandCap such terms (near-flat rows) need a set: kFbSlotsLean of them;
+// otherwise one per row up to kFbSlots (one per CU: no more rows run at once).
+// Rows beyond the pool wait for a set (bounded), so the size affects speed only.
+constexpr int kFbSlotsLean = 8;
+int fb_slots_for(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int max_slots) {
+  int s = std::min(rows, max_slots);
+  if (candidate_theta(cfg, vocab) >= 0x1p-10f) s = std::min(s, kFbSlotsLean);
+  return s;
+}
+
 Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int32_t n_prev,
                  int max_slots = kFbSlots) {
   Layout L{};
   const size_t r = (size_t)rows, n = (size_t)vocab;
-  L.fb_slots = rows < max_slots ? rows : max_slots;
+  L.fb_slots = fb_slots_for(rows, vocab, cfg, max_slots);
   const size_t ns = (size_t)L.fb_slots;
   size_t off = 0;
   L.status = off;  off = align_up(off + r * sizeof(uint32_t));

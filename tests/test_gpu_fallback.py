@@ -31,6 +31,19 @@ def test_fallback_pool_contention(cuda):
     compare_rows(x, p, u, g)
 
 
+def test_lean_fallback_pool_contention(cuda):
+    """With min-p >= 2^-10 a call holds 8 full-row buffer sets: here 96
+    near-flat rows all need one (every term passes min-p 0.05, far more than
+    the candidate list holds), so rows wait for sets in turn.  Every row
+    against the oracle."""
+    rows, n = 96, 20000
+    x = np.random.default_rng(23).normal(0, 0.3, (rows, n)).astype(np.float32)
+    p = Params(temperature=1.0, top_k=0, top_p=0.95, min_p=0.05, repetition_penalty=1.0)
+    u = llz.rng_uniforms(37, rows)
+    g = run_gpu(x, p, u, cuda, kept_cap=64)
+    compare_rows(x, p, u, g)
+
+
 @pytest.mark.parametrize("name,check_rows", [("c4", (0, 137, 511, 1023)), ("c5", (0, 1, 1001, 2048, 4095))])
 def test_full_batch(cuda, name, check_rows):
     import torch
