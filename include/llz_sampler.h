@@ -210,6 +210,15 @@ int llz_sampler_sample_uniform(llz_sampler *s, const float *logits, int32_t n,
                                const uint32_t *prev_tokens, int32_t n_prev, float u,
                                uint32_t *token, uint8_t *consumed);
 
+/* The same with the configuration passed per call (the handle's own is
+ * neither used nor changed): one handle, and its device buffers and stream,
+ * serves samplers of any configuration, so a caller that creates a sampler
+ * per request (engine.zig:215) can share one handle per device.  Calls on
+ * one handle must not overlap. */
+int llz_sampler_sample_config(llz_sampler *s, const llz_sampler_config *cfg, const float *logits,
+                              int32_t n, const uint32_t *prev_tokens, int32_t n_prev, float u,
+                              uint32_t *token, uint8_t *consumed);
+
 /* PRNG state snapshot / restore (checkpointing a generation). */
 void llz_sampler_get_state(const llz_sampler *s, uint64_t state[4]);
 void llz_sampler_set_state(llz_sampler *s, const uint64_t state[4]);

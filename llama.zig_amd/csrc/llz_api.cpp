@@ -556,12 +556,13 @@ static bool is_device_ptr(const void* p) {
 
 // One row through llz_sample_rows with the caller's uniform: token and the
 // consumed-draw flag (sampler.zig:162 reached).  Synchronous.
-static int sampler_run(llz_sampler* s, const float* logits, int32_t n, const uint32_t* prev_tokens,
-                       int32_t n_prev, float u, uint32_t* token, uint8_t* consumed) {
-  if (!s || !logits || n <= 0 || !token || n_prev < 0 || (n_prev > 0 && !prev_tokens))
+static int sampler_run(llz_sampler* s, const llz_sampler_config* cfg, const float* logits, int32_t n,
+                       const uint32_t* prev_tokens, int32_t n_prev, float u, uint32_t* token, uint8_t* consumed) {
+  if (!s || !cfg || !logits || n <= 0 || !token || n_prev < 0 || (n_prev > 0 && !prev_tokens))
     return LLZ_E_INVALID_ARG;
+  if (cfg->temperature != cfg->temperature) return LLZ_E_INVALID_ARG;
   if (hipSetDevice(s->device) != hipSuccess) return LLZ_E_HIP;
-  const size_t need_ws = llz_sample_workspace_bytes(1, n, &s->cfg, n_prev);
+  const size_t need_ws = llz_sample_workspace_bytes(1, n, cfg, n_prev);
   if (n > s->cap_n || n_prev > s->cap_prev || need_ws > s->ws_bytes) {
     sampler_free_buffers(s);
     const int32_t cn = n, cp = n_prev > 0 ? n_prev : 1;
@@ -590,7 +591,7 @@ static int sampler_run(llz_sampler* s, const float* logits, int32_t n, const uin
     return LLZ_E_HIP;
   if (hipMemcpyAsync(s->d_u, &u, sizeof(float), hipMemcpyHostToDevice, s->stream) != hipSuccess)
     return LLZ_E_HIP;
-  int rc = llz_sample_rows(d_in, n, 1, n, &s->cfg, nullptr, n_prev > 0 ? s->d_prev : nullptr, n_prev, 0,
+  int rc = llz_sample_rows(d_in, n, 1, n, cfg, nullptr, n_prev > 0 ? s->d_prev : nullptr, n_prev, 0,
                            s->d_u, s->d_token, s->d_consumed, nullptr, s->d_ws, s->ws_bytes,
                            s->stream);
   if (rc != LLZ_OK) return rc;
@@ -601,7 +602,7 @@ static int sampler_run(llz_sampler* s, const float* logits, int32_t n, const uin
       hipStreamSynchronize(s->stream) != hipSuccess)
     return LLZ_E_HIP;
   *token = tok;
-  *consumed = (con != 0 && s->cfg.temperature > 0.0f) ? 1 : 0;
+  *consumed = (con != 0 && cfg->temperature > 0.0f) ? 1 : 0;
   return LLZ_OK;
 }
 
@@ -613,7 +614,7 @@ int llz_sampler_sample(llz_sampler* s, const float* logits, int32_t n, const uin
   std::memcpy(snap, s->prng, sizeof(snap));
   const float u = llz_rng_float(s->prng);
   uint8_t consumed = 0;
-  const int rc = sampler_run(s, logits, n, prev_tokens, n_prev, u, token, &consumed);
+  const int rc = sampler_run(s, &s->cfg, logits, n, prev_tokens, n_prev, u, token, &consumed);
   if (rc != LLZ_OK || !consumed) std::memcpy(s->prng, snap, sizeof(snap));
   return rc;
 }
@@ -622,7 +623,15 @@ int llz_sampler_sample_uniform(llz_sampler* s, const float* logits, int32_t n, c
                                int32_t n_prev, float u, uint32_t* token, uint8_t* consumed) {
   if (!consumed) return LLZ_E_INVALID_ARG;
   *consumed = 0;
-  return sampler_run(s, logits, n, prev_tokens, n_prev, u, token, consumed);
+  return s ? sampler_run(s, &s->cfg, logits, n, prev_tokens, n_prev, u, token, consumed) : LLZ_E_INVALID_ARG;
+}
+
+int llz_sampler_sample_config(llz_sampler* s, const llz_sampler_config* cfg, const float* logits, int32_t n,
+                              const uint32_t* prev_tokens, int32_t n_prev, float u, uint32_t* token,
+                              uint8_t* consumed) {
+  if (!consumed) return LLZ_E_INVALID_ARG;
+  *consumed = 0;
+  return sampler_run(s, cfg, logits, n, prev_tokens, n_prev, u, token, consumed);
 }
 
 }  // extern "C"

@@ -40,8 +40,8 @@ EXPORTED = (
     "llz_sampler_config_default", "llz_sample_workspace_bytes", "llz_sample_rows", "llz_sample_rows_noalloc",
     "llz_argmax_rows", "llz_rng_seed", "llz_rng_next", "llz_rng_float", "llz_rng_uniforms",
     "llz_sampler_create", "llz_sampler_destroy", "llz_sampler_sample", "llz_sampler_sample_uniform",
-    "llz_sampler_get_state",
-    "llz_sampler_set_state", "llz_debug_math", "llz_debug_hw_error", "llz_debug_kernel_events", "llz_debug_set_queue_cap", "llz_strerror",
+    "llz_sampler_sample_config", "llz_sampler_get_state", "llz_sampler_set_state", "llz_debug_math",
+    "llz_debug_hw_error", "llz_debug_kernel_events", "llz_debug_set_queue_cap", "llz_strerror",
 )
 
 
@@ -153,6 +153,9 @@ def _lib():
         L.llz_sampler_sample_uniform.argtypes = [vp, vp, i32, C.POINTER(C.c_uint32), i32, C.c_float,
                                                  C.POINTER(C.c_uint32), C.POINTER(C.c_uint8)]
         L.llz_sampler_sample_uniform.restype = C.c_int
+        L.llz_sampler_sample_config.argtypes = [vp, C.POINTER(CConfig), vp, i32, C.POINTER(C.c_uint32), i32,
+                                                C.c_float, C.POINTER(C.c_uint32), C.POINTER(C.c_uint8)]
+        L.llz_sampler_sample_config.restype = C.c_int
         L.llz_sampler_get_state.argtypes = [vp, C.POINTER(u64)]
         L.llz_sampler_get_state.restype = None
         L.llz_sampler_set_state.argtypes = [vp, C.POINTER(u64)]
@@ -463,6 +466,19 @@ class Sampler:
         rc = _lib().llz_sampler_sample_uniform(self._h, ptr, n, prev.ctypes.data_as(C.POINTER(C.c_uint32)),
                                                prev.shape[0], C.c_float(u), C.byref(tok), C.byref(con))
         _check(rc, "llz_sampler_sample_uniform")
+        return int(tok.value), bool(con.value)
+
+    def sample_config(self, cfg: SamplerConfig, logits, u: float, prev_tokens=()) -> Tuple[int, bool]:
+        """One row with the caller's configuration and uniform (the handle's own
+        configuration is not used): (token, consumed-draw flag)."""
+        prev = np.ascontiguousarray(np.asarray(prev_tokens, dtype=np.uint32))
+        x = np.ascontiguousarray(logits, dtype=np.float32)
+        c = cfg.to_c()
+        tok, con = C.c_uint32(), C.c_uint8()
+        rc = _lib().llz_sampler_sample_config(self._h, C.byref(c), x.ctypes.data, x.shape[0],
+                                              prev.ctypes.data_as(C.POINTER(C.c_uint32)), prev.shape[0],
+                                              C.c_float(u), C.byref(tok), C.byref(con))
+        _check(rc, "llz_sampler_sample_config")
         return int(tok.value), bool(con.value)
 
     @property

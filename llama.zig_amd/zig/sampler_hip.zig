@@ -24,13 +24,18 @@
 //! the stream advances exactly as the reference's does.
 //!
 //! Differences a caller can see, all outside the reference's signatures:
-//!   * the first `sample` opens the GPU (device 0): `init` stays infallible;
+//!   * the first `sample` of the process opens the GPU (device 0): `init`
+//!     stays infallible, and every Sampler shares that one device handle
+//!     (a stream and buffers sized to the longest row seen), each call
+//!     passing its own configuration, so a Sampler created per request
+//!     (engine.zig:215) costs nothing on the device and nothing leaks;
 //!   * `sample` can fail with error.GpuUnavailable or error.GpuFailure as
 //!     well as error.OutOfMemory (callers use `try`, as main.zig:667 does);
-//!   * `deinit` releases the device buffers.  The reference has no deinit;
-//!     a Sampler that is never deinit'ed keeps them until the process ends.
+//!   * `deinit` exists for callers that want it and does nothing: the shared
+//!     handle lives until the process ends;
 //!   * `allocator` is accepted and unused: the library keeps its own device
-//!     buffers, sized on the first call and grown when a longer row arrives.
+//!     buffers;
+//!   * calls from several threads are serialised on the shared handle.
 const std = @import("std");
 const tokenizer = @import("tokenizer.zig");
 
@@ -70,9 +75,9 @@ pub const c = struct {
     pub const E_NO_DEVICE: c_int = -5;
 
     pub extern "llzsample" fn llz_sampler_create(cfg: *const Config, device: i32, out: *?*Handle) c_int;
-    pub extern "llzsample" fn llz_sampler_destroy(s: ?*Handle) void;
-    pub extern "llzsample" fn llz_sampler_sample_uniform(
+    pub extern "llzsample" fn llz_sampler_sample_config(
         s: *Handle,
+        cfg: *const Config,
         logits: [*]const f32,
         n: i32,
         prev_tokens: ?[*]const u32,
@@ -82,6 +87,21 @@ pub const c = struct {
         consumed: *u8,
     ) c_int;
 };
+
+/// The process's device handle, shared by every Sampler (each call passes its
+/// own configuration), opened by the first `sample`; calls are serialised.
+var shared_gpu: ?*c.Handle = null;
+var shared_lock: std.Thread.Mutex = .{};
+
+fn sharedGpu() !*c.Handle {
+    if (shared_gpu) |h| return h;
+    const cfg = toC(.{});
+    var h: ?*c.Handle = null;
+    const rc = c.llz_sampler_create(&cfg, 0, &h);
+    if (rc != c.OK) return mapError(rc);
+    shared_gpu = h;
+    return h.?;
+}
 
 fn toC(cfg: SamplerConfig) c.Config {
     return .{
@@ -99,8 +119,6 @@ fn toC(cfg: SamplerConfig) c.Config {
 pub const Sampler = struct {
     cfg: SamplerConfig,
     prng: std.Random.DefaultPrng,
-    /// The device sampler, opened by the first `sample`.
-    gpu: ?*c.Handle = null,
 
     pub fn init(cfg: SamplerConfig) Sampler {
         return .{
@@ -113,21 +131,19 @@ pub const Sampler = struct {
         _ = allocator;
         if (logits.len == 0 or logits.len > std.math.maxInt(i32) or prev_tokens.len > std.math.maxInt(i32))
             return error.InvalidLength;
-        if (self.gpu == null) {
-            const cfg = toC(self.cfg);
-            var h: ?*c.Handle = null;
-            const rc = c.llz_sampler_create(&cfg, 0, &h);
-            if (rc != c.OK) return mapError(rc);
-            self.gpu = h;
-        }
+        shared_lock.lock();
+        defer shared_lock.unlock();
+        const gpu = try sharedGpu();
         // The draw sampler.zig:162 would make; undone below when the row
         // leaves the chain before it.
         const before = self.prng;
         const u = self.prng.random().float(f32);
+        const cfg = toC(self.cfg);
         var token: u32 = 0;
         var consumed: u8 = 0;
-        const rc = c.llz_sampler_sample_uniform(
-            self.gpu.?,
+        const rc = c.llz_sampler_sample_config(
+            gpu,
+            &cfg,
             logits.ptr,
             @intCast(logits.len),
             if (prev_tokens.len > 0) prev_tokens.ptr else null,
@@ -141,10 +157,10 @@ pub const Sampler = struct {
         return token;
     }
 
-    /// Releases the device buffers (optional; see the file comment).
+    /// Nothing to release: the device handle is the process's shared one
+    /// (see the file comment).  Kept for callers that pair init with deinit.
     pub fn deinit(self: *Sampler) void {
-        if (self.gpu) |h| c.llz_sampler_destroy(h);
-        self.gpu = null;
+        _ = self;
     }
 };
 

@@ -194,3 +194,21 @@ def test_sampler_object_ignores_post(cuda):
         o = O.sample_row(x, w.params, u)
         assert (tok, con) == (o.token, bool(o.consumed)), i
     s.close()
+
+
+def test_shared_handle_takes_each_calls_config(cuda):
+    """llz_sampler_sample_config: one handle serves samplers of different
+    configurations (the Zig drop-in shares one per process), each call with
+    its own configuration and uniform, against the oracle."""
+    w = WORKLOADS["c1"]
+    x = w.logits(2)
+    s = llz.Sampler(llz.SamplerConfig.of(w.params))
+    chains = [w.params, dataclasses_replace(w.params, temperature=1.3, top_k=5, top_p=1.0),
+              dataclasses_replace(w.params, min_p=0.2), dataclasses_replace(w.params, temperature=0.0)]
+    for i, u in enumerate(llz.rng_uniforms(11, 8)):
+        p = chains[i % len(chains)]
+        row = x[i % 2]
+        tok, con = s.sample_config(llz.SamplerConfig.of(p), row, float(u))
+        o = O.sample_row(row, p, u)
+        assert (tok, con) == (o.token, bool(o.consumed)), (i, p)
+    s.close()
