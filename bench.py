@@ -3,8 +3,11 @@
 
 With no flags it measures the headline workload -- 256 rows x 128256 vocab
 fp32 with configuration 2's logits and filter chain (T 1.0, top-k 40, top-p
-0.95, min-p 0.05) -- and prints ONE JSON line.  ``--workload c1 .. c5`` (or
-``all``) measures the reference's other configurations, one JSON line each.
+0.95, min-p 0.05) -- and prints ONE JSON line.  ``--workload c1 .. c5`` measures
+the reference's other configurations, ``headline-exact``, ``headline-post``,
+``headline-penalty`` and ``headline-default`` the headline's logits with the
+exact outputs, the decode loop's post-processing, the repetition penalty or
+the reference's default chain, and ``all`` every line, one JSON line each.
 
 A step is one llz_sample_rows call over one resident batch.  Inputs rotate
 over enough distinct device buffers that each step reads its logits from HBM,
@@ -16,6 +19,7 @@ thread and with the host's share of threads.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import platform
@@ -44,16 +48,20 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(w, x_host, u_host, threads: int, budget_s: float) -> dict:
+def cpu_baseline(w, x_host, u_host, threads: int, budget_s: float, params=None, post=None, prev=None) -> dict:
     """The oracle (sampler.zig restated in C, -O2, no fast-math) on host cores:
-    whole batches of the workload's first rows, repeated until budget_s."""
+    whole batches of the workload's first rows, repeated until budget_s.  With
+    post (soft-cap, logit scale) the rows are post-processed inside the timed
+    loop, as the decode loop does before sampling (main.zig:653-666)."""
     import oracle_lib as O
 
+    params = params if params is not None else w.params
     rows = x_host.shape[0]
     n_rows = 0
     t0 = time.perf_counter()
     while True:
-        O.sample_rows(x_host, w.params, u_host, threads=threads)
+        x = x_host if post is None else O.logit_post(x_host, post.final_logit_softcapping, post.logit_scale)
+        O.sample_rows(x, params, u_host, prev_tokens=prev, threads=threads)
         n_rows += rows
         dt = time.perf_counter() - t0
         if dt >= budget_s:
@@ -134,10 +142,16 @@ def c1_latency(w, x_host, u_host, reps: int) -> dict:
 # bench lines: (workload, mode).  "token": the call asks for the token alone
 # (the reference's Sampler.sample returns only the token, sampler.zig:26-28);
 # "exact": it also asks for the kept probabilities and the row statistics
-# (the exact normaliser on every row).
+# (the exact normaliser on every row); "post": the token call after the
+# decode loop's post-processing, soft-cap 30 and logit scale 0.5
+# (main.zig:653-666); "penalty": the token call with the reference's default
+# repetition penalty (window 32, 1.1, sampler.zig:54-75) over 32 history
+# tokens per row.
 LINES = {
     "headline": ("headline", "token"),
     "headline-exact": ("headline", "exact"),
+    "headline-post": ("headline", "post"),
+    "headline-penalty": ("headline", "penalty"),
     "headline-default": ("headline-default", "token"),
     "c1": ("c1", "token"),
     "c2": ("c2", "token"),
@@ -161,7 +175,15 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
     dev = torch.device("cuda:0")
     rows, vocab = w.rows, w.vocab
     batch_bytes = rows * vocab * 4
-    cfg = llz.SamplerConfig.of(w.params)
+    params = w.params
+    post = prev = None
+    if mode == "post":
+        post = llz.LogitPost(final_logit_softcapping=30.0, logit_scale=0.5)
+    if mode == "penalty":
+        params = dataclasses.replace(params, repetition_window=32, repetition_penalty=1.1)
+        prev_host = np.random.default_rng(41).integers(0, vocab, size=(rows, 32)).astype(np.int32)
+        prev = torch.from_numpy(prev_host).to(dev)
+    cfg = llz.SamplerConfig.of(params)
     exact = mode == "exact"
     stream = torch.cuda.current_stream()
 
@@ -186,7 +208,7 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
         us = [torch.roll(u0, shifts=b * max(1, rows // nbuf), dims=0).contiguous() for b in range(nbuf)]
         del x0
     call = llz.PreparedCall(rows, vocab, cfg, dev, kept_cap=64 if exact else 0, probs=exact, stats=exact,
-                            stream=stream)
+                            stream=stream, post=post, prev_tokens=prev)
 
     def step(i):
         b = i % nbuf
@@ -195,7 +217,7 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
     # parity spot check of the timed call against the oracle, and the path
     # each row takes (the same call with the path bits asked for)
     probe = llz.PreparedCall(rows, vocab, cfg, dev, kept_cap=64 if exact else 0, probs=exact, stats=exact,
-                             path=True, stream=stream)
+                             path=True, stream=stream, post=post, prev_tokens=prev)
     tok0, con0, paths = [], [], []
     for b in range(nbuf if name == "c1" else 1):
         r = probe(xs[b], us[b])
@@ -205,7 +227,11 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
         paths.append(r.row_path.cpu().numpy().view(np.uint32).copy())
     tok0, con0, paths = np.concatenate(tok0), np.concatenate(con0), np.concatenate(paths)
     nchk = min(8, tok0.shape[0])
-    o_tok, o_con, _ = O.sample_rows(x_host[:nchk], w.params, u_host[:nchk], threads=HOST_THREADS)
+    x_chk = x_host[:nchk]
+    if post is not None:
+        x_chk = O.logit_post(x_chk, post.final_logit_softcapping, post.logit_scale)
+    o_tok, o_con, _ = O.sample_rows(x_chk, params, u_host[:nchk],
+                                    prev_tokens=None if prev is None else prev_host[:nchk], threads=HOST_THREADS)
     parity_ok = bool(np.array_equal(tok0[:nchk], o_tok) and np.array_equal(con0[:nchk], o_con))
     frac = lambda bit: round(float(np.mean((paths & bit) != 0)), 4)  # noqa: E731
     path_fracs = {"stream_norm": frac(llz.PATH_STREAM_NORM), "full_sort": frac(llz.PATH_FULL_SORT),
@@ -270,9 +296,9 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
         "dtype": "f32",
         "data": f"synthetic ({w.text}); numpy default_rng per row; inputs resident in HBM, "
                 f"{nbuf} rotating buffers ({nbuf * batch_bytes / 2**20:.0f} MiB) to defeat the Infinity Cache",
-        "config": {"workload": line, "rows": rows, "vocab": vocab, "temperature": w.params.temperature,
-                   "top_k": w.params.top_k, "top_p": w.params.top_p, "min_p": w.params.min_p,
-                   "typical_p": w.params.typical_p,
+        "config": {"workload": line, "rows": rows, "vocab": vocab, "temperature": params.temperature,
+                   "top_k": params.top_k, "top_p": params.top_p, "min_p": params.min_p,
+                   "typical_p": params.typical_p,
                    "call": ("token, kept probabilities (64) and row statistics" if exact else "token alone"),
                    "parallelism": "none (1 GPU)"},
         "gbps": round(alg / (ms_per_step * 1e-3) / 1e9, 1),
@@ -285,6 +311,11 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
         "paths": path_fracs,
         "parity_spot_check": {"rows": nchk, "ok": parity_ok},
     }
+    if post is not None:
+        out["config"].update(final_logit_softcapping=post.final_logit_softcapping, logit_scale=post.logit_scale)
+    if prev is not None:
+        out["config"].update(repetition_window=params.repetition_window,
+                             repetition_penalty=params.repetition_penalty, history_tokens=int(prev_host.shape[1]))
     if name == "c1":
         out["latency"] = c1_latency(w, x_host, u_host, reps=50)
     del xs, us, call
@@ -294,9 +325,13 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
         reps = -(-64 // min(rows, 64))
         sample = np.ascontiguousarray(np.tile(x_host[: min(rows, 64)], (reps, 1))[:64])
         usample = np.ascontiguousarray(np.tile(u_host[: min(rows, 64)], reps)[:64])
-        out["cpu_baseline"] = cpu_baseline(w, sample, usample, HOST_THREADS, args.cpu_seconds)
-        out["cpu_baseline_1core"] = cpu_baseline(w, sample[: min(16, sample.shape[0])],
-                                                 usample[: min(16, sample.shape[0])], 1, args.cpu_seconds)
+        psample = None
+        if prev is not None:
+            psample = np.ascontiguousarray(np.tile(prev_host[: min(rows, 64)], (reps, 1))[:64])
+        out["cpu_baseline"] = cpu_baseline(w, sample, usample, HOST_THREADS, args.cpu_seconds, params, post, psample)
+        k1 = min(16, sample.shape[0])
+        out["cpu_baseline_1core"] = cpu_baseline(w, sample[:k1], usample[:k1], 1, args.cpu_seconds, params, post,
+                                                 None if psample is None else psample[:k1])
     return out
 
 
@@ -306,7 +341,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--workload", default="headline",
-                    help="headline (default), headline-exact, headline-default, c1 .. c5, or all (one JSON line each)")
+                    help="headline (default), headline-exact, headline-post, headline-penalty, headline-default, "
+                         "c1 .. c5, or all (one JSON line each)")
     ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="wall-clock budget of each CPU baseline mode")
     ap.add_argument("--no-cpu-baseline", action="store_true")

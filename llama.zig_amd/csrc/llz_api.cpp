@@ -288,7 +288,31 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   P.cap = cap;
   P.inv_scale = inv;
   P.rpen = cfg->repetition_penalty;
+  P.rpen_inv = 1.0f / cfg->repetition_penalty;
   P.pen_w = (xf_src & kXfPen) ? window : 0;
+  if (xf_src & kXfCap) {
+    // soft-capping: k_stats estimates the capped logits from a closed form
+    // (cap_est, llz_xform.h) within 20 C 2^-24 of the reference's values (C =
+    // cap inv_scale), max(1, rp, 1/rp) 44 C 2^-24 at penalised positions; the
+    // estimates' relative error grows by est_xe = l2e_t times that (|C| for
+    // a negative logit scale).  Rows with est_xe above 2^-11 (the candidate
+    // margins' budget: 2^-16 + est_xe within the 2^-10 of the thresholds),
+    // or with parameters outside the bound's assumptions, take the exact
+    // streaming path.
+    const double C = (double)cap * (double)inv;
+    const bool pen = (xf_src & kXfPen) != 0u;
+    const double rp = pen ? (double)cfg->repetition_penalty : 1.0;
+    const double bound = (pen ? std::max(1.0, std::max(rp, 1.0 / rp)) * 44.0 : 20.0) * std::fabs(C) * 0x1p-24;
+    const double xe = (double)P.l2e_t * bound * (1.0 + 0x1p-20);
+    const bool ok = cap > 0.0f && std::isfinite(cap) && inv != 0.0f && std::isfinite(inv) && std::fabs(C) < 1.0e30 &&
+                    rp > 0.0 && std::isfinite(rp) && P.l2e_t > 0.0f && std::isfinite(P.l2e_t) && xe <= 0x1p-11;
+    P.cap_a2 = (float)(2.0 * 1.4426950408889634 / (double)cap);
+    P.cap_c = (float)C;
+    if (ok)
+      P.est_xe = (float)xe;
+    else
+      P.flags |= kFlagXfExact;
+  }
   P.prev_stride = prev_stride;
   P.fb_slots = L.fb_slots;
   {

@@ -299,11 +299,12 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
 // Relative error bound of the estimate for terms that matter on grid j
 // (see the header comment), doubled.  bw = |B_w|, the magnitude of the wave's
 // rounded R_w argument fma(m, -RN(log2(e)/T), c_w) (at most 64); t1: T == 1,
-// where the reference's argument takes one rounding instead of two.
-__device__ __forceinline__ float fast_eps(int j, float bw, bool t1) {
+// where the reference's argument takes one rounding instead of two; xe: the
+// estimates' extra error on soft-capped rows (RowParams.est_xe, 0 on others).
+__device__ __forceinline__ float fast_eps(int j, float bw, bool t1, float xe) {
   const float ax = (float)(25 - j);
   const float coef = (t1 ? 3.0f : 4.0f) * ax + 2.0f * bw + 3.0f;
-  return 2.0f * (0.6931472f * coef * 0x1p-24f + 0x1p-21f);
+  return 2.0f * (0.6931472f * coef * 0x1p-24f + 0x1p-21f + xe);
 }
 
 // A float with its mantissa LSB forced to 1 (see the no-tie argument: an
@@ -317,11 +318,11 @@ struct GridConst {
   float tspec;         // rh >= tspec: large term or candidate
 };
 
-__device__ __forceinline__ GridConst grid_const(int j, float R, float theta, float bw, bool t1) {
+__device__ __forceinline__ GridConst grid_const(int j, float R, float theta, float bw, bool t1, float xe) {
   GridConst c;
   c.j = j;
   const float sc = ldexpf(R, 23 - j);
-  const float eps = fast_eps(j, bw, t1);
+  const float eps = fast_eps(j, bw, t1, xe);
   c.sc_lo = odd_mantissa(sc * (1.0f - eps));
   c.sc_hi = odd_mantissa(sc * (1.0f + eps));
   // candidates: e >= theta  =>  e / u >= theta 2^(23-j)

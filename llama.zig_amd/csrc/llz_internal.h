@@ -24,11 +24,18 @@ constexpr uint32_t kFlagTIsOne = 1u;    // temperature == 1.0f exactly: (v - m) 
 constexpr uint32_t kFlagVecSrc = 2u;    // 16-byte loads are legal on the rows the chain reads
 constexpr uint32_t kFlagFallback = 4u;  // the full-row fallback buffers are present
 constexpr uint32_t kFlagTokenOnly = 8u;  // no probabilities or row statistics requested: the token alone
+constexpr uint32_t kFlagXfExact = 16u;   // transformed rows the single pass cannot estimate: the exact streaming path
 
 // RowParams.xf_src / xf_orig: transforms applied as a row is read
 constexpr uint32_t kXfCap = 1u;    // v = tanh(v / cap) * cap   (main.zig:653-658)
 constexpr uint32_t kXfScale = 2u;  // v *= inv_scale            (main.zig:663-666)
 constexpr uint32_t kXfPen = 4u;    // repetition penalty        (sampler.zig:54-75)
+
+// k_stats's transform modes (a template parameter: each mode its own
+// kernel, so the plain rows carry no transform code)
+constexpr int kXmNone = 0;   // rows read as they are
+constexpr int kXmLight = 1;  // logit scale and/or the fused penalty, applied exactly as each segment lands
+constexpr int kXmCap = 2;    // soft-capping: phase L estimates from a closed form, exact values where needed
 
 // per-row status bits (diagnostics)
 constexpr uint32_t kPathSumLe0 = 1u;
@@ -82,6 +89,10 @@ struct RowParams {
   float cap;         // final-logit soft-cap s (kXfCap)
   float inv_scale;   // RN(1 / logit_scale) (kXfScale)
   float rpen;        // repetition penalty (kXfPen)
+  float rpen_inv;    // RN(1 / rpen): kXmCap's estimate of a penalised logit
+  float cap_a2;      // kXmCap: RN(2 log2(e) / cap)
+  float cap_c;       // kXmCap: RN(cap * inv_scale), the soft-capped logits' bound
+  float est_xe;      // kXmCap: bound of the estimates' relative error beyond the plain rows' (0 otherwise)
   int32_t pen_w;     // kXfPen: window length (<= kPenMax)
   int64_t prev_stride;
   int32_t fb_slots;  // full-row fallback buffers in the workspace

@@ -201,30 +201,29 @@ __device__ __forceinline__ float expm1_f32(float x) {
 }
 
 // tanh(x) for f32, the tanhf.c algorithm as musl carries it: by |x|,
-// 1 - 2 / (expm1(2|x|) + 2), expm1(2|x|) / (expm1(2|x|) + 2) or
-// -expm1(-2|x|) / (expm1(-2|x|) + 2), with the sign put back.
+//   |x| > 10 (or NaN):         1 + 0 / |x|
+//   |x| > log(3) / 2:          1 - 2 / (expm1(2|x|) + 2)
+//   |x| > log(5/3) / 2:        expm1(2|x|) / (expm1(2|x|) + 2)
+//   normal:                    -expm1(-2|x|) / (expm1(-2|x|) + 2)
+//   subnormal or zero:         |x|
+// with the sign put back.  Every lane evaluates one expm1 and one division
+// with the operands its range selects (each range's operations and their
+// order are the branch's own, so the value is the branchy form's bit for
+// bit), which keeps the code and its live registers to one copy where a
+// kernel applies it to many logits at once.
 __device__ __forceinline__ float tanh_f32(float x) {
   const uint32_t ux = fbits(x);
   const uint32_t w = ux & 0x7fffffffu;
   const bool sign = (ux >> 31) != 0;
   const float ax = bitsf(w);
-  float t;
-  if (w > 0x3f0c9f54u) {    // |x| > log(3) / 2, or NaN
-    if (w > 0x41200000u) {  // |x| > 10
-      t = 1.0f + 0.0f / ax;
-    } else {
-      t = expm1_f32(2.0f * ax);
-      t = 1.0f - 2.0f / (t + 2.0f);
-    }
-  } else if (w > 0x3e82c578u) {  // |x| > log(5/3) / 2
-    t = expm1_f32(2.0f * ax);
-    t = t / (t + 2.0f);
-  } else if (w >= 0x00800000u) {  // normal
-    t = expm1_f32(-2.0f * ax);
-    t = -t / (t + 2.0f);
-  } else {  // subnormal or zero
-    t = ax;
-  }
+  const bool huge = w > 0x41200000u;  // |x| > 10, or not finite
+  const bool big = w > 0x3f0c9f54u;   // |x| > log(3) / 2
+  const bool mid = w > 0x3e82c578u;   // |x| > log(5/3) / 2
+  const float e = expm1_f32(mid ? 2.0f * ax : -2.0f * ax);
+  const float num = huge ? 0.0f : (big ? 2.0f : (mid ? e : -e));
+  const float q = num / (huge ? ax : e + 2.0f);
+  float t = huge ? 1.0f + q : (big ? 1.0f - q : q);
+  t = w < 0x00800000u ? ax : t;  // subnormal or zero
   return sign ? -t : t;
 }
 

@@ -696,7 +696,9 @@ __device__ __forceinline__ const KArgs* kernel_args_ptr() {
 template <class Src>
 __device__ __forceinline__ Src make_src(const RowParams& P, const RowPtrs& Q, int row, const PenShared* pen) {
   if constexpr (std::is_same<Src, RowSrc>::value) {
-    return row_src(P, Q, row, pen);
+    return row_src<true>(P, Q, row, pen);
+  } else if constexpr (std::is_same<Src, LightSrc>::value) {
+    return row_src<false>(P, Q, row, pen);
   } else {
     return PlainSrc{Q.src + (int64_t)row * P.src_stride};
   }
@@ -994,10 +996,10 @@ __device__ __forceinline__ bool select_short(const RowParams& P, const RowPtrs& 
 // calls it; `sh` may alias the caller's shared memory once all of it is read.
 // pre_ok: thread 64 + i holds candidate i in cand_pre for i < cand_n0, and
 // cc_in <= 448 (the later ones are read here).
-template <class Src>
+template <class Src, class OSrc>
 __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q, SampleShared& sh, float m,
                                            float S, uint32_t cc_in, bool uncertified, float u_row, bool pre_ok,
-                                           uint64_t cand_pre, uint32_t cand_n0, const Src& X, const Src& O,
+                                           uint64_t cand_pre, uint32_t cand_n0, const Src& X, const OSrc& O,
                                            const PenShared* pen, const KArgs* A, int row) {
   int bank = 0;
   const int t = (int)threadIdx.x;

@@ -369,9 +369,12 @@ __device__ __forceinline__ void resolve_ahead(uint32_t& N_io, int& j_io, int slo
 // the integer sum before a tie (all that decides it) is that of the lane's
 // queued prefix, plus the corrections of the segment's lanes below it, plus
 // the lane's exact roundings before it.
-__device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q, const RowParams& P, int row, int w,
-                                                int qn, const float4 (&v4q)[2], float Rw, float cw, float m,
-                                                float theta, bool t1) {
+// v4q: the queued lanes' logits as the chain reads them, or raw (kXmCap:
+// phase L's estimate and the exact value are both taken from them here).
+template <int XM, class Src>
+__device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q, const RowParams& P, const Src& X,
+                                                int row, int w, int qn, const float4 (&v4q)[2], float Rw, float cw,
+                                                float m, float theta, bool t1) {
   const int lane = lane_id();
   const float bw = F.bw[w];  // |aw| of this wave (phase M)
   const int n = P.n;
@@ -389,13 +392,18 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
     pos2[h] = qp & 0x7fffffffu;
     pre2[h] = qp >> 31;  // parity: only that decides a tie
     j2[h] = F.sj[pos2[h] >> 8];
-    const GridConst gc = grid_const(j2[h], Rw, theta, bw, t1);
+    const GridConst gc = grid_const(j2[h], Rw, theta, bw, t1, P.est_xe);
     const uint32_t tspec = __float_as_uint(gc.tspec);
     const float vv[4] = {v4q[h].x, v4q[h].y, v4q[h].z, v4q[h].w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const bool present = act2[h] && (int)pos2[h] + c < n;
-      const float q = present ? __builtin_amdgcn_exp2f(fmaf(vv[c], P.l2e_t, -cw)) : 0.0f;  // phase L's q, bit for bit
+      float vq = vv[c];
+      if constexpr (XM == kXmCap) {  // phase L's estimate of the soft-capped (and penalised) logit
+        vq = cap_est(vq, P.cap_a2, P.cap_c);
+        if (present && (X.xf & kXfPen) && X.penalised((int)pos2[h] + c)) vq = pen_est(vq, P.rpen, P.rpen_inv);
+      }
+      const float q = present ? __builtin_amdgcn_exp2f(fmaf(vq, P.l2e_t, -cw)) : 0.0f;  // phase L's q, bit for bit
       const uint32_t lo = __float_as_uint(fmaf(q, gc.sc_lo, MAGIC));
       const uint32_t hi = __float_as_uint(fmaf(q, gc.sc_hi, MAGIC));
       rl[h][c] = lo - MAGIC_BITS;
@@ -410,7 +418,8 @@ __device__ __forceinline__ void settle_specials(FastShared& F, const RowPtrs& Q,
     rem &= rem - 1u;
     const int h = bt >> 2, c = bt & 3;
     const float4 vh = h == 0 ? v4q[0] : v4q[1];
-    const float v = c == 0 ? vh.x : c == 1 ? vh.y : c == 2 ? vh.z : vh.w;
+    float v = c == 0 ? vh.x : c == 1 ? vh.y : c == 2 ? vh.z : vh.w;
+    if constexpr (XM == kXmCap) v = X.fix((int)(h == 0 ? pos2[0] : pos2[1]) + c, v);  // the exact value
     const float e = exact_term(v, m, P.temperature, t1);
     bool tie;
     const uint32_t r = grid_round(e, h == 0 ? j2[0] : j2[1], tie);
@@ -518,8 +527,9 @@ __device__ __noinline__ int claim_row(unsigned long long* word, unsigned long lo
 // segment through buffer loads); otherwise element loads.  XF: the rows are
 // read through post-processing and/or the fused repetition penalty
 // (llz_xform.h); otherwise as they are.
-template <bool FASTLD, bool XF>
+template <bool FASTLD, int XM>
 __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& U, PenShared& pen_sh) {
+  constexpr bool XF = XM != kXmNone;
   const RowParams P = A.P;
   const RowPtrs Q = A.Q;
   constexpr int dcap = DCAP;  // EXACT slots per round
@@ -532,10 +542,13 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   const float* xr = Q.src + (int64_t)row * P.src_stride;
   // reads of the row through the caller's post-processing and the penalty
   // (plain reads when !XF)
-  using Src = typename std::conditional<XF, RowSrc, PlainSrc>::type;
-  Src X, O;  // the chain's input; sampleArgmax's input (sampler.zig:89)
+  using Src = typename std::conditional<XM == kXmCap, RowSrc,
+                                        typename std::conditional<XF, LightSrc, PlainSrc>::type>::type;
+  using OSrc = typename std::conditional<XF, RowSrc, PlainSrc>::type;
+  Src X;   // the chain's input
+  OSrc O;  // sampleArgmax's input (sampler.zig:89)
   if constexpr (XF) {
-    X = row_src(P, Q, row, &pen_sh);
+    X = row_src<XM == kXmCap>(P, Q, row, &pen_sh);
     O = row_orig(P, Q, row);
   } else {
     X = PlainSrc{xr};
@@ -549,21 +562,34 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       pen_wm = uni_u64(pen_sh.wmask[w]);
     }
   }
-  // one landed segment's logits (k: the wave's segment index) through the
-  // transforms: post-processing on every element, the penalty only in the
-  // segments that hold a penalised position
-  auto seg_fix = [&](int k, float4 v) {
-    if constexpr (XF) {
+  // Phase L's per-element work is the plain rows' plus, at most, one
+  // multiply (kXmLight: the logit scale; 1 without one, v * 1 == v) or the
+  // soft-cap estimate (kXmCap: cap_est on the raw logit, after the raw
+  // maximum has taken it).  The penalty is applied to the few elements it
+  // touches after the loop (the loop holds the row's register segments and
+  // six loads in flight: any code that branches on the penalty inside it
+  // costs registers it does not have).
+  const float xscale = (XM == kXmLight && (P.xf_src & kXfScale)) ? P.inv_scale : 1.0f;
+  auto seg_in = [&](const int k, float4 v) -> float4 {
+    if constexpr (XM == kXmLight) {
       const int pos = (w + W * k) * SEG + lane * 4;
-      v = X.pre4(pos, v, n);
-      if ((pen_wm >> (k & 63)) & 1ull) v = X.pen4(pos, v, n);
+      v.x = (FASTLD || pos + 0 < n) ? v.x * xscale : v.x;
+      v.y = (FASTLD || pos + 1 < n) ? v.y * xscale : v.y;
+      v.z = (FASTLD || pos + 2 < n) ? v.z * xscale : v.z;
+      v.w = (FASTLD || pos + 3 < n) ? v.w * xscale : v.w;
     }
+    return v;
+  };
+  // the estimate's source value of a maximum-source value v (kXmCap: its
+  // soft-cap estimate)
+  auto est_of = [&](float v) -> float {
+    if constexpr (XM == kXmCap) return cap_est(v, P.cap_a2, P.cap_c);
     return v;
   };
   const float l2e_t = P.l2e_t;
   const int G = (n + SEG - 1) / SEG;
   const int SPW = (G + W - 1) / W;
-  const bool fits = SPW <= SPWMAX && P.cand_theta > 0.0f && fabsf(l2e_t) <= 0x1p40f;
+  const bool fits = SPW <= SPWMAX && P.cand_theta > 0.0f && fabsf(l2e_t) <= 0x1p40f && !(P.flags & kFlagXfExact);
   // the row's uniform, read now: the selection stage's draw needs it at the
   // end of a long serial path (a memory barrier keeps the load here)
   const float u_row = Q.uniforms[row];
@@ -595,8 +621,23 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   auto seg_q = [&](const int k, float4 v) {
     const bool ok = lane4 < seg_lim(k);
     const float ck = ok ? cw : kInfS;
-    const float m = max3_raw(max3_raw(mx, v.x, v.y), v.z, v.w);
-    mx = ok ? m : mx;
+    if constexpr (XM != kXmCap) {  // kXmCap: the maximum comes from the estimates after the loop
+      const float m = max3_raw(max3_raw(mx, v.x, v.y), v.z, v.w);
+      mx = ok ? m : mx;
+    }
+    if constexpr (XM == kXmCap) {  // in place
+      v.x = est_of(v.x);
+      v.y = est_of(v.y);
+      v.z = est_of(v.z);
+      v.w = est_of(v.w);
+      if constexpr (!FASTLD) {  // single positions past the row: no estimate (q = 0)
+        const int pos = (w + W * k) * SEG + lane4;
+        v.x = pos + 0 < n ? v.x : -kInfS;
+        v.y = pos + 1 < n ? v.y : -kInfS;
+        v.z = pos + 2 < n ? v.z : -kInfS;
+        v.w = pos + 3 < n ? v.w : -kInfS;
+      }
+    }
     return q_of(v, l2e_t, ck);
   };
   // segment sums: lane k of my_a holds segment k's (stored after the loop)
@@ -639,17 +680,17 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         if (k < nseg_w) {
           lds_dma_wait<kLoadWindow - 1>();  // the window's loads behind it (the register ones come later)
           float4* p = reinterpret_cast<float4*>(&F.u.data[w][i][lane * 4]);
-          const float4 v = seg_fix(k, *p);
-          if (i == 0) set_cw(wave_max_f32(lane4 < seg_lim(k) ? max4(v) : -kInfS));  // the first segment processed
+          const float4 v = seg_in(k, *p);
+          if (i == 0) set_cw(wave_max_f32(lane4 < seg_lim(k) ? est_of(max4(v)) : -kInfS));  // the first segment processed
           const float4 q = seg_q(k, v);
           *p = q;
           seg_sum(k, q);
         }
       } else {
         const int k = i - KL;
-        d[k] = seg_fix(k, d[k]);
-        if (k == 0 && nseg_w <= KV) set_cw(wave_max_f32(lane4 < seg_lim(0) ? max4(d[0]) : -kInfS));
-        float4 q = seg_q(k, d[k]);  // a NaN logit makes its segment sum NaN
+        const float4 v = seg_in(k, d[k]);
+        if (k == 0 && nseg_w <= KV) set_cw(wave_max_f32(lane4 < seg_lim(0) ? est_of(max4(v)) : -kInfS));
+        float4 q = seg_q(k, v);  // a NaN logit makes its segment sum NaN
         // materialise q here, while the loads land (not sunk into phase S)
         asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
         d[k] = q;
@@ -666,12 +707,13 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     for (int k = 0; k < KV; ++k) d[k] = ld1x4(xr, base_w + k * (W * SEG), k < nseg_w ? n : 0);
     for (int k = KV; k < nseg_w; ++k) seg_to_lds(xr, w + W * k, n, false, &F.u.data[w][k - KV][0]);
     __builtin_amdgcn_sched_barrier(0);
-    d[0] = seg_fix(0, d[0]);
-    set_cw(wave_max_f32(lane4 < seg_lim(0) ? max4(d[0]) : -kInfS));
+    const float4 v0 = seg_in(0, d[0]);
+    set_cw(wave_max_f32(lane4 < seg_lim(0) ? est_of(max4(v0)) : -kInfS));
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
-      if (k > 0) d[k] = seg_fix(k, d[k]);
-      float4 q = seg_q(k, d[k]);
+      float4 v = v0;
+      if (k > 0) v = seg_in(k, d[k]);
+      float4 q = seg_q(k, v);
       asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
       d[k] = q;
       seg_sum(k, q);
@@ -679,9 +721,55 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     }
     for (int k = KV; k < nseg_w; ++k) {
       float4* p = reinterpret_cast<float4*>(&F.u.data[w][k - KV][lane * 4]);
-      const float4 q = seg_q(k, seg_fix(k, *p));
+      const float4 q = seg_q(k, seg_in(k, *p));
       *p = q;
       seg_sum(k, q);
+    }
+  }
+  // ---- the penalty (sampler.zig:54-75) on this wave's penalised elements,
+  // after the loop.  Lane j takes the row's penalised position j when it lies
+  // in one of this wave's segments: it reads the logit, and the element's
+  // estimate becomes the one phase L would have computed for the penalised
+  // value (kXmLight: penalise(v s), exact; kXmCap: pen_est of the soft-cap
+  // estimate); each touched segment's sum of estimates is folded again as
+  // phase L folds it.  LDS-resident segments take the estimate from the lane
+  // that holds the position, register segments from the lane that owns it.
+  uint32_t pen_p = 0xffffffffu;  // this lane's penalised position (of this wave's segments)
+  float pen_r = 0.0f;            // its logit as the caller wrote it
+  if constexpr (XF) {
+    if (fits && pen_wm != 0ull) {
+      const uint32_t pp = lane < pen_sh.n ? pen_sh.pos[lane] : 0xffffffffu;
+      const bool mine = pp != 0xffffffffu && ((pp >> 8) & (uint32_t)(W - 1)) == (uint32_t)w;
+      pen_p = mine ? pp : 0xffffffffu;
+      pen_r = mine ? xr[pp] : 0.0f;
+      const float src = XM == kXmCap ? pen_est(est_of(pen_r), P.rpen, P.rpen_inv) : penalise(pen_r * xscale, P.rpen);
+      const float qn = __builtin_amdgcn_exp2f(fmaf(src, l2e_t, -cw));
+      const int kk = (int)(pp >> 11);  // the wave's segment index k of segment pp >> 8 = w + W k
+      if (mine && kk >= KV) F.u.data[w][kk - KV][pp & (uint32_t)(SEG - 1)] = qn;
+#pragma unroll
+      for (int k = 0; k < KV; ++k) {
+        if ((pen_wm >> k) & 1ull) {
+          uint64_t bm = bal64(mine && kk == k);
+          while (bm != 0ull) {
+            const int b = __ffsll((long long)bm) - 1;
+            bm &= bm - 1ull;
+            const uint32_t pb = readlane_u32(pp, b);
+            const float qb = __uint_as_float(readlane_u32(__float_as_uint(qn), b));
+            const uint32_t c = pb & 3u;
+            const bool own = (uint32_t)lane == ((pb >> 2) & 63u);
+            d[k].x = own && c == 0u ? qb : d[k].x;
+            d[k].y = own && c == 1u ? qb : d[k].y;
+            d[k].z = own && c == 2u ? qb : d[k].z;
+            d[k].w = own && c == 3u ? qb : d[k].w;
+          }
+          seg_sum(k, d[k]);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();  // this wave's own LDS writes: LDS order suffices
+      for (uint64_t rest = pen_wm >> KV; rest != 0ull; rest &= rest - 1ull) {
+        const int k = KV + __ffsll((long long)rest) - 1;
+        seg_sum(k, *reinterpret_cast<const float4*>(&F.u.data[w][k - KV][lane * 4]));
+      }
     }
   }
   if (lane < nseg_w) F.v.aseg[w + W * lane] = my_a;
@@ -716,6 +804,52 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     }
   }
   mx = wave_max_f32(mx);
+  if constexpr (XF) {
+    if (fits) {
+      // The wave's exact maximum from the estimates as they stand (penalised
+      // elements patched): an element of the largest value has the largest
+      // term, and every estimate lies within eps of its term (2^-16 on the
+      // scaled rows, 2^-16 + est_xe <= 2^-10.9 on soft-capped ones), so its
+      // q >= q_max (1 - eps) / (1 + eps) >= q_max (1 - 2^-9); each lane's
+      // segments holding such an estimate are read again and evaluated
+      // exactly.  (Nothing here takes f(max) for max(f): tanh_f32, like the
+      // reference's tanhf, is not monotone between adjacent floats.)
+      auto scan_max = [&]() -> float {
+        float ql = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KV; ++k) ql = fmaxf(ql, max4(d[k]));  // absent lanes and segments hold q = 0
+        for (int k = KV; k < nseg_w; ++k) ql = fmaxf(ql, max4(*reinterpret_cast<const float4*>(&F.u.data[w][k - KV][lane * 4])));
+        const float qthr = wave_max_f32(ql) * (1.0f - 0x1p-9f);
+        uint64_t sm = 0ull;
+#pragma unroll
+        for (int k = 0; k < KV; ++k) sm |= (max4(d[k]) >= qthr ? 1ull : 0ull) << k;
+        for (int k = KV; k < nseg_w; ++k)
+          sm |= (max4(*reinterpret_cast<const float4*>(&F.u.data[w][k - KV][lane * 4])) >= qthr ? 1ull : 0ull) << k;
+        float ex = -kInfS;
+        while (sm != 0ull) {
+          const int k = __ffsll((long long)sm) - 1;
+          sm &= sm - 1ull;
+          const int pos = (w + W * k) * SEG + lane4;
+#pragma unroll 1
+          for (int c = 0; c < 4; ++c)
+            if (pos + c < n) ex = fmaxf(ex, X.at(pos + c));
+        }
+        return wave_max_f32(ex);
+      };
+      if constexpr (XM == kXmCap) {
+        // phase L took no maximum (the soft-cap's exact value costs some
+        // sixty operations; the estimates locate the largest elements)
+        mx = scan_max();
+      } else if (pen_wm != 0ull) {
+        // phase L's maximum is that of the scaled logits, the penalised
+        // ones at their unpenalised values: when none of those held it, the
+        // others' maximum stands and the penalised values join it
+        const bool mine = pen_p != 0xffffffffu;
+        const bool top = bal64(mine && pen_r * xscale == mx) != 0ull;
+        mx = top ? scan_max() : fmaxf(mx, wave_max_f32(mine ? penalise(X.pre(pen_r), P.rpen) : -kInfS));
+      }
+    }
+  }
   // token-only rows: the lanes that may hold a candidate (a term that may
   // reach thr_e; Rw scales this wave's estimates q to terms), queued in
   // F.qpos[w] and re-read into tv.  The segments whose estimated sum reaches
@@ -760,7 +894,8 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       for (int h = 0; h < QCAP / kWave; ++h) {
         const int i = h * kWave + lane;
         const int pos = i < nq ? (int)F.qpos[w][i] : 0;
-        tv[h] = X.fix4(pos, FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n), n);
+        const float4 r = FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n);
+        tv[h] = XM == kXmCap ? r : X.fix4(pos, r, n);  // kXmCap: raw (transformed where they are used)
       }
     } else {
 #pragma unroll
@@ -867,7 +1002,15 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         uint32_t mk = 0u;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const bool pass = live && tpos[h] + c < n && __builtin_amdgcn_exp2f(fmaf(vs[c], l2e_t, -cw)) >= thr_q;
+          // kXmCap: the element's estimate (soft-cap, and the penalty where it
+          // applies), within 2^-16 + est_xe <= 2^-10.9 of the term, inside
+          // thr_e's margin of 2^-10
+          float vq = vs[c];
+          if constexpr (XM == kXmCap) {
+            vq = est_of(vq);
+            if ((P.xf_src & kXfPen) && live && X.penalised(tpos[h] + c)) vq = pen_est(vq, P.rpen, P.rpen_inv);
+          }
+          const bool pass = live && tpos[h] + c < n && __builtin_amdgcn_exp2f(fmaf(vq, l2e_t, -cw)) >= thr_q;
           mk |= pass ? (1u << c) : 0u;
         }
         tmk[h] = mk;
@@ -896,7 +1039,9 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         uint32_t id = 0u;
         if (lane < ttot) {
           id = sg[2 * lane + 1];
-          e = exact_term(__uint_as_float(sg[2 * lane]), m, P.temperature, t1);  // sampler.zig:85
+          float v = __uint_as_float(sg[2 * lane]);
+          if constexpr (XM == kXmCap) v = X.fix((int)id, v);  // the exact value of a raw re-read
+          e = exact_term(v, m, P.temperature, t1);  // sampler.zig:85
         }
         const bool cand = lane < ttot && e >= theta_t;
         const uint64_t cb = bal64(cand);
@@ -912,7 +1057,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         for (int h = 0; h < NH; ++h) {
           if (tmk[h] != 0u) {
             const int pos = tpos[h];
-            const float4 e = exact_terms4(tv[h], m, P.temperature, t1);  // sampler.zig:85
+            const float4 e = exact_terms4(XM == kXmCap ? X.fix4(pos, tv[h], n) : tv[h], m, P.temperature, t1);  // sampler.zig:85
             const float es[4] = {e.x, e.y, e.z, e.w};
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -1084,10 +1229,11 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       for (int h = 0; h < 2; ++h) {
         const int i = h * kWave + lane;
         const int pos = i < cnt ? (int)(F.qpos[w][i] & 0x7fffffffu) : 0;
-        v4q[h] = X.fix4(pos, FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n), n);
+        const float4 r = FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n);
+        v4q[h] = XM == kXmCap ? r : X.fix4(pos, r, n);  // kXmCap: raw (settle_specials transforms them)
       }
     };
-    auto settle = [&](int cnt) { settle_specials(F, Q, P, row, w, cnt, v4q, Rw, cw, m, theta, t1); };
+    auto settle = [&](int cnt) { settle_specials<XM>(F, Q, P, X, row, w, cnt, v4q, Rw, cw, m, theta, t1); };
     // The queue is filled in chunks of at most qcap <= QCAP entries, each holding
     // whole batches (a segment's lanes are settled together): chunk 0 in LDS,
     // chunks 1.. in this row's overflow area of the workspace, kQovfWave
@@ -1105,7 +1251,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       // that are not PLAIN (or absent) get zero scales and an unreachable
       // tspec, so every bracket is MAGIC and no lane is special
       const bool plain_l = have && F.sflag[w + W * lane] == (uint8_t)PLAIN;
-      const GridConst gc_l = grid_const(have ? (int)F.sj[w + W * lane] : 0, Rw, theta, fabsf(aw), t1);
+      const GridConst gc_l = grid_const(have ? (int)F.sj[w + W * lane] : 0, Rw, theta, fabsf(aw), t1, P.est_xe);
       const float sclo_l = plain_l ? gc_l.sc_lo : 0.0f;
       const float schi_l = plain_l ? gc_l.sc_hi : 0.0f;
       const uint32_t tsp_l = plain_l ? __float_as_uint(gc_l.tspec) : 0xffffffffu;
@@ -1519,11 +1665,11 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
 }
 
 // One row per workgroup: launches whose rows fit the CUs at once.
-template <bool FASTLD, bool XF>
+template <bool FASTLD, int XM>
 __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
   __shared__ StatsShared U;
   __shared__ PenShared pen_sh;  // kXfPen: the row's penalised positions
-  stats_row<FASTLD, XF>(A, (int)blockIdx.x, U, pen_sh);
+  stats_row<FASTLD, XM>(A, (int)blockIdx.x, U, pen_sh);
 }
 
 // More rows than CUs: one workgroup per CU (all resident), each taking rows
@@ -1531,7 +1677,7 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
 // left, so rows of unequal cost spread over every CU.  (Launched one row per
 // workgroup instead, the hardware hands workgroups to the XCDs in turn, so a
 // batch whose cost alternates from row to row loads half of the XCDs only.)
-template <bool FASTLD, bool XF>
+template <bool FASTLD, int XM>
 __global__ __launch_bounds__(NT) void k_stats_rows(KArgs A) {
   __shared__ StatsShared U;
   __shared__ PenShared pen_sh;
@@ -1543,7 +1689,7 @@ __global__ __launch_bounds__(NT) void k_stats_rows(KArgs A) {
     const __attribute__((address_space(4))) KArgs* Ap =
         (const __attribute__((address_space(4))) KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(Ap));
-    stats_row<FASTLD, XF>(*(const KArgs*)Ap, row, U, pen_sh);
+    stats_row<FASTLD, XM>(*(const KArgs*)Ap, row, U, pen_sh);
     if (threadIdx.x == 0) next_row = claim_row(A.Q.claim, A.P.epoch, A.P.grid);
     __syncthreads();  // also: every wave is done with this row's shared memory
     row = next_row;
@@ -1558,26 +1704,31 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
                          hipStream_t st) {
   if (ev_begin && hipEventRecord(ev_begin, st) != hipSuccess) return hipErrorUnknown;
   const bool fastld = (P.flags & kFlagVecSrc) != 0 && (P.n % 4) == 0;
-  const bool xf = P.xf_src != 0u || P.xf_orig != 0u;
+  // the transform mode: soft-capping (the chain's input) takes the
+  // estimating single pass, the scale and the penalty alone the exact one
+  const int xm = (P.xf_src & kXfCap) ? kXmCap : ((P.xf_src | P.xf_orig) != 0u ? kXmLight : kXmNone);
+  const KArgs A{P, Q};
   // more rows than workgroups: the grid's workgroups claim rows (the
   // special-queue overflow area has one block per workgroup of the grid)
-  if (P.grid < P.rows) {
-    if (fastld && !xf)
-      hipLaunchKernelGGL((k_stats_rows<true, false>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
-    else if (fastld)
-      hipLaunchKernelGGL((k_stats_rows<true, true>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
-    else if (!xf)
-      hipLaunchKernelGGL((k_stats_rows<false, false>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
+  const bool claim = P.grid < P.rows;
+  const dim3 grid(claim ? P.grid : P.rows), block(NT);
+  void (*kern)(KArgs) = nullptr;
+  if (claim) {
+    if (fastld)
+      kern = xm == kXmNone ? k_stats_rows<true, kXmNone> : xm == kXmLight ? k_stats_rows<true, kXmLight>
+                                                                          : k_stats_rows<true, kXmCap>;
     else
-      hipLaunchKernelGGL((k_stats_rows<false, true>), dim3(P.grid), dim3(NT), 0, st, KArgs{P, Q});
-  } else if (fastld && !xf)
-    hipLaunchKernelGGL((k_stats<true, false>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
-  else if (fastld)
-    hipLaunchKernelGGL((k_stats<true, true>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
-  else if (!xf)
-    hipLaunchKernelGGL((k_stats<false, false>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
-  else
-    hipLaunchKernelGGL((k_stats<false, true>), dim3(P.rows), dim3(NT), 0, st, KArgs{P, Q});
+      kern = xm == kXmNone ? k_stats_rows<false, kXmNone> : xm == kXmLight ? k_stats_rows<false, kXmLight>
+                                                                           : k_stats_rows<false, kXmCap>;
+  } else {
+    if (fastld)
+      kern = xm == kXmNone ? k_stats<true, kXmNone> : xm == kXmLight ? k_stats<true, kXmLight> : k_stats<true, kXmCap>;
+    else
+      kern = xm == kXmNone ? k_stats<false, kXmNone> : xm == kXmLight ? k_stats<false, kXmLight>
+                                                                      : k_stats<false, kXmCap>;
+  }
+  void* args[] = {const_cast<KArgs*>(&A)};
+  if (hipLaunchKernel((const void*)kern, grid, block, args, 0, st) != hipSuccess) return hipErrorLaunchFailure;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (ev_end && hipEventRecord(ev_end, st) != hipSuccess) return hipErrorUnknown;

@@ -20,8 +20,8 @@
 //     C_q / S, with top_p: that needs S itself.  The reference's S is the
 //     sequential f32 sum of n positive terms, within (n - 1) 2^-24 / (1 - (n -
 //     1) 2^-24) of the real sum (the recursive-summation bound), which phase
-//     L's estimates give to 2^-14; a top-p decision that holds at both ends
-//     of that interval holds at S.
+//     L's estimates give to 2^-14 (2^-14 + est_xe on soft-capped rows); a
+//     top-p decision that holds at both ends of that interval holds at S.
 // A row whose decisions all hold is finished here, bit-exact; any other row
 // continues with the exact phases.
 #pragma once
@@ -139,7 +139,7 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   const int Lc = open_end ? M : L;
   // the interval of the reference's normaliser
   const double g = (double)(n - 1) * 0x1p-24;
-  const double gr = g / (1.0 - g) + 0x1p-14;
+  const double gr = g / (1.0 - g) + 0x1p-14 + (double)P.est_xe;  // est_xe: soft-capped rows' estimates
   const double S_lo = (double)s_est * (1.0 - gr), S_hi = (double)s_est * (1.0 + gr);
   if (!(S_lo > 0.0) || !(S_hi < 1.0e300)) ok = false;
   // 1/S at the interval's ends, rounded outwards (one rounding of 2^-53 each)

@@ -35,6 +35,39 @@ __device__ __forceinline__ float logit_post(float v, uint32_t xf, float cap, flo
 // sampler.zig:65-69 on a logit of a penalised position.
 __device__ __forceinline__ float penalise(float v, float rp) { return v > 0.0f ? v / rp : v * rp; }
 
+// Soft-capped rows (kXmCap): the single pass's estimate of a logit's
+// post-processed value f(r) = RN(RN(tanh(RN(r / cap)) cap) inv) from the
+// closed form C tanh(z) = C - 2C / (exp(2z) + 1), z = r / cap, C = cap inv:
+//   v~ = RN(RN(rc (-2C)) + C),  rc = rcp(RN(exp2(RN(r a2)) + 1)),
+//   a2 = RN(2 log2(e) / cap),
+// one hardware exp2 and one reciprocal where the exact tanh takes some sixty
+// operations.  Error against f (first order, in units of C 2^-24, the
+// hardware exp2 and rcp within 1 ulp):
+//   v~ against C tanh(z): the exp2 argument's two roundings and the exp2
+//   move 1 / (e^(2z) + 1) by a relative (|2z| + 1) 2^-23 (1 - rho), rho =
+//   1 / (e^(2z) + 1), and 2 rho (1 - rho) (|2z| + 1) 2^-23 <= 1.6 units;
+//   the sum's rounding and the reciprocal add 2 rho 3 2^-24 <= 6; C's
+//   rounding, the product's (|2C rc| 2^-24 <= 2 units) and the sum's 4:
+//   11.6 units;
+//   f against C tanh(z): RN(r / cap) moves tanh by at most max z sech^2 z
+//   < 0.45 units; tanh_f32 is within 3 units of tanh (checked on every
+//   float); the two products' roundings add 1 unit each: 6.45 units;
+// so |v~ - f| < 20 C 2^-24.  A penalised position's estimate pen_est(v~)
+// (sampler.zig:65-69 with a multiply by RN(1 / rp)) lies within
+// max(1, rp, 1 / rp) (2 * 20 + 3) C 2^-24 of the reference's value (the
+// doubled term covers a sign that v~ and f do not share; the 3 units are
+// RN(1 / rp) and the two sides' roundings).  The host turns the bound
+// (taken as 44 units with the penalty) into est_xe = l2e_t * bound, the
+// estimates' extra relative error (exp2 of an argument off by l2e_t |dv| is
+// off by ln 2 l2e_t |dv| to first order; the factor 1 / ln 2 covers the
+// rest), and takes the single pass only where est_xe <= 2^-11.
+__device__ __forceinline__ float cap_est(float r, float a2, float c) {
+  const float e = __builtin_amdgcn_exp2f(r * a2);
+  const float rc = __builtin_amdgcn_rcpf(e + 1.0f);
+  return rc * (-2.0f * c) + c;  // a product and a sum: one uniform operand each (an fma would hold -2C in a VGPR)
+}
+__device__ __forceinline__ float pen_est(float v, float rp, float rp_inv) { return v > 0.0f ? v * rp_inv : v * rp; }
+
 // The penalised positions of one row, ascending, and for each of the
 // single-pass kernel's eight waves the segments (256 logits; wave w owns
 // segments w, w + 8, ...) holding one: bit k of wmask[w] for segment w + 8k.
@@ -78,14 +111,24 @@ __device__ __forceinline__ void pen_build(PenShared& ps, const RowParams& P, con
   }
 }
 
-// A row of logits as the chain reads it (see the file comment).
-struct RowSrc {
+// A row of logits as the chain reads it (see the file comment).  CAP =
+// false: a row whose transforms include no soft-capping (kXmLight), without
+// the tanh code, which a kernel would otherwise carry (and hold registers
+// for) wherever it reads the row.
+template <bool CAP>
+struct RowSrcT {
   const float* x;       // the row as the caller passed it
   uint32_t xf;          // kXf* bits applied on reads through at() / load4()
   float cap, inv_scale, rp;
   const PenShared* pen; // penalised positions (kXfPen)
 
-  __device__ __forceinline__ float pre(float v) const { return logit_post(v, xf, cap, inv_scale); }
+  __device__ __forceinline__ float pre(float v) const {
+    if constexpr (CAP) {
+      return logit_post(v, xf, cap, inv_scale);
+    } else {
+      return (xf & kXfScale) ? v * inv_scale : v;
+    }
+  }
 
   __device__ __forceinline__ bool penalised(int i) const {
     const int np = pen->n;
@@ -146,6 +189,9 @@ struct RowSrc {
   }
 };
 
+using RowSrc = RowSrcT<true>;
+using LightSrc = RowSrcT<false>;
+
 // A row read as it is (no post-processing, no fused penalty): the same
 // interface as RowSrc with no transform code, so kernels that do not
 // transform compile as if they read the pointer directly.
@@ -170,8 +216,9 @@ struct PlainSrc {
 
 // The chain's view of row `row` (src: the caller's rows, or the penalised
 // copy) and sampleArgmax's view (the caller's rows, post-processing only).
-__device__ __forceinline__ RowSrc row_src(const RowParams& P, const RowPtrs& Q, int row, const PenShared* pen) {
-  return RowSrc{Q.src + (int64_t)row * P.src_stride, P.xf_src, P.cap, P.inv_scale, P.rpen, pen};
+template <bool CAP = true>
+__device__ __forceinline__ RowSrcT<CAP> row_src(const RowParams& P, const RowPtrs& Q, int row, const PenShared* pen) {
+  return RowSrcT<CAP>{Q.src + (int64_t)row * P.src_stride, P.xf_src, P.cap, P.inv_scale, P.rpen, pen};
 }
 __device__ __forceinline__ RowSrc row_orig(const RowParams& P, const RowPtrs& Q, int row) {
   return RowSrc{Q.orig + (int64_t)row * P.orig_stride, P.xf_orig & ~kXfPen, P.cap, P.inv_scale, 1.0f, nullptr};

@@ -335,11 +335,16 @@ class PreparedCall:
     statistics may finish rows without the exact normaliser."""
 
     def __init__(self, rows: int, vocab: int, cfg: SamplerConfig, device, *, kept_cap: int = 0,
-                 probs: bool = False, stats: bool = False, path: bool = False, stream=None):
+                 probs: bool = False, stats: bool = False, path: bool = False, stream=None,
+                 post: Optional[LogitPost] = None, prev_tokens=None):
         torch = _torch()
         self.rows, self.vocab = rows, vocab
         self._c = cfg.to_c()
         self._stream = _stream_ptr(stream)
+        self._post = post.to_c() if post is not None else None
+        # the repetition history: a [rows, n_prev] int32 device tensor, fixed for every call
+        self._prev = prev_tokens
+        self._n_prev = int(prev_tokens.shape[1]) if prev_tokens is not None else 0
         self.result = SampleResult(torch.empty(rows, dtype=torch.int32, device=device),
                                    torch.empty(rows, dtype=torch.uint8, device=device))
         self._ex = None
@@ -362,15 +367,18 @@ class PreparedCall:
                 r.row_path = torch.empty(rows, dtype=torch.int32, device=device)
                 ex.d_row_path = r.row_path.data_ptr()
             self._ex = ex
-        need = int(_lib().llz_sample_workspace_bytes(rows, vocab, C.byref(self._c), 0))
+        need = int(_lib().llz_sample_workspace_bytes(rows, vocab, C.byref(self._c), self._n_prev))
         self.workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
 
     def __call__(self, logits, uniforms) -> SampleResult:
         if tuple(logits.shape) != (self.rows, self.vocab) or logits.stride(1) != 1:
             raise ValueError("logits must have the prepared shape with contiguous rows")
         r = self.result
+        prev = self._prev
         rc = _lib().llz_sample_rows(
-            logits.data_ptr(), logits.stride(0), self.rows, self.vocab, C.byref(self._c), None, None, 0, 0,
+            logits.data_ptr(), logits.stride(0), self.rows, self.vocab, C.byref(self._c),
+            C.byref(self._post) if self._post is not None else None,
+            prev.data_ptr() if prev is not None else None, self._n_prev, prev.stride(0) if prev is not None else 0,
             uniforms.data_ptr(), r.tokens.data_ptr(), r.consumed.data_ptr(),
             C.byref(self._ex) if self._ex is not None else None, self.workspace.data_ptr(), self.workspace.numel(),
             self._stream)
