@@ -54,7 +54,7 @@ constexpr uint32_t kPathError = 0x80000000u;
 // the kernel's phases, slot k of row r at llz_phase_stamps[r * kStampSlots +
 // k].  In ordinary builds LLZ_STAMP compiles to nothing.
 constexpr int kStampRows = 4096;
-constexpr int kStampSlots = 44;
+constexpr int kStampSlots = 60;
 #ifdef LLZ_PHASE_STAMPS
 static __device__ unsigned long long llz_phase_stamps[kStampRows * kStampSlots];  // read by llz_stats.hip's copy-out
 #define LLZ_STAMP(row, k)                                                                     \

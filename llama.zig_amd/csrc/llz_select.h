@@ -549,7 +549,7 @@ struct EntropyResult {
 
 template <class Src>
 __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float S, float T, uint32_t flags,
-                                                   SampleShared& sh, int bank) {
+                                                   SampleShared& sh, int bank, int row) {
   constexpr int EV = 2 * kLaneV;  // logits per thread per tile
   constexpr int ET = kNT * EV;
   constexpr int EP = kWave * EV;  // the prologue's terms (wave 0's share of the first tile)
@@ -590,9 +590,11 @@ __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float 
     }
     wg_bcast<kNT>(t == 0, H, unused, sh.wg, bank);
   }
+  LLZ_STAMP(row, 48);
 
   for (int base = 0; base < n; base += ET) {
     const int pos = base + t * EV;
+    if (base == 20 * ET) LLZ_STAMP(row, 53);
     if (base > 0) rt.fix_tail(pos, raw);
     float xa[EV];
 #pragma unroll
@@ -630,25 +632,36 @@ __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float 
       }
       return te[k];
     };
-    // the certified cases are selected without branches; one branch per
-    // element leads to the exact term
-    auto R = [&](int k, int j, bool& tie) -> uint32_t {
-      tie = false;
+    // the rounding on grid j from the estimate: true when the estimate's
+    // error bound fixes it (out), false when the exact term must decide
+    auto cheap = [&](int k, int j, uint32_t& out) -> bool {
       const float y = ldexpf(tl[k], 23 - j);
       const float d = y * EPS;
       const float r = rintf(y);
       const bool big = y - d >= 0x1p24f;
       const bool cert = y < 0x1p22f && fabsf(y - r) + d < 0.5f;
       const bool is_tiny = ((tiny >> k) & 1u) != 0u;
-      const bool ok = is_tiny ? j >= -60 : (((mid >> k) & 1u) != 0u && (big || cert));
-      uint32_t out = is_tiny ? 0u : (big ? kSat : (uint32_t)r);
-      if (!ok) out = grid_round(exact(k), j, tie);
+      out = is_tiny ? 0u : (big ? kSat : (uint32_t)r);
+      return is_tiny ? j >= -60 : (((mid >> k) & 1u) != 0u && (big || cert));
+    };
+    // the certified cases are selected without branches; one branch per
+    // element leads to the exact term
+    auto R = [&](int k, int j, bool& tie) -> uint32_t {
+      tie = false;
+      uint32_t out;
+      if (!cheap(k, j, out)) out = grid_round(exact(k), j, tie);
       return out;
     };
     auto E = [&](int k) { return exact(k); };
     auto present = [&](int k) { return pos + k < n; };
+    if (base == 20 * ET) LLZ_STAMP(row, 54);
     H = tile_accumulate_fn<kNT, EV>(H, R, E, present, sh.wg, bank, base == 0 ? EP - 1 : -1);
+    if (base == 0) LLZ_STAMP(row, 49);
+    if (base == ET) LLZ_STAMP(row, 50);
+    if (base == 16 * ET) LLZ_STAMP(row, 51);
+    if (base == 20 * ET) LLZ_STAMP(row, 55);
   }
+  LLZ_STAMP(row, 52);
   return EntropyResult{H, bank};
 }
 
@@ -1145,7 +1158,7 @@ __device__ __forceinline__ void select_row(const RowParams& P, const RowPtrs& Q,
     } else if (typical && K >= 2) {
       path |= kPathEntropy;
       {
-        const EntropyResult er = entropy_pass<Src>(X, n, m, S, P.temperature, P.flags, sh, bank);
+        const EntropyResult er = entropy_pass<Src>(X, n, m, S, P.temperature, P.flags, sh, bank, row);
         H = er.H;
         bank = er.bank;
       }
@@ -1737,7 +1750,7 @@ __device__ __noinline__ void select_full_row(const KArgs* A, int row, const PenS
   if (typical && K >= 2) {
     path |= kPathEntropy;
     {
-      const EntropyResult er = entropy_pass<Src>(X, n, m, S, P.temperature, P.flags, sh, bank);
+      const EntropyResult er = entropy_pass<Src>(X, n, m, S, P.temperature, P.flags, sh, bank, row);
       H = er.H;
       bank = er.bank;
     }

@@ -555,12 +555,12 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     O = PlainSrc{Q.orig + (int64_t)row * P.orig_stride};
   }
   uint64_t pen_wm = 0;  // segments of this wave holding a penalised position
+  // the penalty window's ids, loaded now by every wave (lane j: id j): the
+  // penalty is applied after the load loop, which does not need it, so the
+  // load lands meanwhile
+  uint32_t pen_id = 0xffffffffu;
   if constexpr (XF) {
-    if (P.xf_src & kXfPen) {
-      pen_build(pen_sh, P, Q, row);
-      lds_barrier();
-      pen_wm = uni_u64(pen_sh.wmask[w]);
-    }
+    if (P.xf_src & kXfPen) pen_id = pen_window_id(P, Q, row);
   }
   // Phase L's per-element work is the plain rows' plus, at most, one
   // multiply (kXmLight: the logit scale; 1 without one, v * 1 == v) or the
@@ -734,14 +734,34 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   // estimate); each touched segment's sum of estimates is folded again as
   // phase L folds it.  LDS-resident segments take the estimate from the lane
   // that holds the position, register segments from the lane that owns it.
+  LLZ_STAMP(row, 46);
   uint32_t pen_p = 0xffffffffu;  // this lane's penalised position (of this wave's segments)
   float pen_r = 0.0f;            // its logit as the caller wrote it
+  uint64_t pen_lanes = 0ull;     // the lanes holding one
+  bool pen_first = false;        // lane j: id j is the window's first occurrence of an id < n
   if constexpr (XF) {
+    if (P.xf_src & kXfPen) {
+      // Each wave takes the window's distinct ids < n (sampler.zig:62-70
+      // penalises an id once) in its own segments from its registers: no
+      // barrier waits for the other waves here.
+      bool first = pen_id < (uint32_t)n;
+      for (int j = 0; j < P.pen_w; ++j) {
+        const uint32_t o = readlane_u32(pen_id, j);
+        first = first && !(j < lane && o == pen_id);
+      }
+      pen_first = first;
+      const bool mine = first && ((pen_id >> 8) & (uint32_t)(W - 1)) == (uint32_t)w;
+      pen_p = mine ? pen_id : 0xffffffffu;
+      pen_r = mine ? xr[pen_id] : 0.0f;
+      pen_lanes = bal64(mine);
+      for (uint64_t bm = pen_lanes; bm != 0ull; bm &= bm - 1ull) {
+        const uint32_t k = readlane_u32(pen_id, __ffsll((long long)bm) - 1) >> 11;  // segment pos >> 8 = w + W k
+        if (k < 64u) pen_wm |= 1ull << k;
+      }
+    }
     if (fits && pen_wm != 0ull) {
-      const uint32_t pp = lane < pen_sh.n ? pen_sh.pos[lane] : 0xffffffffu;
-      const bool mine = pp != 0xffffffffu && ((pp >> 8) & (uint32_t)(W - 1)) == (uint32_t)w;
-      pen_p = mine ? pp : 0xffffffffu;
-      pen_r = mine ? xr[pp] : 0.0f;
+      const uint32_t pp = pen_p;
+      const bool mine = pp != 0xffffffffu;
       const float src = XM == kXmCap ? pen_est(est_of(pen_r), P.rpen, P.rpen_inv) : penalise(pen_r * xscale, P.rpen);
       const float qn = __builtin_amdgcn_exp2f(fmaf(src, l2e_t, -cw));
       const int kk = (int)(pp >> 11);  // the wave's segment index k of segment pp >> 8 = w + W k
@@ -770,6 +790,33 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         const int k = KV + __ffsll((long long)rest) - 1;
         seg_sum(k, *reinterpret_cast<const float4*>(&F.u.data[w][k - KV][lane * 4]));
       }
+      LLZ_STAMP(row, 44);
+    }
+  }
+  // a position of this wave's segments through the row's transforms,
+  // exactly, the penalty from the wave's own list (the shared one is built
+  // below, read after the next barrier)
+  auto fix_here = [&](int pos, float v) -> float {
+    if constexpr (!XF) {
+      return v;
+    } else {
+      v = X.pre(v);
+      bool hit = false;
+      if ((pen_wm >> (((uint32_t)pos >> 11) & 63u)) & 1ull) {  // a segment holding one (most hold none)
+        for (uint64_t bm = pen_lanes; bm != 0ull; bm &= bm - 1ull)
+          hit = hit || (uint32_t)pos == readlane_u32(pen_p, __ffsll((long long)bm) - 1);
+      }
+      return hit ? penalise(v, P.rpen) : v;
+    }
+  };
+  if constexpr (XF) {
+    // the row's sorted list of penalised positions and the waves' segment
+    // masks in LDS (wave 0), for the phases after the next barrier; the rows
+    // the single pass does not take read it in their scan right below
+    if (P.xf_src & kXfPen) {
+      pen_list(pen_sh, pen_id, pen_first);
+      LLZ_STAMP(row, 43);
+      if (!fits) lds_barrier();
     }
   }
   if (lane < nseg_w) F.v.aseg[w + W * lane] = my_a;
@@ -832,7 +879,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
           const int pos = (w + W * k) * SEG + lane4;
 #pragma unroll 1
           for (int c = 0; c < 4; ++c)
-            if (pos + c < n) ex = fmaxf(ex, X.at(pos + c));
+            if (pos + c < n) ex = fmaxf(ex, fix_here(pos + c, xr[pos + c]));
         }
         return wave_max_f32(ex);
       };
@@ -848,6 +895,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         const bool top = bal64(mine && pen_r * xscale == mx) != 0ull;
         mx = top ? scan_max() : fmaxf(mx, wave_max_f32(mine ? penalise(X.pre(pen_r), P.rpen) : -kInfS));
       }
+      LLZ_STAMP(row, 45);
     }
   }
   // token-only rows: the lanes that may hold a candidate (a term that may
@@ -894,8 +942,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       for (int h = 0; h < QCAP / kWave; ++h) {
         const int i = h * kWave + lane;
         const int pos = i < nq ? (int)F.qpos[w][i] : 0;
-        const float4 r = FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n);
-        tv[h] = XM == kXmCap ? r : X.fix4(pos, r, n);  // kXmCap: raw (transformed where they are used)
+        tv[h] = FASTLD ? ld4(xr, pos, n) : ld1x4(xr, pos, n);  // raw: transformed where they are read
       }
     } else {
 #pragma unroll
@@ -998,6 +1045,15 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         const int i = h * kWave + lane;
         const bool live = tq <= QCAP && i < tq;
         tpos[h] = live ? (int)F.qpos[w][i] : 0;
+        // the re-reads as the chain reads them (kXmLight: exactly; kXmCap
+        // keeps them raw: its test below takes estimates, and the exact
+        // values are taken for the candidates alone)
+        if constexpr (XM == kXmLight) {
+          tv[h].x = fix_here(tpos[h] + 0, tv[h].x);
+          tv[h].y = fix_here(tpos[h] + 1, tv[h].y);
+          tv[h].z = fix_here(tpos[h] + 2, tv[h].z);
+          tv[h].w = fix_here(tpos[h] + 3, tv[h].w);
+        }
         const float vs[4] = {tv[h].x, tv[h].y, tv[h].z, tv[h].w};
         uint32_t mk = 0u;
 #pragma unroll
@@ -1008,7 +1064,12 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
           float vq = vs[c];
           if constexpr (XM == kXmCap) {
             vq = est_of(vq);
-            if ((P.xf_src & kXfPen) && live && X.penalised(tpos[h] + c)) vq = pen_est(vq, P.rpen, P.rpen_inv);
+            bool hit = false;  // a penalised position of this wave's
+            if ((pen_wm >> (((uint32_t)(tpos[h] + c) >> 11) & 63u)) & 1ull) {
+              for (uint64_t bm = pen_lanes; bm != 0ull; bm &= bm - 1ull)
+                hit = hit || (uint32_t)(tpos[h] + c) == readlane_u32(pen_p, __ffsll((long long)bm) - 1);
+            }
+            if (hit) vq = pen_est(vq, P.rpen, P.rpen_inv);
           }
           const bool pass = live && tpos[h] + c < n && __builtin_amdgcn_exp2f(fmaf(vq, l2e_t, -cw)) >= thr_q;
           mk |= pass ? (1u << c) : 0u;
@@ -1040,7 +1101,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         if (lane < ttot) {
           id = sg[2 * lane + 1];
           float v = __uint_as_float(sg[2 * lane]);
-          if constexpr (XM == kXmCap) v = X.fix((int)id, v);  // the exact value of a raw re-read
+          if constexpr (XM == kXmCap) v = fix_here((int)id, v);  // the exact value of a raw re-read
           e = exact_term(v, m, P.temperature, t1);  // sampler.zig:85
         }
         const bool cand = lane < ttot && e >= theta_t;
@@ -1057,7 +1118,14 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         for (int h = 0; h < NH; ++h) {
           if (tmk[h] != 0u) {
             const int pos = tpos[h];
-            const float4 e = exact_terms4(XM == kXmCap ? X.fix4(pos, tv[h], n) : tv[h], m, P.temperature, t1);  // sampler.zig:85
+            float4 v4 = tv[h];
+            if constexpr (XM == kXmCap) {
+              v4.x = pos + 0 < n ? fix_here(pos + 0, v4.x) : v4.x;
+              v4.y = pos + 1 < n ? fix_here(pos + 1, v4.y) : v4.y;
+              v4.z = pos + 2 < n ? fix_here(pos + 2, v4.z) : v4.z;
+              v4.w = pos + 3 < n ? fix_here(pos + 3, v4.w) : v4.w;
+            }
+            const float4 e = exact_terms4(v4, m, P.temperature, t1);  // sampler.zig:85
             const float es[4] = {e.x, e.y, e.z, e.w};
 #pragma unroll
             for (int c = 0; c < 4; ++c) {

@@ -77,38 +77,35 @@ struct PenShared {
   int n;
 };
 
-// Wave 0 collects the row's penalised positions (the window is read from the
-// history row; ids >= n never match, sampler.zig:64).  The caller
-// synchronises the workgroup before any read uses them.
-__device__ __forceinline__ void pen_build(PenShared& ps, const RowParams& P, const RowPtrs& Q, int row) {
+// The row's penalty window as lane j's id j (0xffffffff past the window):
+// one load, issued early by the caller so that it lands while other work
+// goes on.
+__device__ __forceinline__ uint32_t pen_window_id(const RowParams& P, const RowPtrs& Q, int row) {
+  const int lane = lane_id();
+  const uint32_t* win = Q.prev_win + (int64_t)row * P.prev_stride;
+  return lane < P.pen_w ? win[lane] : 0xffffffffu;
+}
+
+// Wave 0 writes the row's penalised positions to LDS, ascending, with the
+// waves' segment masks: lane j holds the window's id j and whether it is the
+// first occurrence of an id < n (sampler.zig:62-70 penalises each id once;
+// ids >= n never match, :64).  The caller synchronises the workgroup before
+// any read uses them.
+__device__ __forceinline__ void pen_list(PenShared& ps, uint32_t id, bool first) {
   if (wave_id() != 0) return;
   const int lane = lane_id();
-  const int w = P.pen_w;  // <= kPenMax, the window's length
-  const uint32_t* win = Q.prev_win + (int64_t)row * P.prev_stride;
-  const uint32_t id = lane < w ? win[lane] : 0xffffffffu;
-  // keep the first occurrence of each id < n
-  bool keep = lane < w && id < (uint32_t)P.n;
-  for (int j = 0; j < w; ++j) {
-    const uint32_t o = readlane_u32(id, j);
-    keep = keep && !(j < lane && o == id);
-  }
-  // rank among the kept ids (distinct), then scatter in ascending order
-  const uint64_t km = bal64(keep);
+  const uint64_t km = bal64(first);
   uint32_t rank = 0;
-  for (int j = 0; j < w; ++j) {
-    const uint32_t o = readlane_u32(id, j);
-    rank += (((km >> j) & 1ull) != 0ull && o < id) ? 1u : 0u;
+  uint64_t wm = 0;
+  for (uint64_t bm = km; bm != 0ull; bm &= bm - 1ull) {
+    const uint32_t o = readlane_u32(id, __ffsll((long long)bm) - 1);
+    rank += o < id ? 1u : 0u;
+    const uint32_t g = o >> 8;  // its segment
+    if ((int)(g & 7u) == lane && (g >> 3) < 64u) wm |= 1ull << (g >> 3);
   }
-  if (keep) ps.pos[rank] = id;
+  if (first) ps.pos[rank] = id;
   if (lane == 0) ps.n = __popcll(km);
-  if (lane < 8) {
-    uint64_t wm = 0;
-    for (int j = 0; j < w; ++j) {
-      const uint32_t g = readlane_u32(id, j) >> 8;  // its segment
-      if (((km >> j) & 1ull) != 0ull && (int)(g & 7u) == lane && (g >> 3) < 64u) wm |= 1ull << (g >> 3);
-    }
-    ps.wmask[lane] = wm;
-  }
+  if (lane < 8) ps.wmask[lane] = wm;
 }
 
 // A row of logits as the chain reads it (see the file comment).  CAP =
@@ -131,6 +128,9 @@ struct RowSrcT {
   }
 
   __device__ __forceinline__ bool penalised(int i) const {
+    // the segment's bit first (one LDS read; most segments hold none)
+    const uint32_t g = (uint32_t)i >> 8;
+    if ((g >> 3) < 64u && ((pen->wmask[g & 7u] >> (g >> 3)) & 1ull) == 0ull) return false;
     const int np = pen->n;
     // lower bound of i in the sorted list
     int lo = 0, hi = np;

@@ -36,6 +36,10 @@ SLOTS = {
     38: "token-only: row maximum read", 39: "token-only: candidate segments scanned",
     35: "token-only: prefix and min-p counted", 36: "token-only: top-p and order checked", 37: "token-only: drawn",
     40: "recollect: histogram", 41: "recollect: cut", 42: "recollect: collected",
+    43: "penalty: shared list built (wave 0)", 44: "penalty: elements patched", 45: "transforms: maximum settled",
+    46: "L: load loop done (wave 0)",
+    48: "entropy: first 512 terms", 49: "entropy: tile 0", 50: "entropy: tile 1", 51: "entropy: tile 16",
+    52: "entropy: last tile",
 }
 # phases as (name, from slot, to slot)
 PHASES = [
@@ -58,6 +62,13 @@ PHASES = [
     ("decisions: draw", 36, 37), ("decisions: outputs + barrier", 37, 15),
     ("recollect: histogram pass", 6, 40), ("recollect: cut", 40, 41), ("recollect: collect pass", 41, 42),
     ("after recollect: sort, filters, draw", 42, 15),
+    ("penalty: list -> L end", 43, 1), ("penalty: patch (after loads)", 0, 44), ("penalty: loop end -> patched", 46, 44),
+    ("penalty: patched -> list built", 44, 43),
+    ("transforms: maximum (from start)", 0, 45), ("transforms: patch -> maximum", 44, 45),
+    ("L: load loop (w0)", 0, 46), ("L: loop end -> L end", 46, 1), ("transforms: maximum -> L end", 45, 1),
+    ("entropy: before it", 6, 48), ("entropy: first 512 terms -> tile 0", 48, 49), ("entropy: tile 1", 49, 50),
+    ("entropy: tiles 2..16", 50, 51), ("entropy: tiles 17..", 51, 52), ("entropy: after it", 52, 12),
+    ("entropy tile 20: loads + arguments", 53, 54), ("entropy tile 20: accumulate", 54, 55), ("entropy tile 16 end -> 20 start", 51, 53),
 ]
 
 
@@ -69,6 +80,9 @@ def main() -> int:
     ap.add_argument("--exact", action="store_true", help="ask for row statistics (the exact phases on every row)")
     ap.add_argument("--chain-params", default="", help="override the workload's chain, e.g. T=0.8,top_p=0.9,min_p=0,top_k=0")
     ap.add_argument("--dump", default="", help="also save every row's raw timestamps (.npy)")
+    ap.add_argument("--post", default="", help="soft-cap and logit scale, e.g. 30,0.5 (main.zig:653-666)")
+    ap.add_argument("--penalty", default="", help="repetition window and penalty over as many random history "
+                                                  "tokens per row, e.g. 32,1.1 (sampler.zig:54-75)")
     ap.add_argument("--chain", type=int, default=1,
                     help="launches back to back before reading (the last one's stamps, as in a benchmark loop)")
     a = ap.parse_args()
@@ -86,7 +100,7 @@ def main() -> int:
     L.llz_debug_phase_stamps.argtypes = [C.c_void_p, C.c_int, C.c_int]
     L.llz_debug_phase_stamps.restype = C.c_int
     rows_st = min(rows, 4096)
-    buf = np.zeros((rows_st, 44), np.uint64)
+    buf = np.zeros((rows_st, 60), np.uint64)
     x = torch.from_numpy(w.logits(rows)).cuda()
     u = torch.from_numpy(llz.rng_uniforms(w.uniform_seed, rows)).cuda()
     params = w.params
@@ -96,13 +110,24 @@ def main() -> int:
         names = {"T": "temperature", "top_p": "top_p", "min_p": "min_p", "top_k": "top_k", "typical_p": "typical_p"}
         kv = dict(item.split("=") for item in a.chain_params.split(","))
         params = dataclasses.replace(params, **{names[k]: (int(v) if k == "top_k" else float(v)) for k, v in kv.items()})
+    post = prev = None
+    if a.post:
+        cap, scale = (float(v) for v in a.post.split(","))
+        post = llz.LogitPost(final_logit_softcapping=cap, logit_scale=scale)
+    if a.penalty:
+        import dataclasses
+
+        win, rp = a.penalty.split(",")
+        params = dataclasses.replace(params, repetition_window=int(win), repetition_penalty=float(rp))
+        prev = torch.from_numpy(np.random.default_rng(41).integers(0, w.vocab, size=(rows, int(win)))
+                                .astype(np.int32)).cuda()
     cfg = llz.SamplerConfig.of(params)
     res = None
     for _ in range(a.reps):
         assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 1) == 0
         torch.cuda.synchronize()
         for _ in range(a.chain):
-            res = llz.sample_rows(x, cfg, u, path=True, stats=a.exact)
+            res = llz.sample_rows(x, cfg, u, prev, post=post, path=True, stats=a.exact)
         torch.cuda.synchronize()
     assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 0) == 0
     if a.dump:
