@@ -738,7 +738,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   uint32_t pen_p = 0xffffffffu;  // this lane's penalised position (of this wave's segments)
   float pen_r = 0.0f;            // its logit as the caller wrote it
   uint64_t pen_lanes = 0ull;     // the lanes holding one
-  bool pen_first = false;        // lane j: id j is the window's first occurrence of an id < n
+  uint32_t pen_idf = 0xffffffffu;  // lane j: id j, bit 31 set unless its first occurrence of an id < n
   if constexpr (XF) {
     if (P.xf_src & kXfPen) {
       // Each wave takes the window's distinct ids < n (sampler.zig:62-70
@@ -749,7 +749,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         const uint32_t o = readlane_u32(pen_id, j);
         first = first && !(j < lane && o == pen_id);
       }
-      pen_first = first;
+      pen_idf = first ? pen_id : (pen_id | 0x80000000u);
       const bool mine = first && ((pen_id >> 8) & (uint32_t)(W - 1)) == (uint32_t)w;
       pen_p = mine ? pen_id : 0xffffffffu;
       pen_r = mine ? xr[pen_id] : 0.0f;
@@ -811,12 +811,12 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   };
   if constexpr (XF) {
     // the row's sorted list of penalised positions and the waves' segment
-    // masks in LDS (wave 0), for the phases after the next barrier; the rows
-    // the single pass does not take read it in their scan right below
-    if (P.xf_src & kXfPen) {
-      pen_list(pen_sh, pen_id, pen_first);
-      LLZ_STAMP(row, 43);
-      if (!fits) lds_barrier();
+    // masks in LDS (wave 0): the rows the single pass does not take read it
+    // in their scan right below; the others only if they go on to the exact
+    // phases (built there: a row the token path finishes never needs it)
+    if ((P.xf_src & kXfPen) && !fits) {
+      pen_list(pen_sh, pen_idf);
+      lds_barrier();
     }
   }
   if (lane < nseg_w) F.v.aseg[w + W * lane] = my_a;
@@ -1159,6 +1159,13 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       // overwrote written again (F.qpos is rewritten in phase S)
       if (lane < nseg_w) F.v.aseg[w + W * lane] = my_a;
       __syncthreads();
+    }
+  }
+  if constexpr (XF) {
+    if ((P.xf_src & kXfPen) && fits) {  // the exact phases read the list (see above)
+      pen_list(pen_sh, pen_idf);
+      LLZ_STAMP(row, 43);
+      lds_barrier();
     }
   }
   // the segment sums of q of round `lane` (segments W lane .. W lane + W - 1,

@@ -87,13 +87,15 @@ __device__ __forceinline__ uint32_t pen_window_id(const RowParams& P, const RowP
 }
 
 // Wave 0 writes the row's penalised positions to LDS, ascending, with the
-// waves' segment masks: lane j holds the window's id j and whether it is the
-// first occurrence of an id < n (sampler.zig:62-70 penalises each id once;
-// ids >= n never match, :64).  The caller synchronises the workgroup before
-// any read uses them.
-__device__ __forceinline__ void pen_list(PenShared& ps, uint32_t id, bool first) {
+// waves' segment masks: lane j holds the window's id j, with bit 31 set
+// unless it is the first occurrence of an id < n (sampler.zig:62-70
+// penalises each id once; ids >= n never match, :64).  The caller
+// synchronises the workgroup before any read uses them.
+__device__ __forceinline__ void pen_list(PenShared& ps, uint32_t idf) {
   if (wave_id() != 0) return;
   const int lane = lane_id();
+  const bool first = (idf >> 31) == 0u;
+  const uint32_t id = idf & 0x7fffffffu;
   const uint64_t km = bal64(first);
   uint32_t rank = 0;
   uint64_t wm = 0;
