@@ -232,9 +232,9 @@ int llz_debug_math(const float *d_in, float *d_exp, float *d_log, float *d_expm1
                    int64_t n, void *stream);
 
 /* Test hook (no counterpart in the reference): the largest relative error,
- * in units of 2^-23, of the hardware exp2 (op 0) or log2 (op 1) that the
- * kernels' estimates use, over the `count` floats whose bit patterns start at
- * `first_bits`, against double-precision exp2 / log2.  Writes
+ * in units of 2^-23, of the hardware exp2 (op 0), log2 (op 1) or reciprocal
+ * (op 2) that the kernels' estimates use, over the `count` floats whose bit
+ * patterns start at `first_bits`, against double precision.  Writes
  * round-toward-zero(error * 2^20), saturated at 0xffffffff, to *d_max_err
  * (device memory, one u32, overwritten).  The estimates' error bounds assume
  * at most 1 unit (1 ulp) on the ranges the kernels evaluate. */

@@ -446,7 +446,7 @@ int llz_debug_math(const float* d_in, float* d_exp, float* d_log, float* d_expm1
 }
 
 int llz_debug_hw_error(int32_t op, uint32_t first_bits, uint32_t count, uint32_t* d_max_err, void* stream) {
-  if (!d_max_err || (op != 0 && op != 1) || count == 0) return LLZ_E_INVALID_ARG;
+  if (!d_max_err || op < 0 || op > 2 || count == 0) return LLZ_E_INVALID_ARG;
   hipError_t e = launch_hw_error(op, first_bits, count, d_max_err, (hipStream_t)stream);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }

@@ -117,12 +117,14 @@ def test_device_log_matches_oracle(cuda, name, lo, hi, step):
     ("exp2-negative", 0, 0x80000000, 0xc2fc0000),   # -0 .. -126 (every input with a normal result)
     ("exp2-positive", 0, 0x00000000, 0x42800000),   # 0 .. 64
     ("log2-entropy", 1, 0x08800000, 0x3e800000),    # 2^-110 .. 2^-2
+    ("rcp-softcap", 2, 0x3f800000, 0x71800000),     # 1 .. 2^100 (exp2 + 1 in the soft-cap estimate)
 ])
 def test_hardware_exp2_log2_within_one_ulp(cuda, name, op, lo, hi):
     """The certified estimates (the single-pass statistics, the streaming
-    normaliser, the entropy pass) take the hardware exp2 and log2 to be within
-    1 ulp of the exact result (relative error <= 2^-23); checked on every
-    float of the ranges they evaluate, against double precision."""
+    normaliser, the entropy pass, the soft-cap estimate) take the hardware
+    exp2, log2 and reciprocal to be within 1 ulp of the exact result (relative
+    error <= 2^-23); checked on every float of the ranges they evaluate,
+    against double precision."""
     err = llz.debug_hw_error(op, lo, hi - lo + 1)
     assert err <= 1.0, f"{name}: {err} units of 2^-23"
 
