@@ -110,6 +110,8 @@ enum {
     LLZ_PATH_DECLINE_SHIFT = 8,  /* bits 8-15: the bucket path's decline reason (see above)  */
     LLZ_PATH_RECOLLECT = 1 << 16, /* a flooded candidate list collected again, its largest  */
                                  /*   terms only, so the selection ran on a list            */
+    LLZ_PATH_SPLIT = 1 << 17,    /* with LLZ_PATH_TOKEN_ONLY: the row was read by several   */
+                                 /*   workgroups, one chunk each (calls of few rows)       */
     LLZ_PATH_ERROR = (int)0x80000000u
 };
 
@@ -254,6 +256,14 @@ int llz_debug_kernel_events(void *begin_event, void *end_event);
  * in the workspace on ordinary rows; 0 restores the kernel's own.  Results
  * do not depend on it.  Process-wide. */
 int llz_debug_set_queue_cap(uint32_t cap);
+
+/* Test hook (no counterpart in the reference): split rows for the following
+ * llz_sample_rows calls (token-only calls of at most 64 plain rows read each
+ * row with several workgroups, one chunk of 2048 nv logits each).  mode 0:
+ * the library's choice (the smallest nv <= 8 whose workgroups fit the CUs
+ * at once); 1: off; 2, 4 or 8: nv at least that.  Results do not depend on
+ * it.  Process-wide.  LLZ_E_INVALID_ARG for any other mode. */
+int llz_debug_set_split(int32_t mode);
 
 /* Name of a return code. */
 const char *llz_strerror(int code);

@@ -24,6 +24,8 @@ hipEvent_t g_ev_begin = nullptr;
 hipEvent_t g_ev_end = nullptr;
 // test hook: a smaller special-queue chunk (see llz_debug_set_queue_cap)
 std::atomic<uint32_t> g_queue_cap{0u};
+// test hook: split rows off, or their smallest chunk width (see llz_debug_set_split)
+std::atomic<int> g_split_mode{0};
 
 bool penalty_active(const llz_sampler_config* cfg, int32_t n_prev) {
   return cfg->repetition_penalty != 1.0f && n_prev > 0 && cfg->repetition_window > 0;
@@ -55,7 +57,7 @@ uint32_t post_bits(const llz_logit_post* post) {
 // fallback buffer sets (25 B per logit each, fb_slots_for) with their owner
 // words; the penalised copy only for windows too long to fuse.
 struct Layout {
-  size_t status, claim, cand, qovf, owner, fb, fb_mask, penal, total;
+  size_t status, claim, cand, qovf, owner, fb, fb_mask, penal, split, total;
   int fb_slots;
   bool has_penal;
 };
@@ -91,6 +93,9 @@ Layout layout_of(int32_t rows, int32_t vocab, const llz_sampler_config* cfg, int
   L.fb_mask = off; off = align_up(off + ns * n);
   L.has_penal = penalty_copy(cfg, n_prev);
   L.penal = off;   if (L.has_penal) off = align_up(off + r * n * sizeof(float));
+  // last, so that a workspace without it holds every other part at the same
+  // offsets: calls of at most kSplitRows rows, the split rows' chunk records
+  L.split = off;   if (rows <= kSplitRows) off = align_up(off + r * sizeof(SplitRow));
   L.total = off;
   return L;
 }
@@ -232,7 +237,9 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
     return LLZ_E_INVALID_ARG;
 
   const Layout L = layout_of(rows, vocab, cfg, n_prev, max_slots);
-  if (!d_workspace || workspace_bytes < L.total) return too_small_code;
+  // a workspace that ends before the split rows' records holds the rest
+  if (!d_workspace || workspace_bytes < L.split) return too_small_code;
+  const bool split_room = rows <= kSplitRows && workspace_bytes >= L.total;
   char* ws = (char*)d_workspace;
 
   const float* src = d_logits;
@@ -322,6 +329,31 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
     if (cus <= 0) return LLZ_E_HIP;
     P.grid = std::min(std::min(rows, cus), kMaxGrid);
   }
+  // Split rows: a token-only call of at most kSplitRows plain, 16-byte
+  // aligned rows reads each row with S workgroups of one chunk each (the
+  // smallest chunk, 2048 nv logits, whose rows x S workgroups fit the CUs at
+  // once), where one workgroup per row would leave most CUs idle.
+  if (split_room && tok_only && (xf_src | xb) == 0u && vec && vocab % 4 == 0 && P.tok_theta > 0.0f &&
+      P.l2e_t > 0.0f && P.l2e_t <= 0x1p40f && g_split_mode.load(std::memory_order_relaxed) != 1) {
+    const int cus = device_cus(st);
+    for (int nv = std::max(1, g_split_mode.load(std::memory_order_relaxed)); nv <= kSplitNV && cus > 0; nv *= 2) {
+      const int s = (vocab + 2048 * nv - 1) / (2048 * nv);
+      if (s <= kSplitMax && rows * s <= cus) {
+        if (s >= 2) {
+          P.split_s = s;
+          P.split_nv = nv;
+        }
+        break;
+      }
+    }
+    // a chunk's possible candidates: d2 = (m_c - v) l2e_t < log2(1 / theta)
+    // + 2^-8 (rounded up to a float)
+    const double b = std::log2(1.0 / (double)P.tok_theta) + 0x1p-8;
+    float bf = (float)b;
+    if ((double)bf < b) bf = std::nextafter(bf, INFINITY);
+    P.split_b = bf;
+    P.split_bs = 256.0f / bf;
+  }
   P.epoch = g_epoch.fetch_add(1, std::memory_order_relaxed) & ((1ull << 62) - 1);
   // the test hook's special-queue chunk (0: the kernel's own)
   P.qcap = g_queue_cap.load(std::memory_order_relaxed);
@@ -346,6 +378,7 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   Q.qovf = (uint32_t*)(ws + L.qovf);
   Q.claim = (unsigned long long*)(ws + L.claim);
   Q.prev_win = (xf_src & kXfPen) ? d_prev_tokens + (n_prev - window) : nullptr;
+  Q.split = P.split_s > 0 ? (SplitRow*)(ws + L.split) : nullptr;
   e = launch_sample(P, Q, g_ev_begin, g_ev_end, st);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }
@@ -356,8 +389,9 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
 // per-device address hipGetSymbolAddress returns for it, never the name.
 // Nothing in it needs clearing between calls: the status words, candidate
 // lists and queue overflow are written before they are read within a call,
-// and a fallback slot is free for a call whenever its owner word holds
-// anything but that call's epoch.
+// a fallback slot is free for a call whenever its owner word holds anything
+// but that call's epoch, and a split row's chunk records count for a call
+// only once tagged with its epoch.
 // ---------------------------------------------------------------------------
 constexpr size_t kScratchBytes = (size_t)LLZ_NOALLOC_SCRATCH_BYTES;
 constexpr int kScratchSlots = 8;  // full-row fallback buffer sets in the scratch
@@ -428,6 +462,12 @@ int llz_sample_rows(const float* d_logits, int64_t row_stride, int32_t rows, int
 
 int llz_debug_set_queue_cap(uint32_t cap) {
   g_queue_cap.store(cap, std::memory_order_relaxed);
+  return LLZ_OK;
+}
+
+int llz_debug_set_split(int32_t mode) {
+  if (!(mode == 0 || mode == 1 || mode == 2 || mode == 4 || mode == 8)) return LLZ_E_INVALID_ARG;
+  g_split_mode.store(mode, std::memory_order_relaxed);
   return LLZ_OK;
 }
 

@@ -18,6 +18,14 @@ constexpr int kMaxGrid = 256;
 // the number of CUs, since k_stats's LDS holds one row-workgroup per CU, so
 // no more rows than this can be inside the fallback at once.
 constexpr int kFbSlots = 256;
+// Split rows (token-only calls of few rows): a row's logits are read by up to
+// kSplitMax workgroups at once, each taking one chunk of 2048 nv consecutive
+// logits (nv float4 per thread, nv <= kSplitNV) and handing at most kSplitK
+// of them to the workgroup that finishes the row.
+constexpr int kSplitMax = 64;
+constexpr int kSplitK = 64;
+constexpr int kSplitNV = 8;
+constexpr int kSplitRows = 64;
 
 // RowParams.flags
 constexpr uint32_t kFlagTIsOne = 1u;    // temperature == 1.0f exactly: (v - m) / T == v - m
@@ -47,6 +55,7 @@ constexpr uint32_t kPathResolveGeneric = 32u;  // diagnostic: an event beyond a 
 constexpr uint32_t kPathTokenOnly = 128u;     // the token certified without the exact normaliser
 constexpr uint32_t kPathBuckets = 64u;        // full row without a sort: kept prefix, total and draw by p-key buckets
 constexpr uint32_t kPathRecollect = 1u << 16;  // a flooded candidate list collected again (its largest terms)
+constexpr uint32_t kPathSplit = 1u << 17;      // token-only row finished from chunks read by several workgroups
 constexpr uint32_t kPathError = 0x80000000u;
 
 // Phase timestamps (measurement builds only, -DLLZ_PHASE_STAMPS): thread 0
@@ -98,6 +107,26 @@ struct RowParams {
   int32_t fb_slots;  // full-row fallback buffers in the workspace
   int32_t grid;      // k_stats workgroups: rows [0, grid) one each, the rest claimed (Q.claim)
   uint64_t epoch;    // this call's tag: a fallback slot whose owner word holds it is in use
+  int32_t split_s;   // split rows: chunks per row (0: rows are not split)
+  int32_t split_nv;  // split rows: float4 per thread per chunk (chunk = 2048 split_nv logits)
+  float split_b;     // split rows: a chunk's elements with (m_c - v) l2e_t < split_b may be candidates
+  float split_bs;    // split rows: 256 / split_b (histogram bins per unit of log2)
+};
+
+// Split rows: one chunk's summary and the row's record in the workspace
+// (words written and read only through device-coherent atomic accesses).
+struct SplitRec {
+  unsigned long long tag;  // the call's epoch once the words below are final
+  unsigned long long mc;   // bits of the chunk's maximum m (NaNs skipped) | bits of c = RN(m l2e_t) << 32
+  unsigned long long sv;   // bits of s = sum of exp2(fma(v, l2e_t, -c)) | bits of vt << 32, the largest
+                           // logit of the chunk's possible candidates left out of its list (-inf: none)
+  unsigned long long nf;   // entries of its list | flags << 32 (1: a NaN or a maximum beyond 3e38)
+};
+struct SplitRow {
+  SplitRec rec[kSplitMax];
+  unsigned long long elect;  // the call's epoch once a workgroup has taken the row's merge
+  unsigned long long pad[7];
+  unsigned long long cand[kSplitMax * kSplitK];  // chunk k's list at [k kSplitK, k kSplitK + ncoll): logit bits | position << 32
 };
 
 struct RowPtrs {
@@ -118,6 +147,7 @@ struct RowPtrs {
   uint32_t* qovf;         // [min(rows, kMaxGrid)][kQovfRow] k_stats special-queue overflow, per workgroup
   unsigned long long* claim;  // rows claimed beyond the grid: (epoch tag << 24) | count
   const uint32_t* prev_win;  // kXfPen: row 0's window (its last pen_w history tokens)
+  SplitRow* split;           // [rows] split rows' chunk summaries and lists
 };
 
 // k_stats's one kernel argument.

@@ -14,6 +14,7 @@
 #include "llz_math.h"
 #include "llz_norm.h"
 #include "llz_select.h"
+#include "llz_split.h"
 #include "llz_token.h"
 #include "llz_wg.h"
 
@@ -527,8 +528,9 @@ __device__ __noinline__ int claim_row(unsigned long long* word, unsigned long lo
 // segment through buffer loads); otherwise element loads.  XF: the rows are
 // read through post-processing and/or the fused repetition penalty
 // (llz_xform.h); otherwise as they are.
+// wslot: the workgroup's block of the special-queue overflow area.
 template <bool FASTLD, int XM>
-__device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& U, PenShared& pen_sh) {
+__device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& U, PenShared& pen_sh, int wslot) {
   constexpr bool XF = XM != kXmNone;
   const RowParams P = A.P;
   const RowPtrs Q = A.Q;
@@ -1316,7 +1318,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     // settles.  qch: current chunk,
     // qn: its entries, lane c of ccnt: the entries of an earlier chunk c.
     // (one block per workgroup: a workgroup samples one row at a time)
-    uint32_t* const ovp = Q.qovf + (int64_t)blockIdx.x * kQovfRow + (int64_t)w * kQovfWave;
+    uint32_t* const ovp = Q.qovf + (int64_t)wslot * kQovfRow + (int64_t)w * kQovfWave;
     const int qcap = (P.qcap > 0u && P.qcap < (uint32_t)QCAP) ? (int)P.qcap : QCAP;  // entries per chunk
     int qch = 0;
     uint32_t ccnt = 0;
@@ -1744,7 +1746,7 @@ template <bool FASTLD, int XM>
 __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
   __shared__ StatsShared U;
   __shared__ PenShared pen_sh;  // kXfPen: the row's penalised positions
-  stats_row<FASTLD, XM>(A, (int)blockIdx.x, U, pen_sh);
+  stats_row<FASTLD, XM>(A, (int)blockIdx.x, U, pen_sh, (int)blockIdx.x);
 }
 
 // More rows than CUs: one workgroup per CU (all resident), each taking rows
@@ -1764,12 +1766,34 @@ __global__ __launch_bounds__(NT) void k_stats_rows(KArgs A) {
     const __attribute__((address_space(4))) KArgs* Ap =
         (const __attribute__((address_space(4))) KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(Ap));
-    stats_row<FASTLD, XM>(*(const KArgs*)Ap, row, U, pen_sh);
+    stats_row<FASTLD, XM>(*(const KArgs*)Ap, row, U, pen_sh, (int)blockIdx.x);
     if (threadIdx.x == 0) next_row = claim_row(A.Q.claim, A.P.epoch, A.P.grid);
     __syncthreads();  // also: every wave is done with this row's shared memory
     row = next_row;
     if (row >= A.P.rows) return;
   }
+}
+
+// Split rows (token-only calls of few rows, plain 16-byte aligned rows):
+// workgroup b reads chunk b % split_s of row b / split_s (NV float4 per
+// thread); a workgroup that sees the row's chunks published merges it, and
+// the one that takes an uncertified row finishes it with the single-row
+// path of k_stats (its overflow block: the row's, rows <= kSplitRows <
+// kMaxGrid).
+union SplitLds {
+  SplitShared split;
+  StatsShared stats;
+};
+template <int NV>
+__global__ __launch_bounds__(NT) void k_split(KArgs A) {
+  __shared__ SplitLds U;
+  __shared__ PenShared pen_sh;  // unused by plain rows
+  const int ns = A.P.split_s;
+  const int row = (int)blockIdx.x / ns, c = (int)blockIdx.x - row * ns;
+  if (!split_chunk<NV>(A, row, c, U.split)) return;
+  if (split_merge(A, row, U.split) != 0) return;
+  __syncthreads();  // every wave is done with the merge's shared memory
+  stats_row<true, kXmNone>(A, row, U.stats, pen_sh, row);
 }
 
 }  // namespace
@@ -1786,9 +1810,18 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
   // more rows than workgroups: the grid's workgroups claim rows (the
   // special-queue overflow area has one block per workgroup of the grid)
   const bool claim = P.grid < P.rows;
-  const dim3 grid(claim ? P.grid : P.rows), block(NT);
+  const bool split = P.split_s >= 2 && fastld && xm == kXmNone && P.rows <= kSplitRows;
+  const dim3 grid(split ? P.rows * P.split_s : (claim ? P.grid : P.rows)), block(NT);
   void (*kern)(KArgs) = nullptr;
-  if (claim) {
+  if (split) {
+    switch (P.split_nv) {
+      case 1: kern = k_split<1>; break;
+      case 2: kern = k_split<2>; break;
+      case 4: kern = k_split<4>; break;
+      case 8: kern = k_split<8>; break;
+      default: return hipErrorInvalidValue;
+    }
+  } else if (claim) {
     if (fastld)
       kern = xm == kXmNone ? k_stats_rows<true, kXmNone> : xm == kXmLight ? k_stats_rows<true, kXmLight>
                                                                           : k_stats_rows<true, kXmCap>;

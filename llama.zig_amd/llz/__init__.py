@@ -41,7 +41,8 @@ EXPORTED = (
     "llz_argmax_rows", "llz_rng_seed", "llz_rng_next", "llz_rng_float", "llz_rng_uniforms",
     "llz_sampler_create", "llz_sampler_destroy", "llz_sampler_sample", "llz_sampler_sample_uniform",
     "llz_sampler_sample_config", "llz_sampler_get_state", "llz_sampler_set_state", "llz_debug_math",
-    "llz_debug_hw_error", "llz_debug_kernel_events", "llz_debug_set_queue_cap", "llz_strerror",
+    "llz_debug_hw_error", "llz_debug_kernel_events", "llz_debug_set_queue_cap", "llz_debug_set_split",
+    "llz_strerror",
 )
 
 
@@ -168,6 +169,8 @@ def _lib():
         L.llz_debug_kernel_events.restype = C.c_int
         L.llz_debug_set_queue_cap.argtypes = [C.c_uint32]
         L.llz_debug_set_queue_cap.restype = C.c_int
+        L.llz_debug_set_split.argtypes = [i32]
+        L.llz_debug_set_split.restype = C.c_int
         L.llz_strerror.argtypes = [C.c_int]
         L.llz_strerror.restype = C.c_char_p
         _LIB = L
@@ -247,6 +250,7 @@ PATH_BUCKETS = 64  # full row without a sort: kept prefix, total and draw from p
 PATH_TOKEN_ONLY = 128  # the token decided without the exact normaliser (calls asking for the token alone)
 PATH_DECLINE_SHIFT = 8  # bits 8-15: why the bucket path declined a full-row row (a number, not flags)
 PATH_RECOLLECT = 1 << 16  # a flooded candidate list collected again (its largest terms)
+PATH_SPLIT = 1 << 17  # token-only row finished from chunks read by several workgroups (with PATH_TOKEN_ONLY)
 
 
 def sample_rows(logits, cfg: SamplerConfig, uniforms, prev_tokens=None, *, post: Optional[LogitPost] = None,
@@ -430,6 +434,15 @@ def debug_set_queue_cap(cap: int) -> None:
     """The single pass's special-queue chunk for following calls (0: the
     kernel's own); a test hook, results do not depend on it."""
     _check(_lib().llz_debug_set_queue_cap(int(cap)), "llz_debug_set_queue_cap")
+
+
+def debug_set_split(mode) -> None:
+    """Split rows for following calls (token-only calls of at most 64 plain
+    rows read each row with several workgroups, one chunk of 2048 nv logits
+    each): True or 1 turns them off, False or 0 restores the library's
+    choice, 2, 4 or 8 asks for nv at least that.  A test hook; results do
+    not depend on it."""
+    _check(_lib().llz_debug_set_split(int(mode)), "llz_debug_set_split")
 
 
 def set_kernel_events(begin=None, end=None) -> None:
