@@ -12,9 +12,10 @@ the reference's default chain, and ``all`` every line, one JSON line each.
 A step is one llz_sample_rows call over one resident batch.  Inputs rotate
 over enough distinct device buffers that each step reads its logits from HBM,
 not from the 256 MB Infinity Cache.  Each line carries the roofline of the
-step's only kernel (k_stats), the fraction of rows on each path, and the CPU
-baseline (the reference sampler restated in C) timed on this host with one
-thread and with the host's share of threads.
+step's one kernel (k_stats; k_split for token-only calls of at most 32 rows,
+which read each row with several workgroups), the fraction of rows on each
+path, and the CPU baseline (the reference sampler restated in C) timed on
+this host with one thread and with the host's share of threads.
 """
 from __future__ import annotations
 
@@ -238,14 +239,14 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
                   "entropy": frac(llz.PATH_ENTROPY), "sum_le0": frac(llz.PATH_SUM_LE0),
                   "walk_rounds": frac(llz.PATH_WALK_ROUNDS), "resolve_generic": frac(llz.PATH_RESOLVE_GENERIC),
                   "buckets": frac(llz.PATH_BUCKETS), "token_only": frac(llz.PATH_TOKEN_ONLY),
-                  "recollect": frac(llz.PATH_RECOLLECT),
+                  "recollect": frac(llz.PATH_RECOLLECT), "split": frac(llz.PATH_SPLIT),
                   "single_pass": round(float(np.mean((paths & (llz.PATH_STREAM_NORM | llz.PATH_FULL_SORT)) == 0)), 4)}
     del probe
 
     # W untimed warmup steps right before the timed region (after the spot
     # check, whose host work leaves the GPU idle), a synchronisation, then the
     # timed region: K steps back to back on one stream, bracketed by HIP
-    # events on that stream.  k_stats is the only kernel of a step, so the
+    # events on that stream.  The sampling kernel is the only kernel of a step, so the
     # events' interval over K is its average launch duration (the host
     # enqueues faster than the GPU runs, so launches follow each other with
     # no idle gap).  The first dispatch after the synchronisation's idle gap
@@ -277,7 +278,8 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
     # (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, scaled by a device copy),
     # not measured by this run
     traffic = None
-    traffic_src = os.path.join("profiles", f"k_stats_{line}_traffic.json")
+    kernel = "k_split" if path_fracs["split"] >= 0.5 else "k_stats"
+    traffic_src = os.path.join("profiles", f"{kernel}_{line}_traffic.json")
     if os.path.exists(os.path.join(ROOT, traffic_src)):
         with open(os.path.join(ROOT, traffic_src)) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -303,7 +305,7 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
                    "parallelism": "none (1 GPU)"},
         "gbps": round(alg / (ms_per_step * 1e-3) / 1e9, 1),
         "ms_per_step_events": round(ms_events, 5),
-        "roofline": {"bound": "hbm", "kernel": "k_stats", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
                      "traffic": traffic, "traffic_source": traffic_src if traffic is not None else None,
                      "kernel_ms": round(ms_events, 5),

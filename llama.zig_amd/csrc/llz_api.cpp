@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -26,6 +27,13 @@ hipEvent_t g_ev_end = nullptr;
 std::atomic<uint32_t> g_queue_cap{0u};
 // test hook: split rows off, or their smallest chunk width (see llz_debug_set_split)
 std::atomic<int> g_split_mode{0};
+
+// With LLZ_DEBUG set in the environment, a HIP error behind an LLZ_E_HIP
+// return is printed to stderr (the return code alone does not name it).
+void report_hip(const char* where, hipError_t e) {
+  static const bool on = std::getenv("LLZ_DEBUG") != nullptr;
+  if (on) std::fprintf(stderr, "llz: %s: %s (%d)\n", where, hipGetErrorString(e), (int)e);
+}
 
 bool penalty_active(const llz_sampler_config* cfg, int32_t n_prev) {
   return cfg->repetition_penalty != 1.0f && n_prev > 0 && cfg->repetition_window > 0;
@@ -380,6 +388,7 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   Q.prev_win = (xf_src & kXfPen) ? d_prev_tokens + (n_prev - window) : nullptr;
   Q.split = P.split_s > 0 ? (SplitRow*)(ws + L.split) : nullptr;
   e = launch_sample(P, Q, g_ev_begin, g_ev_end, st);
+  if (e != hipSuccess) report_hip("llz_sample_rows: launch", e);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }
 

@@ -284,13 +284,31 @@ __device__ __forceinline__ bool split_chunk(const KArgs& A, int row, int c, Spli
   return S.elected != 0u;
 }
 
+// One workgroup of those that saw row `row`'s chunks published takes the
+// row (compare-and-swap of the row's word to the call's epoch); true in
+// every thread of that one.
+__device__ __forceinline__ bool split_take(const KArgs& A, int row, SplitShared& S) {
+  SplitRow& R = A.Q.split[row];
+  if (threadIdx.x == 0) {
+    uint32_t el = 0u;
+    unsigned long long cur = dev_ld(&R.elect);
+    if (cur != A.P.epoch)
+      el = __hip_atomic_compare_exchange_strong(&R.elect, &cur, (unsigned long long)A.P.epoch, __ATOMIC_RELAXED,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+               ? 1u
+               : 0u;
+    S.elected = el;
+  }
+  __syncthreads();
+  return S.elected != 0u;
+}
+
 // The merge (every thread of a workgroup that saw the row's chunks
-// published).  Returns 1 when it finished the row, 0 when the row is not
-// certified and this workgroup took it for the full path, -1 when another
-// workgroup took it.  Two workgroups may both merge a row: they read the
-// same final records and write the same outputs; only the one that takes
-// the row's word (compare-and-swap) goes on to the full path.
-__device__ __forceinline__ int split_merge(const KArgs& A, int row, SplitShared& S) {
+// published).  Returns true when it finished the row (outputs written),
+// false when the row is not certified.  Two workgroups may both merge a row
+// (k_split merges before taking the row, to save a round trip): they read
+// the same final records and write the same outputs.
+__device__ __forceinline__ bool split_merge(const KArgs& A, int row, SplitShared& S) {
   const RowParams& P = A.P;
   const RowPtrs& Q = A.Q;
   const int t = (int)threadIdx.x, lane = lane_id();
@@ -365,6 +383,7 @@ __device__ __forceinline__ int split_merge(const KArgs& A, int row, SplitShared&
     for (int h = 0; h < kPer; ++h) {
       const int i = h * kSplitNT + t;
       const bool live = i < nslots && (uint32_t)(i % kSplitK) < S.ncv[i / kSplitK];
+      if (bal64(live) == 0ull) continue;  // most slots belong to chunks that hold no candidate
       const float e = live ? exact_term(lo_f(en[h]), m, T, t1) : 0.0f;  // sampler.zig:85
       const bool cand = live && e >= theta;
       const uint64_t cb = bal64(cand);
@@ -387,23 +406,8 @@ __device__ __forceinline__ int split_merge(const KArgs& A, int row, SplitShared&
       ok = S.tfail == 0u;
     }
   }
-  if (ok) {
-    if (t == 0 && Q.status) Q.status[row] = kPathTokenOnly | kPathSplit;  // after token_select's store (same thread)
-    return 1;
-  }
-  // not certified: one workgroup takes the row
-  if (t == 0) {
-    uint32_t el = 0u;
-    unsigned long long cur = dev_ld(&R.elect);
-    if (cur != P.epoch)
-      el = __hip_atomic_compare_exchange_strong(&R.elect, &cur, (unsigned long long)P.epoch, __ATOMIC_RELAXED,
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-               ? 1u
-               : 0u;
-    S.elected = el;
-  }
-  __syncthreads();
-  return S.elected != 0u ? 0 : -1;
+  if (ok && t == 0 && Q.status) Q.status[row] = kPathTokenOnly | kPathSplit;  // after token_select's store (same thread)
+  return ok;
 }
 
 }  // namespace llz

@@ -1791,8 +1791,8 @@ __global__ __launch_bounds__(NT) void k_split(KArgs A) {
   const int ns = A.P.split_s;
   const int row = (int)blockIdx.x / ns, c = (int)blockIdx.x - row * ns;
   if (!split_chunk<NV>(A, row, c, U.split)) return;
-  if (split_merge(A, row, U.split) != 0) return;
-  __syncthreads();  // every wave is done with the merge's shared memory
+  if (split_merge(A, row, U.split)) return;
+  if (!split_take(A, row, U.split)) return;  // (its barrier: every wave is done with the merge's shared memory)
   stats_row<true, kXmNone>(A, row, U.stats, pen_sh, row);
 }
 

@@ -83,6 +83,8 @@ def main() -> int:
     ap.add_argument("--post", default="", help="soft-cap and logit scale, e.g. 30,0.5 (main.zig:653-666)")
     ap.add_argument("--penalty", default="", help="repetition window and penalty over as many random history "
                                                   "tokens per row, e.g. 32,1.1 (sampler.zig:54-75)")
+    ap.add_argument("--no-split", action="store_true",
+                    help="one workgroup per row also for token-only calls of few rows (the split rows off)")
     ap.add_argument("--chain", type=int, default=1,
                     help="launches back to back before reading (the last one's stamps, as in a benchmark loop)")
     a = ap.parse_args()
@@ -122,6 +124,8 @@ def main() -> int:
         prev = torch.from_numpy(np.random.default_rng(41).integers(0, w.vocab, size=(rows, int(win)))
                                 .astype(np.int32)).cuda()
     cfg = llz.SamplerConfig.of(params)
+    if a.no_split:
+        llz.debug_set_split(1)
     res = None
     for _ in range(a.reps):
         assert L.llz_debug_phase_stamps(buf.ctypes.data, rows_st, 1) == 0
