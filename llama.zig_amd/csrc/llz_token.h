@@ -35,30 +35,13 @@ namespace llz {
 constexpr int kTokCap = 256;  // candidates of a token-only row at most
 
 // Rank sort of c <= kTokCap distinct keys (e desc as ~bits, id asc) for
-// wave 0: up to one key per lane, wave 0 alone; otherwise wave w counts, for
-// every key, the keys of its eighth of the list below it (part[w][i], no
-// clearing needed), and after one barrier wave 0 adds the eight counts and
-// places each key.  Only wave 0 reads `out` (in LDS order after its own
-// writes).
+// wave 0: wave w counts, for every key, the keys of its eighth of the list
+// below it (part[w][i], no clearing needed); after one barrier wave 0 adds
+// the eight counts and places each key.  Only wave 0 reads `out` (in LDS
+// order after its own writes).
 __device__ __forceinline__ void token_sort(const uint64_t* in, uint64_t* out, uint16_t* part, int c) {
   constexpr int NW = kNT / kWave;
   const int lane = lane_id(), w = wave_id();
-  if (c <= kWave) {
-    // one key per lane of wave 0, ranked against the others by readlane: no
-    // barrier
-    if (w == 0) {
-      const uint64_t k = lane < c ? in[lane] : ~0ull;
-      const uint32_t klo = (uint32_t)k, khi = (uint32_t)(k >> 32);
-      uint32_t r = 0;
-      for (int j = 0; j < c; ++j) {
-        const uint64_t kj = ((uint64_t)readlane_u32(khi, j) << 32) | readlane_u32(klo, j);
-        r += kj < k ? 1u : 0u;
-      }
-      if (lane < c) out[r] = k;
-      __builtin_amdgcn_wave_barrier();
-    }
-    return;
-  }
   const int j0 = (w * c) / NW, j1 = ((w + 1) * c) / NW;
   for (int i = lane; i < c; i += kWave) {
     const uint64_t ki = in[i];
