@@ -153,7 +153,6 @@ struct FastShared {
   uint32_t tfail; // token-only rows: not certified (the exact phases follow)
 };
 
-typedef float llz_f4v __attribute__((ext_vector_type(4)));
 typedef int llz_i4v __attribute__((ext_vector_type(4)));
 
 // Raw buffer load of 16 bytes (buffer_load_dwordx4 ... offen): address =

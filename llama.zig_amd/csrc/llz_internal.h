@@ -6,6 +6,8 @@
 
 namespace llz {
 
+typedef float llz_f4v __attribute__((ext_vector_type(4)));  // four floats as one 16-byte access
+
 constexpr int kCandCap = 2048;  // candidate list capacity per row (power of two)
 constexpr int kPenMax = 64;     // fused repetition penalty: window entries at most (one per lane)
 constexpr int kQovfWave = 4096;  // k_stats special-queue overflow entries per wave

@@ -475,40 +475,50 @@ __device__ int prefix_filters(const List& L, int M, float p_nc, int n, const Row
   return K > M ? -1 : K;
 }
 
-// A row read tile by tile, eight logits per thread (thread t holds positions
-// t*8 .. t*8+7 of a 4096-logit tile), with the next tile's loads issued
+// A row read tile by tile, V logits per thread (thread t holds positions
+// t*V .. t*V+V-1 of a tile of 512 V), with the next tile's loads issued
 // before the current tile's work.  With 16-byte loads every thread loads
 // from min(pos, nlast) (the last start that stays inside the row), so no
 // branch separates a tile's loads from the work they overlap; the one
 // thread whose span crosses the row's end re-reads its logits where they are
 // used (fix_tail).  Positions past the row read as 0.
-struct RowTiles8 {
-  static constexpr int V = 8;
+template <int V_>
+struct RowTilesT {
+  static constexpr int V = V_;
+  static_assert(V % 4 == 0, "whole float4 per thread");
   const float* xs;
   int n;
   bool vec8;
   int nlast;
-  __device__ RowTiles8(const float* x, int n_, bool vec) : xs(x), n(n_), vec8(vec && n_ >= V),
+  __device__ RowTilesT(const float* x, int n_, bool vec) : xs(x), n(n_), vec8(vec && n_ >= V),
                                                           nlast(vec && n_ >= V ? ((n_ - V) & ~3) : 0) {}
+  // the row through a global-address-space pointer: the callers run out of
+  // line, where a generic pointer would make these flat loads, which count
+  // on the LDS counter too (every LDS wait would wait for them)
+  __device__ __forceinline__ const __attribute__((address_space(1))) float* g() const {
+    return (const __attribute__((address_space(1))) float*)xs;
+  }
   __device__ __forceinline__ void load(int pos, float (&r)[V]) const {
     if (vec8) {
       const int pc = min(pos, nlast);
-      const float4 q0 = *reinterpret_cast<const float4*>(xs + pc);
-      const float4 q1 = *reinterpret_cast<const float4*>(xs + pc + 4);
-      r[0] = q0.x; r[1] = q0.y; r[2] = q0.z; r[3] = q0.w;
-      r[4] = q1.x; r[5] = q1.y; r[6] = q1.z; r[7] = q1.w;
+#pragma unroll
+      for (int h = 0; h < V / 4; ++h) {
+        const llz_f4v q = *(const __attribute__((address_space(1))) llz_f4v*)(g() + pc + 4 * h);
+        r[4 * h + 0] = q.x; r[4 * h + 1] = q.y; r[4 * h + 2] = q.z; r[4 * h + 3] = q.w;
+      }
     } else {
 #pragma unroll
-      for (int k = 0; k < V; ++k) r[k] = pos + k < n ? xs[pos + k] : 0.0f;
+      for (int k = 0; k < V; ++k) r[k] = pos + k < n ? g()[pos + k] : 0.0f;
     }
   }
   __device__ __forceinline__ void fix_tail(int pos, float (&r)[V]) const {
     if (vec8 && pos > nlast && pos < n) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) r[k] = pos + k < n ? xs[pos + k] : 0.0f;
+      for (int k = 0; k < V; ++k) r[k] = pos + k < n ? g()[pos + k] : 0.0f;
     }
   }
 };
+using RowTiles8 = RowTilesT<8>;
 
 // Entropy sum over the whole row in index order (sampler.zig:129-132):
 // entropy -= p * log(p) for every p = RN(e / S) > 0, which is the exact
@@ -549,7 +559,13 @@ struct EntropyResult {
 
 template <class Src>
 __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float S, float T, uint32_t flags,
-                                                   SampleShared& sh, int bank, int row) {
+                                                   SampleShared& sh_arg, int bank, int row) {
+  // Out of line, the function receives generic pointers: the shared memory
+  // recast to the LDS address space (RowTiles8 reads the row through a
+  // global one), so that the accesses are ds_ and global_ instructions.  A
+  // flat access counts on both the LDS and the vector memory counters, so
+  // each LDS wait would also wait for the next tile's loads in flight.
+  SampleShared& sh = *(SampleShared*)(__attribute__((address_space(3))) SampleShared*)(&sh_arg);
   constexpr int EV = 2 * kLaneV;  // logits per thread per tile
   constexpr int ET = kNT * EV;
   constexpr int EP = kWave * EV;  // the prologue's terms (wave 0's share of the first tile)
@@ -562,8 +578,7 @@ __device__ __noinline__ EntropyResult entropy_pass(Src X, int n, float m, float 
   const float rS = 1.0f / S;
   const int t = (int)threadIdx.x;
 
-  const RowTiles8 rt(X.x, n, vec);
-  static_assert(RowTiles8::V == EV, "eight logits per thread");
+  const RowTilesT<EV> rt(X.x, n, vec);
   // sampler.zig:85 and :131 on one argument x; the term is +0 when p == 0
   auto exact_term = [&](float x) {
     const float p = exp_f32(x) / S;
@@ -724,9 +739,12 @@ __device__ __noinline__ NormResult select_norm_fallback(const KArgs* A, int row,
                                                         int bank, float m_known) {
   const RowParams& P = A->P;
   const Src X = make_src<Src>(P, A->Q, row, pen);
-  if (threadIdx.x == 0) sh.cand_count = 0;
+  // the shared memory in the LDS address space (a generic reference would
+  // make every access flat)
+  SampleShared& shl = *(SampleShared*)(__attribute__((address_space(3))) SampleShared*)(&sh);
+  if (threadIdx.x == 0) shl.cand_count = 0;
   NormResult r;
-  r.S = row_normaliser(X, P.n, P, sh, bank, r.m, m_known);
+  r.S = row_normaliser(X, P.n, P, shl, bank, r.m, m_known);
   r.bank = bank;
   return r;
 }

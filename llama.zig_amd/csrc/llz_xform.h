@@ -25,6 +25,14 @@
 
 namespace llz {
 
+// A row's logits through a global-address-space pointer.  The readers below
+// also run inside out-of-line functions, where a generic pointer makes flat
+// loads, which count on the LDS counter too: every LDS wait there would then
+// also wait for the row's loads in flight.
+__device__ __forceinline__ const __attribute__((address_space(1))) float* grow(const float* x) {
+  return (const __attribute__((address_space(1))) float*)x;
+}
+
 // main.zig:653-666 on one logit.
 __device__ __forceinline__ float logit_post(float v, uint32_t xf, float cap, float inv_scale) {
   if (xf & kXfCap) v = tanh_f32(v / cap) * cap;
@@ -151,7 +159,7 @@ struct RowSrcT {
     return v;
   }
 
-  __device__ __forceinline__ float at(int i) const { return fix(i, x[i]); }
+  __device__ __forceinline__ float at(int i) const { return fix(i, grow(x)[i]); }
 
   // Four consecutive read values from position pos; positions >= n are left
   // as they are (callers fill them with their own neutral value).  pre4:
@@ -177,11 +185,11 @@ struct RowSrcT {
   // kLaneV consecutive logits from pos (positions >= n read as 0).
   __device__ __forceinline__ void load4(int pos, int n, bool vec, float (&v)[kLaneV]) const {
     if (vec && pos + kLaneV <= n) {
-      const float4 q = *reinterpret_cast<const float4*>(x + pos);
+      const llz_f4v q = *(const __attribute__((address_space(1))) llz_f4v*)(grow(x) + pos);
       v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
     } else {
 #pragma unroll
-      for (int k = 0; k < kLaneV; ++k) v[k] = pos + k < n ? x[pos + k] : 0.0f;
+      for (int k = 0; k < kLaneV; ++k) v[k] = pos + k < n ? grow(x)[pos + k] : 0.0f;
     }
     if (xf != 0u) {
 #pragma unroll
@@ -201,17 +209,17 @@ struct PlainSrc {
   const float* x;
   __device__ __forceinline__ float pre(float v) const { return v; }
   __device__ __forceinline__ float fix(int, float v) const { return v; }
-  __device__ __forceinline__ float at(int i) const { return x[i]; }
+  __device__ __forceinline__ float at(int i) const { return grow(x)[i]; }
   __device__ __forceinline__ float4 pre4(int, float4 v, int) const { return v; }
   __device__ __forceinline__ float4 pen4(int, float4 v, int) const { return v; }
   __device__ __forceinline__ float4 fix4(int, float4 v, int) const { return v; }
   __device__ __forceinline__ void load4(int pos, int n, bool vec, float (&v)[kLaneV]) const {
     if (vec && pos + kLaneV <= n) {
-      const float4 q = *reinterpret_cast<const float4*>(x + pos);
+      const llz_f4v q = *(const __attribute__((address_space(1))) llz_f4v*)(grow(x) + pos);
       v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
     } else {
 #pragma unroll
-      for (int k = 0; k < kLaneV; ++k) v[k] = pos + k < n ? x[pos + k] : 0.0f;
+      for (int k = 0; k < kLaneV; ++k) v[k] = pos + k < n ? grow(x)[pos + k] : 0.0f;
     }
   }
 };
