@@ -79,6 +79,35 @@ def test_workspace_bytes():
     assert L.llz_sample_workspace_bytes(1, 10, C.byref(c), -1) == 0
 
 
+def test_workspace_split_section():
+    """Calls of at most 64 rows carry the split rows' records, 34,880 B per row
+    (64 chunk records of 32 B, the election word and its padding, 64 x 64 list
+    words of 8 B), last in the workspace; larger calls do not."""
+    cfg = llz.SamplerConfig(temperature=1.0, top_k=40, top_p=0.95, min_p=0.05)
+    per_row = 64 * 32 + 64 + 64 * 64 * 8
+    assert per_row == 34880
+
+    def step(rows):  # the bytes one more row adds
+        return llz.workspace_bytes(rows + 1, 128256, cfg) - llz.workspace_bytes(rows, 128256, cfg)
+
+    # every other section grows by the same bytes per row below and above 64
+    # rows (up to 256), so one more row costs the split record more below 64
+    # (sections are 256-byte aligned)
+    assert abs((step(10) - step(100)) - per_row) <= 512
+    # and the 65th row drops the whole section
+    assert llz.workspace_bytes(65, 128256, cfg) < llz.workspace_bytes(64, 128256, cfg) + step(100) - 63 * per_row
+
+
+def test_split_hook_modes():
+    """llz_debug_set_split takes 0, 1, 2, 4 and 8 only (host-side, no GPU call)."""
+    L = llz.library()
+    for ok in (0, 1, 2, 4, 8):
+        assert L.llz_debug_set_split(ok) == llz.LLZ_OK, ok
+    for bad in (3, 5, 16, -1, 0x102, 0x200):
+        assert L.llz_debug_set_split(bad) == llz.LLZ_E_INVALID_ARG, bad
+    assert L.llz_debug_set_split(0) == llz.LLZ_OK
+
+
 def test_argument_validation_without_gpu():
     """Invalid calls return an error code before any HIP call is made."""
     L = llz.library()
