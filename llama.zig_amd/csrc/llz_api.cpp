@@ -341,10 +341,14 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   // aligned rows reads each row with S workgroups of one chunk each (the
   // smallest chunk, 2048 nv logits, whose rows x S workgroups fit the CUs at
   // once), where one workgroup per row would leave most CUs idle.
-  if (split_room && tok_only && (xf_src | xb) == 0u && vec && vocab % 4 == 0 && P.tok_theta > 0.0f &&
-      P.l2e_t > 0.0f && P.l2e_t <= 0x1p40f && g_split_mode.load(std::memory_order_relaxed) != 1) {
+  // Rows read through post-processing or the fused penalty take chunks of at
+  // most 2 float4 per thread: each logit's exact transform is then a few per
+  // thread (calls of up to 8 rows at 128k vocab).
+  if (split_room && tok_only && vec && vocab % 4 == 0 && P.tok_theta > 0.0f && P.l2e_t > 0.0f &&
+      P.l2e_t <= 0x1p40f && g_split_mode.load(std::memory_order_relaxed) != 1) {
     const int cus = device_cus(st);
-    for (int nv = std::max(1, g_split_mode.load(std::memory_order_relaxed)); nv <= kSplitNV && cus > 0; nv *= 2) {
+    const int nv_max = (xf_src | xb) != 0u ? 2 : kSplitNV;
+    for (int nv = std::max(1, g_split_mode.load(std::memory_order_relaxed)); nv <= nv_max && cus > 0; nv *= 2) {
       const int s = (vocab + 2048 * nv - 1) / (2048 * nv);
       if (s <= kSplitMax && rows * s <= cus) {
         if (s >= 2) {

@@ -55,6 +55,7 @@
 #include "llz_select.h"
 #include "llz_token.h"
 #include "llz_wg.h"
+#include "llz_xform.h"
 
 namespace llz {
 
@@ -72,6 +73,8 @@ struct SplitShared {
   float wvt[kSplitW];
   uint32_t win[kSplitW];    // elements below B per wave
   unsigned long long lst[kSplitK];  // the chunk's list, staged for wave 0's stores
+  uint32_t pen[kPenMax];  // the penalised positions in this chunk (fused penalty)
+  uint32_t npen;
   uint32_t ncoll;     // entries written to the chunk's list
   uint32_t nb;        // bins collected
   uint32_t elected;   // this workgroup saw every chunk published (then: took the row's full path)
@@ -107,9 +110,12 @@ __device__ __forceinline__ float4 split_ld4(const float* xr, int pos, int n) {
 
 // Chunk c of row `row` (every thread of the workgroup), NV = split_nv float4
 // per thread (a template parameter: the loads, all issued at once, need no
-// branch between them).  Returns true in every thread of a workgroup that
-// saw every chunk of the row published and goes on to merge it.
-template <int NV>
+// branch between them).  XF: the row is read through the caller's
+// post-processing and the fused repetition penalty (P.xf_src), applied
+// exactly to every logit of the chunk as it lands (a few per thread).
+// Returns true in every thread of a workgroup that saw every chunk of the
+// row published and goes on to merge it.
+template <int NV, bool XF>
 __device__ __forceinline__ bool split_chunk(const KArgs& A, int row, int c, SplitShared& S) {
   const RowParams& P = A.P;
   const RowPtrs& Q = A.Q;
@@ -127,6 +133,54 @@ __device__ __forceinline__ bool split_chunk(const KArgs& A, int row, int c, Spli
   float4 v[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) v[j] = split_ld4(xr, base + (j * kSplitNT + t) * 4, n);  // absent: -inf
+  if constexpr (XF) {
+    const uint32_t xf = P.xf_src;
+    // main.zig:653-666 on each logit of the row (positions past it stay -inf)
+    if (xf & (kXfCap | kXfScale)) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int pos = base + (j * kSplitNT + t) * 4;
+        v[j].x = pos + 0 < n ? logit_post(v[j].x, xf, P.cap, P.inv_scale) : v[j].x;
+        v[j].y = pos + 1 < n ? logit_post(v[j].y, xf, P.cap, P.inv_scale) : v[j].y;
+        v[j].z = pos + 2 < n ? logit_post(v[j].z, xf, P.cap, P.inv_scale) : v[j].z;
+        v[j].w = pos + 3 < n ? logit_post(v[j].w, xf, P.cap, P.inv_scale) : v[j].w;
+      }
+    }
+    // sampler.zig:54-75: each distinct id < n of the window (lane j of wave
+    // 0 holds id j) that lies in this chunk, penalised by the thread that
+    // holds it
+    if (xf & kXfPen) {
+      if (w == 0) {
+        const uint32_t id = pen_window_id(P, Q, row);
+        bool first = id < (uint32_t)n;
+        for (int j = 0; j < P.pen_w; ++j) {
+          const uint32_t o = readlane_u32(id, j);
+          first = first && !(j < lane && o == id);
+        }
+        const bool mine = first && id >= (uint32_t)base && id - (uint32_t)base < (uint32_t)(kSplitSeg * NV);
+        const uint64_t bm = bal64(mine);
+        const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+        if (mine) S.pen[__popcll(bm & lt)] = id;
+        if (lane == 0) S.npen = (uint32_t)__popcll(bm);
+      }
+      lds_barrier();
+      const int np = (int)S.npen;
+      for (int i = 0; i < np; ++i) {
+        const uint32_t rel = S.pen[i] - (uint32_t)base;
+        const int jj = (int)(rel / kSplitSeg), q = (int)(rel % kSplitSeg);
+        if ((q >> 2) == t) {
+          const int k = q & 3;
+#pragma unroll
+          for (int j = 0; j < NV; ++j) {
+            v[j].x = j == jj && k == 0 ? penalise(v[j].x, P.rpen) : v[j].x;
+            v[j].y = j == jj && k == 1 ? penalise(v[j].y, P.rpen) : v[j].y;
+            v[j].z = j == jj && k == 2 ? penalise(v[j].z, P.rpen) : v[j].z;
+            v[j].w = j == jj && k == 3 ? penalise(v[j].w, P.rpen) : v[j].w;
+          }
+        }
+      }
+    }
+  }
   if (t < kSplitBins) S.hist[t] = 0u;
   if (t == 0) S.ncoll = 0u;
   float mx = -__builtin_inff();

@@ -1784,16 +1784,16 @@ union SplitLds {
   SplitShared split;
   StatsShared stats;
 };
-template <int NV>
+template <int NV, int XM>
 __global__ __launch_bounds__(NT) void k_split(KArgs A) {
   __shared__ SplitLds U;
-  __shared__ PenShared pen_sh;  // unused by plain rows
+  __shared__ PenShared pen_sh;  // the single-row path's penalised positions (kXfPen)
   const int ns = A.P.split_s;
   const int row = (int)blockIdx.x / ns, c = (int)blockIdx.x - row * ns;
-  if (!split_chunk<NV>(A, row, c, U.split)) return;
+  if (!split_chunk<NV, XM != kXmNone>(A, row, c, U.split)) return;
   if (split_merge(A, row, U.split)) return;
   if (!split_take(A, row, U.split)) return;  // (its barrier: every wave is done with the merge's shared memory)
-  stats_row<true, kXmNone>(A, row, U.stats, pen_sh, row);
+  stats_row<true, XM>(A, row, U.stats, pen_sh, row);
 }
 
 }  // namespace
@@ -1810,16 +1810,24 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
   // more rows than workgroups: the grid's workgroups claim rows (the
   // special-queue overflow area has one block per workgroup of the grid)
   const bool claim = P.grid < P.rows;
-  const bool split = P.split_s >= 2 && fastld && xm == kXmNone && P.rows <= kSplitRows;
+  // transformed rows split with chunks of at most 2 float4 per thread (each
+  // logit's exact post-processing is then a few per thread)
+  const bool split = P.split_s >= 2 && fastld && P.rows <= kSplitRows && (xm == kXmNone || P.split_nv <= 2);
   const dim3 grid(split ? P.rows * P.split_s : (claim ? P.grid : P.rows)), block(NT);
   void (*kern)(KArgs) = nullptr;
   if (split) {
-    switch (P.split_nv) {
-      case 1: kern = k_split<1>; break;
-      case 2: kern = k_split<2>; break;
-      case 4: kern = k_split<4>; break;
-      case 8: kern = k_split<8>; break;
-      default: return hipErrorInvalidValue;
+    if (xm == kXmNone) {
+      switch (P.split_nv) {
+        case 1: kern = k_split<1, kXmNone>; break;
+        case 2: kern = k_split<2, kXmNone>; break;
+        case 4: kern = k_split<4, kXmNone>; break;
+        case 8: kern = k_split<8, kXmNone>; break;
+        default: return hipErrorInvalidValue;
+      }
+    } else if (xm == kXmLight) {
+      kern = P.split_nv == 1 ? k_split<1, kXmLight> : k_split<2, kXmLight>;
+    } else {
+      kern = P.split_nv == 1 ? k_split<1, kXmCap> : k_split<2, kXmCap>;
     }
   } else if (claim) {
     if (fastld)

@@ -25,17 +25,18 @@ PATH_TOKEN_ONLY = 128
 PATH_SPLIT = 1 << 17
 
 
-def _run(cuda, x, params, u, cap=64, split=True):
+def _run(cuda, x, params, u, cap=64, split=True, post=None, prev=None):
     """split: True (the library's choice), False (off), or the chunk width
     nv in float4 per thread (2, 4, 8: at least that)."""
     import torch
 
     cfg = llz.SamplerConfig.of(params)
+    pt = None if prev is None else torch.from_numpy(np.ascontiguousarray(prev, dtype=np.int32)).to(cuda)
     llz.debug_set_split(0 if split is True else (1 if split is False else int(split)))
     try:
         res = llz.sample_rows(torch.from_numpy(np.ascontiguousarray(x)).to(cuda), cfg,
-                              torch.from_numpy(np.ascontiguousarray(u, dtype=np.float32)).to(cuda),
-                              kept_cap=cap, probs=False, stats=False, path=True)
+                              torch.from_numpy(np.ascontiguousarray(u, dtype=np.float32)).to(cuda), pt,
+                              post=post, kept_cap=cap, probs=False, stats=False, path=True)
         torch.cuda.synchronize()
     finally:
         llz.debug_set_split(False)
@@ -45,10 +46,12 @@ def _run(cuda, x, params, u, cap=64, split=True):
                 cap=cap)
 
 
-def _check_oracle(x, params, u, g, rows=None):
+def _check_oracle(x, params, u, g, rows=None, post=None, prev=None):
     rows = range(x.shape[0]) if rows is None else rows
+    if post is not None:
+        x = O.logit_post(x, post.final_logit_softcapping, post.logit_scale)
     for r in rows:
-        o = O.sample_row(x[r], params, u[r])
+        o = O.sample_row(x[r], params, u[r], prev_tokens=None if prev is None else prev[r])
         ctx = f"row {r} (path {g['path'][r]:#x})"
         assert g["tokens"][r] == o.token, f"{ctx}: token {g['tokens'][r]} != {o.token}"
         assert g["consumed"][r] == o.consumed, f"{ctx}: consumed"
@@ -224,3 +227,59 @@ def test_split_rows_workspace_reuse(cuda):
                      path=res.row_path.cpu().numpy().view(np.uint32), cap=64)
             assert _split_frac(g) >= 0.9
             _check_oracle(x, w.params, u, g, rows=range(0, r, max(1, r // 4)))
+
+
+# ---- rows read through the decode loop's post-processing and the penalty
+
+POSTS = {"cap+scale": (30.0, 0.5), "scale": (0.0, 0.5), "cap": (30.0, 1.0), "none": None}
+
+
+def _histories(x, n_prev, seed, top=4):
+    """History rows of n_prev random ids whose last `top` are the row's
+    largest logits (the penalty then moves the maximum and the kept set)."""
+    rows, n = x.shape
+    prev = np.random.default_rng(seed).integers(0, n, (rows, n_prev)).astype(np.uint32)
+    for r in range(rows):
+        prev[r, -top:] = np.argsort(-x[r], kind="stable")[:top]
+    return prev
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+@pytest.mark.parametrize("pen", [False, True])
+@pytest.mark.parametrize("post_name", list(POSTS))
+def test_split_rows_transformed(cuda, post_name, pen, rows):
+    """Soft-cap and/or logit scale (main.zig:653-666) and the repetition
+    penalty over a 32-token window (sampler.zig:54-75), applied exactly to
+    every logit of a chunk: the same outputs as the unsplit call, and the
+    oracle's on the post-processed rows with the same histories."""
+    if post_name == "none" and not pen:
+        pytest.skip("plain rows: covered above")
+    w = WORKLOADS["c2"]
+    x = w.logits(rows)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    post = None if POSTS[post_name] is None else llz.LogitPost(final_logit_softcapping=POSTS[post_name][0],
+                                                               logit_scale=POSTS[post_name][1])
+    params = w.params
+    prev = None
+    if pen:
+        params = dataclasses.replace(params, repetition_window=32, repetition_penalty=1.1)
+        prev = _histories(x, 32, seed=rows)
+    g = _run(cuda, x, params, u, post=post, prev=prev)
+    assert _split_frac(g) >= 0.5, f"paths {[hex(p) for p in g['path']]}"
+    _same(g, _run(cuda, x, params, u, split=False, post=post, prev=prev))
+    _check_oracle(x, params, u, g, post=post, prev=prev)
+
+
+def test_split_rows_decode_loop_shape(cuda):
+    """The reference's decode step: one row, the default chain (T 0.8, top-p
+    0.9), soft-cap 30 and logit scale 0.5, the default penalty over the last
+    32 tokens; eight rows of configuration 1's generator, one call each."""
+    w = WORKLOADS["c1"]
+    x = w.logits(8)
+    u = llz.rng_uniforms(w.uniform_seed, 8)
+    post = llz.LogitPost(final_logit_softcapping=30.0, logit_scale=0.5)
+    params = dataclasses.replace(w.params, repetition_window=32, repetition_penalty=1.1)
+    prev = _histories(x, 32, seed=5)
+    for r in range(8):
+        g = _run(cuda, x[r:r + 1], params, u[r:r + 1], cap=256, post=post, prev=prev[r:r + 1])
+        _check_oracle(x[r:r + 1], params, u[r:r + 1], g, post=post, prev=prev[r:r + 1])

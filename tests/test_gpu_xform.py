@@ -42,6 +42,16 @@ HOST_THREADS = 16
 PATH_TOKEN_ONLY = 128
 
 
+@pytest.fixture(autouse=True)
+def _one_workgroup_per_row():
+    """These tests exercise k_stats's transform modes, so calls of few rows
+    run one workgroup per row here (split rows, which apply the same
+    transforms in their chunk pass, are tested in test_gpu_split.py)."""
+    llz.debug_set_split(1)
+    yield
+    llz.debug_set_split(0)
+
+
 def _oracle_post(x, post):
     if post is None:
         return x
