@@ -7,7 +7,9 @@ fp32 with configuration 2's logits and filter chain (T 1.0, top-k 40, top-p
 the reference's other configurations, ``headline-exact``, ``headline-post``,
 ``headline-penalty`` and ``headline-default`` the headline's logits with the
 exact outputs, the decode loop's post-processing, the repetition penalty or
-the reference's default chain, and ``all`` every line, one JSON line each.
+the reference's default chain, ``c1-decode`` configuration 1's one-row calls
+with the post-processing and the penalty (the reference's decode step), and
+``all`` every line, one JSON line each.
 
 A step is one llz_sample_rows call over one resident batch.  Inputs rotate
 over enough distinct device buffers that each step reads its logits from HBM,
@@ -147,7 +149,8 @@ def c1_latency(w, x_host, u_host, reps: int) -> dict:
 # decode loop's post-processing, soft-cap 30 and logit scale 0.5
 # (main.zig:653-666); "penalty": the token call with the reference's default
 # repetition penalty (window 32, 1.1, sampler.zig:54-75) over 32 history
-# tokens per row.
+# tokens per row; "decode": both, on configuration 1's one-row calls (the
+# reference's decode step, main.zig:653-667).
 LINES = {
     "headline": ("headline", "token"),
     "headline-exact": ("headline", "exact"),
@@ -155,6 +158,7 @@ LINES = {
     "headline-penalty": ("headline", "penalty"),
     "headline-default": ("headline-default", "token"),
     "c1": ("c1", "token"),
+    "c1-decode": ("c1", "decode"),
     "c2": ("c2", "token"),
     "c3": ("c3", "token"),
     "c4": ("c4", "token"),
@@ -178,9 +182,9 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
     batch_bytes = rows * vocab * 4
     params = w.params
     post = prev = None
-    if mode == "post":
+    if mode in ("post", "decode"):
         post = llz.LogitPost(final_logit_softcapping=30.0, logit_scale=0.5)
-    if mode == "penalty":
+    if mode in ("penalty", "decode"):
         params = dataclasses.replace(params, repetition_window=32, repetition_penalty=1.1)
         prev_host = np.random.default_rng(41).integers(0, vocab, size=(rows, 32)).astype(np.int32)
         prev = torch.from_numpy(prev_host).to(dev)
@@ -231,8 +235,10 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
     x_chk = x_host[:nchk]
     if post is not None:
         x_chk = O.logit_post(x_chk, post.final_logit_softcapping, post.logit_scale)
-    o_tok, o_con, _ = O.sample_rows(x_chk, params, u_host[:nchk],
-                                    prev_tokens=None if prev is None else prev_host[:nchk], threads=HOST_THREADS)
+    p_chk = None
+    if prev is not None:  # configuration 1's calls share the one history row
+        p_chk = prev_host[:nchk] if prev_host.shape[0] >= nchk else np.tile(prev_host[:1], (nchk, 1))
+    o_tok, o_con, _ = O.sample_rows(x_chk, params, u_host[:nchk], prev_tokens=p_chk, threads=HOST_THREADS)
     parity_ok = bool(np.array_equal(tok0[:nchk], o_tok) and np.array_equal(con0[:nchk], o_con))
     frac = lambda bit: round(float(np.mean((paths & bit) != 0)), 4)  # noqa: E731
     path_fracs = {"stream_norm": frac(llz.PATH_STREAM_NORM), "full_sort": frac(llz.PATH_FULL_SORT),
@@ -318,7 +324,7 @@ def run_workload(line: str, steps: int, warmup: int, args) -> dict:
     if prev is not None:
         out["config"].update(repetition_window=params.repetition_window,
                              repetition_penalty=params.repetition_penalty, history_tokens=int(prev_host.shape[1]))
-    if name == "c1":
+    if line == "c1":
         out["latency"] = c1_latency(w, x_host, u_host, reps=50)
     del xs, us, call
     torch.cuda.empty_cache()
@@ -344,7 +350,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--workload", default="headline",
                     help="headline (default), headline-exact, headline-post, headline-penalty, headline-default, "
-                         "c1 .. c5, or all (one JSON line each)")
+                         "c1 .. c5, c1-decode, or all (one JSON line each)")
     ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="wall-clock budget of each CPU baseline mode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
