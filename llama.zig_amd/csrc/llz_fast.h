@@ -149,6 +149,7 @@ struct FastShared {
   int done;
   uint32_t diag;  // kPathWalkRounds / kPathResolveGeneric (diagnostics for the row's status)
   float qsum[fastp::W];  // token-only rows: per wave, the sum of its estimates q
+  float qwsum[fastp::W];  // token-only rows: per wave, its segments' sums of q times n - their first position
   uint32_t tcand; // token-only rows: candidates collected
   uint32_t tfail; // token-only rows: not certified (the exact phases follow)
 };

@@ -122,7 +122,8 @@ struct SplitRec {
   unsigned long long mc;   // bits of the chunk's maximum m (NaNs skipped) | bits of c = RN(m l2e_t) << 32
   unsigned long long sv;   // bits of s = sum of exp2(fma(v, l2e_t, -c)) | bits of vt << 32, the largest
                            // logit of the chunk's possible candidates left out of its list (-inf: none)
-  unsigned long long nf;   // entries of its list | flags << 32 (1: a NaN or a maximum beyond 3e38)
+  unsigned long long nf;   // entries of its list | 0x10000 for a NaN or a maximum beyond 3e38 | bits of the
+                           // sum of exp2(fma(v, l2e_t, -c)) (n - pos) << 32
 };
 struct SplitRow {
   SplitRec rec[kSplitMax];

@@ -70,6 +70,7 @@ struct SplitShared {
   float wm[kSplitW];
   uint32_t wnan[kSplitW];
   float ws[kSplitW];
+  float wws[kSplitW];  // per wave: its estimates times n - their position
   float wvt[kSplitW];
   uint32_t win[kSplitW];    // elements below B per wave
   unsigned long long lst[kSplitK];  // the chunk's list, staged for wave 0's stores
@@ -83,7 +84,7 @@ struct SplitShared {
   uint16_t part[kSplitW * kTokCap];
   uint32_t ncv[kSplitMax];   // per chunk: its list entries that may pass (0: none)
   uint32_t tcand, tfail, bad;
-  float m, s_est;
+  float m, s_est, w_est;
 };
 
 // Device-coherent accesses to the split records, and the wait for this
@@ -211,7 +212,7 @@ __device__ __forceinline__ bool split_chunk(const KArgs& A, int row, int c, Spli
   const float B = P.split_b, bs = P.split_bs;
   // the estimates' sum, and the elements below B: counted, then (when more
   // than kSplitK) binned
-  float s = 0.0f;
+  float s = 0.0f, sw = 0.0f;
   uint32_t cin = 0u;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -221,6 +222,10 @@ __device__ __forceinline__ bool split_chunk(const KArgs& A, int row, int c, Spli
     const float q2 = __builtin_amdgcn_exp2f(fmaf(x.z, l2e, -cc));
     const float q3 = __builtin_amdgcn_exp2f(fmaf(x.w, l2e, -cc));
     s += (q0 + q1) + (q2 + q3);
+    // weighted by n - pos (the interval of S, llz_token.h): absent
+    // positions have q = 0
+    const float rem = (float)(n - (base + (j * kSplitNT + t) * 4));
+    sw += (q0 * rem + q1 * (rem - 1.0f)) + (q2 * (rem - 2.0f) + q3 * (rem - 3.0f));
     cin += (uint32_t)(((mc - x.x) * l2e < B) + ((mc - x.y) * l2e < B) + ((mc - x.z) * l2e < B) +
                       ((mc - x.w) * l2e < B));
   }
@@ -300,9 +305,11 @@ __device__ __forceinline__ bool split_chunk(const KArgs& A, int row, int c, Spli
     }
   }
   const float ws = wave_sum_f32(s);
+  const float wws = wave_sum_f32(sw);
   vt = wave_max_f32(vt);
   if (lane == 0) {
     S.ws[w] = ws;
+    S.wws[w] = wws;
     S.wvt[w] = vt;
   }
   lds_barrier();
@@ -315,12 +322,15 @@ __device__ __forceinline__ bool split_chunk(const KArgs& A, int row, int c, Spli
     if (lane == 0) {
       SplitRec& rc = R.rec[c];
       const float sum = ((S.ws[0] + S.ws[1]) + (S.ws[2] + S.ws[3])) + ((S.ws[4] + S.ws[5]) + (S.ws[6] + S.ws[7]));
+      const float wsum =
+          ((S.wws[0] + S.wws[1]) + (S.wws[2] + S.wws[3])) + ((S.wws[4] + S.wws[5]) + (S.wws[6] + S.wws[7]));
       float vm = S.wvt[0];
 #pragma unroll
       for (int i = 1; i < kSplitW; ++i) vm = fmaxf(vm, S.wvt[i]);
       dev_st(&rc.mc, pack2(mc, cc));
       dev_st(&rc.sv, pack2(sum, vm));
-      dev_st(&rc.nf, (unsigned long long)ncoll | ((unsigned long long)(special ? 1u : 0u) << 32));
+      dev_st(&rc.nf, (unsigned long long)(ncoll | (special ? 0x10000u : 0u)) |
+                         ((unsigned long long)__float_as_uint(wsum) << 32));
     }
     stores_done();  // the list and the summary complete
     if (lane == 0) {
@@ -389,7 +399,7 @@ __device__ __forceinline__ bool split_merge(const KArgs& A, int row, SplitShared
   }
   if (w == 0) {
     const bool on = lane < ns;
-    float mc = ninf, cc = 0.0f, sc = 0.0f, vt = ninf;
+    float mc = ninf, cc = 0.0f, sc = 0.0f, vt = ninf, wc = 0.0f;
     uint32_t nc = 0u, fl = 0u;
     if (on) {
       SplitRec& rc = R.rec[lane];
@@ -398,8 +408,9 @@ __device__ __forceinline__ bool split_merge(const KArgs& A, int row, SplitShared
       cc = hi_f(a);
       sc = lo_f(b);
       vt = hi_f(b);
-      nc = (uint32_t)d;
-      fl = (uint32_t)(d >> 32);
+      nc = (uint32_t)d & 0xffffu;
+      fl = ((uint32_t)d >> 16) & 1u;
+      wc = hi_f(d);
     }
     const float m = wave_max_f32(mc);
     bool bad = fl != 0u || !(fabsf(m) <= 3.0e38f) || nc > (uint32_t)kSplitK;
@@ -409,7 +420,9 @@ __device__ __forceinline__ bool split_merge(const KArgs& A, int row, SplitShared
     const bool live = on && mc > ninf;
     const float aw = fmaf(m, -l2e, cc);
     bad = bad || (live && !(aw <= 1.0f));
-    const float s_est = wave_sum_f32(live ? sc * __builtin_amdgcn_exp2f(aw) : 0.0f);
+    const float rc = __builtin_amdgcn_exp2f(aw);
+    const float s_est = wave_sum_f32(live ? sc * rc : 0.0f);
+    const float w_est = wave_sum_f32(live ? wc * rc : 0.0f);
     bool inc = false;
     if (live && !bad) {
       // completeness: the chunk's left-out elements stay below theta
@@ -423,6 +436,7 @@ __device__ __forceinline__ bool split_merge(const KArgs& A, int row, SplitShared
       S.bad = any_bad ? 1u : 0u;
       S.m = m;
       S.s_est = s_est;
+      S.w_est = w_est;
       S.tcand = 0u;
       S.tfail = 0u;
     }
@@ -454,7 +468,7 @@ __device__ __forceinline__ bool split_merge(const KArgs& A, int row, SplitShared
     ok = tc <= kTokCap;
     if (ok) {
       token_sort(S.tl, S.tl + kTokCap, S.part, tc);
-      if (w == 0) token_select(kernel_args_ptr(), row, S.tl + kTokCap, tc, S.s_est, u_row, theta, &S.tfail);
+      if (w == 0) token_select(kernel_args_ptr(), row, S.tl + kTokCap, tc, S.s_est, S.w_est, u_row, theta, &S.tfail);
       lds_barrier();
       LLZ_STAMP(sr, 10);
       ok = S.tfail == 0u;

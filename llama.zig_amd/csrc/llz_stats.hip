@@ -827,7 +827,14 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   const bool tok = (P.flags & kFlagTokenOnly) != 0u && fits;
   if (tok) {
     const float qs = wave_fold_f32(lane < nseg_w ? my_a : 0.0f);
-    if (lane == kWave - 1) F.qsum[w] = qs;
+    // and weighted by where they lie: segment w + W lane starts at position
+    // SEG (w + W lane), so each of its terms' weight n - pos is at most
+    // n - SEG (w + W lane) (the interval of S in llz_token.h)
+    const float qw = wave_fold_f32(lane < nseg_w ? my_a * (float)(n - SEG * (w + W * lane)) : 0.0f);
+    if (lane == kWave - 1) {
+      F.qsum[w] = qs;
+      F.qwsum[w] = qw;
+    }
   }
   if (!fits) {  // rows the fast path does not take: maximum and NaN scan only
     if constexpr (FASTLD) {
@@ -1013,13 +1020,15 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
   // in F.v, free once every wave has read the segment sums below.
   if (tok && !nanrow && fabsf(m) <= 3.0e38f && P.tok_theta > 0.0f) {
     LLZ_STAMP(row, 38);
-    float s_est = 0.0f;
+    float s_est = 0.0f, w_est = 0.0f;
     bool tbad = false;
 #pragma unroll
     for (int i = 0; i < W; ++i) {
       const float awi = fmaf(m, -l2e_t, F.cw[i]);
       tbad = tbad | ((G > i) & !(fabsf(awi) <= 64.0f));
-      s_est += G > i ? F.qsum[i] * __builtin_amdgcn_exp2f(awi) : 0.0f;
+      const float ri = __builtin_amdgcn_exp2f(awi);
+      s_est += G > i ? F.qsum[i] * ri : 0.0f;
+      w_est += G > i ? F.qwsum[i] * ri : 0.0f;
     }
     if (!tbad) {
       const float Rw_t = __builtin_amdgcn_exp2f(fmaf(m, -l2e_t, cw));
@@ -1146,7 +1155,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         static_assert(sizeof(F.qpos) >= (size_t)(kNT / kWave) * kTokCap * sizeof(uint16_t), "partial ranks fit the queue rows");
         token_sort(tl, tl + kTokCap, reinterpret_cast<uint16_t*>(&F.qpos[0][0]), tc);
         LLZ_STAMP(row, 34);
-        if (w == 0) token_select(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, u_row, theta_t, &F.tfail);
+        if (w == 0) token_select(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, w_est, u_row, theta_t, &F.tfail);
       } else if (t == 0) {
         F.tfail = 1u;
       }

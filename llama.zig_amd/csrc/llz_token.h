@@ -19,9 +19,11 @@
 //   - top-p compares the running sum, which lies within (2q + 4) 2^-24 of
 //     C_q / S, with top_p: that needs S itself.  The reference's S is the
 //     sequential f32 sum of n positive terms, within (n - 1) 2^-24 / (1 - (n -
-//     1) 2^-24) of the real sum (the recursive-summation bound), which phase
-//     L's estimates give to 2^-14 (2^-14 + est_xe on soft-capped rows); a
-//     top-p decision that holds at both ends of that interval holds at S.
+//     1) 2^-24) of the real sum (the recursive-summation bound), or within
+//     about 2^-24 sum_j e_j (n - j + 1) / S, the same bound by where the mass
+//     lies (an estimate of it comes with S's), which phase L's estimates
+//     give to 2^-14 (2^-14 + est_xe on soft-capped rows); a top-p decision
+//     that holds at both ends of that interval holds at S.
 // A row whose decisions all hold is finished here, bit-exact; any other row
 // continues with the exact phases.
 #pragma once
@@ -91,13 +93,14 @@ __device__ __forceinline__ double wave_incl_scan_f64(double x) {
 
 // Wave 0: the chain's decisions (sampler.zig:100-168) for a token-only row
 // from its candidates srt[0, c), sorted (e desc, id asc) -- every term e >=
-// theta, all of them exact -- and the estimate s_est of the normaliser.
+// theta, all of them exact -- and the estimate s_est of the normaliser
+// (w_est: of sum_j e_j (n - j), an upper bound's estimate; 0: unknown).
 // Writes the token, the draw flag, the kept count and ids; sets *tfail
 // instead when a decision does not hold over the interval of S.
 // Out of line; the launch's arguments come through the kernel's argument
 // segment (as the other out-of-line paths take them).
-__device__ __forceinline__ void token_select(const KArgs* A, int row, const uint64_t* srt, int c, float s_est, float u,
-                                          float theta, uint32_t* tfail) {
+__device__ __forceinline__ void token_select(const KArgs* A, int row, const uint64_t* srt, int c, float s_est,
+                                          float w_est, float u, float theta, uint32_t* tfail) {
   const RowParams& P = A->P;
   const RowPtrs& Q = A->Q;
   const int lane = lane_id();
@@ -139,7 +142,24 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   const int Lc = open_end ? M : L;
   // the interval of the reference's normaliser
   const double g = (double)(n - 1) * 0x1p-24;
-  const double gr = g / (1.0 - g) + 0x1p-14 + (double)P.est_xe;  // est_xe: soft-capped rows' estimates
+  double rs = g / (1.0 - g);
+  // The same bound by where the mass lies (w_est > 0): the computed partial
+  // sums of positive terms satisfy S^_i <= S_i (1 + gamma_i), so |S^ - S| <=
+  // u / (1 - u) sum_{i>=2} S^_i <= u / (1 - u) (1 + gamma_n) sum_i S_i, and
+  // sum_i S_i = sum_j e_j (n - j + 1) (j 1-based: e_j lies in the partial
+  // sums from the j-th on) <= W, estimated by w_est as s_est estimates S,
+  // so W / S <= (w_est / s_est) (1 + e) / (1 - e) <= (w_est / s_est) (1 +
+  // 2^-9) (e = 2^-14 + est_xe <= 2^-10.8).  With the row's mass spread
+  // evenly this halves the interval; with it near the row's end, far more.
+  if (w_est > 0.0f) {
+    const double gn = (double)n * 0x1p-24;
+    const double rw = 0x1p-24 / (1.0 - 0x1p-24) * (1.0 + gn / (1.0 - gn)) * ((double)w_est / (double)s_est) *
+                      (1.0 + 0x1p-9);
+    if (gn < 0.5 && rw < rs) rs = rw;
+  }
+  // the estimate's own error e; S^ in s_est [(1 - rs)(1 - e), (1 + rs)(1 + e)]
+  const double e_est = 0x1p-14 + (double)P.est_xe;  // est_xe: soft-capped rows' estimates
+  const double gr = rs + e_est + rs * e_est;
   const double S_lo = (double)s_est * (1.0 - gr), S_hi = (double)s_est * (1.0 + gr);
   if (!(S_lo > 0.0) || !(S_hi < 1.0e300)) ok = false;
   // 1/S at the interval's ends, rounded outwards (one rounding of 2^-53 each)

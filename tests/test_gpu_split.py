@@ -283,3 +283,39 @@ def test_split_rows_decode_loop_shape(cuda):
     for r in range(8):
         g = _run(cuda, x[r:r + 1], params, u[r:r + 1], cap=256, post=post, prev=prev[r:r + 1])
         _check_oracle(x[r:r + 1], params, u[r:r + 1], g, post=post, prev=prev[r:r + 1])
+
+
+# ---- the interval of S weighted by where the row's mass lies
+
+def _late_mass_rows(rows, n, seed):
+    """Rows whose largest terms lie in their last 1,000 positions, with a
+    top-p whose cut sits 0.3% past a cumulative sum: inside the
+    recursive-summation interval of S (about 0.77% at 128k terms), outside
+    the same bound weighted by position (about 0.01% here)."""
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0.0, 2.0, size=(rows, n)).astype(np.float32)
+    for r in range(rows):
+        x[r, n - 1000 + rng.choice(1000, 8, replace=False)] += np.float32(12.0)
+    base = dataclasses.replace(WORKLOADS["c1"].params, top_p=0.9)
+    u = rng.random(rows, dtype=np.float32)
+    tps = []
+    for r in range(rows):
+        o = O.sample_row(x[r], base, u[r])
+        c = np.cumsum(np.sort(o.probs.astype(np.float64))[::-1])
+        q = next(q for q in range(1, 8) if c[q + 1] > c[q] * 1.02)
+        tps.append(float(np.float32(c[q] * 1.003)))
+    return x, u, base, tps
+
+
+@pytest.mark.parametrize("split", [True, False], ids=["split", "one-workgroup"])
+def test_top_p_cut_certified_by_position_weighted_interval(cuda, split):
+    """Top-p cuts 0.3% from a cumulative sum, in rows whose mass lies at
+    their end: certified on the token path (both launches) and the oracle's
+    results."""
+    n = 128256
+    x, u, base, tps = _late_mass_rows(4, n, seed=77)
+    for r in range(4):
+        params = dataclasses.replace(base, top_p=tps[r])
+        g = _run(cuda, x[r:r + 1], params, u[r:r + 1], cap=256, split=split)
+        assert g["path"][0] & PATH_TOKEN_ONLY, f"row {r}: path {g['path'][0]:#x}"
+        _check_oracle(x[r:r + 1], params, u[r:r + 1], g)
