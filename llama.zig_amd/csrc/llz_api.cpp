@@ -227,7 +227,7 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   if (n_prev > 0 && !d_prev_tokens) return LLZ_E_INVALID_ARG;
   if (extras && (extras->d_kept_ids || extras->d_kept_probs) && extras->kept_cap <= 0)
     return LLZ_E_INVALID_ARG;
-  if (rows >= (1 << 24)) return LLZ_E_INVALID_ARG;  // the row-claim counter's width
+  if (rows > (1 << 24) - 1024) return LLZ_E_INVALID_ARG;  // the row-claim counter's width (rows + grid claims)
   hipStream_t st = (hipStream_t)stream;
   const uint32_t xb = post_bits(post);
   const float cap = (xb & kXfCap) ? post->final_logit_softcapping : 0.0f;
@@ -283,8 +283,10 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   P.kept_cap = extras ? extras->kept_cap : 0;
   P.src_stride = src_stride;
   P.orig_stride = row_stride;
-  // the token alone: no probabilities and no row statistics asked for, and no
-  // typical-p (its entropy needs the exact normaliser).  The token path's list
+  // the token alone: no probabilities and no row statistics asked for.  With
+  // typical-p, k_stats's token path orders the kept terms by their distance
+  // to an interval of the reference's entropy (rows it cannot decide take the
+  // exact phases); split rows do not take typical-p.  The token path's list
   // holds the terms e >= tok_theta: min-p's candidate threshold when it is at
   // least 2^-10; without min-p (the reference's default chain), 2^-10 with
   // top-p, whose cut must then fall inside the list.  Below 2^-10 the list
@@ -294,8 +296,8 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   const bool tok_topp = !tok_minp && !(cfg->min_p > 0.0f) && cfg->top_p > 0.0f && cfg->top_p < 1.0f &&
                         vocab > kCandCap;
   P.tok_theta = tok_minp ? P.cand_theta : (tok_topp ? 0x1p-10f : 0.0f);
-  const bool tok_only = !(extras && (extras->d_kept_probs || extras->d_row_stats)) &&
-                        !(cfg->typical_p > 0.0f && cfg->typical_p < 1.0f) && (tok_minp || tok_topp);
+  const bool typical_on = cfg->typical_p > 0.0f && cfg->typical_p < 1.0f;
+  const bool tok_only = !(extras && (extras->d_kept_probs || extras->d_row_stats)) && (tok_minp || tok_topp);
   P.flags = (cfg->temperature == 1.0f ? kFlagTIsOne : 0u) | (vec ? kFlagVecSrc : 0u) | kFlagFallback |
             (tok_only ? kFlagTokenOnly : 0u);
   P.xf_src = xf_src;
@@ -344,7 +346,7 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   // Rows read through post-processing or the fused penalty take chunks of at
   // most 2 float4 per thread: each logit's exact transform is then a few per
   // thread (calls of up to 8 rows at 128k vocab).
-  if (split_room && tok_only && vec && vocab % 4 == 0 && P.tok_theta > 0.0f && P.l2e_t > 0.0f &&
+  if (split_room && tok_only && !typical_on && vec && vocab % 4 == 0 && P.tok_theta > 0.0f && P.l2e_t > 0.0f &&
       P.l2e_t <= 0x1p40f && g_split_mode.load(std::memory_order_relaxed) != 1) {
     const int cus = device_cus(st);
     const int nv_max = (xf_src | xb) != 0u ? 2 : kSplitNV;

@@ -81,7 +81,7 @@ struct SplitShared {
   uint32_t elected;   // this workgroup saw every chunk published (then: took the row's full path)
   // the merge
   uint64_t tl[2 * kTokCap];  // collected, then sorted
-  uint16_t part[kSplitW * kTokCap];
+  uint8_t part[kSplitW * kTokCap];
   uint32_t ncv[kSplitMax];   // per chunk: its list entries that may pass (0: none)
   uint32_t tcand, tfail, bad;
   float m, s_est, w_est;
@@ -468,7 +468,7 @@ __device__ __forceinline__ bool split_merge(const KArgs& A, int row, SplitShared
     ok = tc <= kTokCap;
     if (ok) {
       token_sort(S.tl, S.tl + kTokCap, S.part, tc);
-      if (w == 0) token_select(kernel_args_ptr(), row, S.tl + kTokCap, tc, S.s_est, S.w_est, u_row, theta, &S.tfail);
+      if (w == 0) token_select(kernel_args_ptr(), row, S.tl + kTokCap, tc, S.s_est, S.w_est, 0.0, -1.0, u_row, theta, &S.tfail);
       lds_barrier();
       LLZ_STAMP(sr, 10);
       ok = S.tfail == 0u;

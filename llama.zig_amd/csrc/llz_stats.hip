@@ -512,15 +512,26 @@ union StatsShared {
 // The next row beyond the grid for a workgroup that finished one: a counter
 // word tagged with the low 40 bits of the call's epoch (a word left by
 // another call, or not yet written, counts as 0 for this one).  Returns grid +
-// the count before the claim (>= rows: nothing left).
+// the count before the claim (>= rows: nothing left).  The first claim of a
+// call installs its tag (compare-and-swap); every later one is a single
+// fetch-and-add, which the device serves back to back, where a
+// compare-and-swap loop lets one claim through per round trip to memory
+// (with rows of some 40 us, the workgroups then queued for their claims).
+// The count stays below 2^24: at most rows + grid claims.
 __device__ __noinline__ int claim_row(unsigned long long* word, unsigned long long epoch, int grid) {
+  constexpr unsigned long long kCnt = (1ull << 24) - 1;
   const unsigned long long tag = (epoch & ((1ull << 40) - 1)) << 24;
   unsigned long long old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (;;) {
-    const unsigned long long cnt = (old & ~((1ull << 24) - 1)) == tag ? (old & ((1ull << 24) - 1)) : 0ull;
-    const unsigned long long seen = atomicCAS(word, old, tag | (cnt + 1));
-    if (seen == old) return grid + (int)cnt;
-    old = seen;
+    if ((old & ~kCnt) == tag) {
+      const unsigned long long prev = __hip_atomic_fetch_add(word, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return grid + (int)(prev & kCnt);
+    }
+    unsigned long long expected = old;
+    if (__hip_atomic_compare_exchange_strong(word, &expected, tag | 1ull, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT))
+      return grid;
+    old = expected;
   }
 }
 
@@ -1030,6 +1041,41 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       s_est += G > i ? F.qsum[i] * ri : 0.0f;
       w_est += G > i ? F.qwsum[i] * ri : 0.0f;
     }
+    const bool typ = P.typical_p > 0.0f && P.typical_p < 1.0f;
+    if (!tbad && typ) {
+      // typical-p (sampler.zig:128-132): this wave's part of sum_i e_i log2
+      // e_i, from its estimates (e_i ~ q_i R_w, log2 e_i ~ log2 q_i + aw),
+      // and the sum of the parts' magnitudes for the error bound.  Every
+      // position outside the row or the wave's segments has q = 0; the
+      // segments past the wave's last are not read
+      const float aw = fmaf(m, -l2e_t, cw);
+      float sx = 0.0f, sa = 0.0f;
+      auto acc = [&](float q) {
+        const float y = q >= 0x1p-100f ? q * (__builtin_amdgcn_logf(q) + aw) : 0.0f;
+        sx += y;
+        sa += fabsf(y);
+      };
+#pragma unroll
+      for (int k = 0; k < KV; ++k) {
+        acc(d[k].x);
+        acc(d[k].y);
+        acc(d[k].z);
+        acc(d[k].w);
+      }
+      for (int i = 0; i < KL && KV + i < nseg_w; ++i) {
+        const float4 q = *reinterpret_cast<const float4*>(&F.u.data[w][i][lane * 4]);
+        acc(q.x);
+        acc(q.y);
+        acc(q.z);
+        acc(q.w);
+      }
+      sx = wave_sum_f32(sx);
+      sa = wave_sum_f32(sa);
+      if (lane == 0) {
+        F.tx[w] = sx;
+        F.txa[w] = sa;
+      }
+    }
     if (!tbad) {
       const float Rw_t = __builtin_amdgcn_exp2f(fmaf(m, -l2e_t, cw));
       const float theta_t = P.tok_theta;
@@ -1152,10 +1198,15 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       LLZ_STAMP(row, 33);
       const int tc = (int)F.tcand;
       if (tc <= kTokCap && F.tfail == 0u) {
-        static_assert(sizeof(F.qpos) >= (size_t)(kNT / kWave) * kTokCap * sizeof(uint16_t), "partial ranks fit the queue rows");
-        token_sort(tl, tl + kTokCap, reinterpret_cast<uint16_t*>(&F.qpos[0][0]), tc);
+        static_assert(sizeof(F.qpos) >= (size_t)(kNT / kWave) * kTokCap * sizeof(uint8_t), "partial ranks fit the queue rows");
+        static_assert(sizeof(F.v) >= 2 * kTokCap * sizeof(uint64_t), "the list and its sorted copy fit F.v");
+        token_sort(tl, tl + kTokCap, reinterpret_cast<uint8_t*>(&F.qpos[0][0]), tc);
         LLZ_STAMP(row, 34);
-        if (w == 0) token_select(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, w_est, u_row, theta_t, &F.tfail);
+        if (w == 0) {
+          double hs_lo = 0.0, hs_hi = -1.0;  // the row's entropy (typical-p rows)
+          if (typ) entropy_star(P, F.tx, F.txa, F.qsum, F.cw, W, G, m, s_est, &hs_lo, &hs_hi);
+          token_select(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, w_est, hs_lo, hs_hi, u_row, theta_t, &F.tfail);
+        }
       } else if (t == 0) {
         F.tfail = 1u;
       }

@@ -34,14 +34,15 @@
 
 namespace llz {
 
-constexpr int kTokCap = 256;  // candidates of a token-only row at most
+constexpr int kTokCap = 512;  // candidates of a token-only row at most
 
 // Rank sort of c <= kTokCap distinct keys (e desc as ~bits, id asc) for
 // wave 0: wave w counts, for every key, the keys of its eighth of the list
-// below it (part[w][i], no clearing needed); after one barrier wave 0 adds
-// the eight counts and places each key.  Only wave 0 reads `out` (in LDS
-// order after its own writes).
-__device__ __forceinline__ void token_sort(const uint64_t* in, uint64_t* out, uint16_t* part, int c) {
+// below it (part[w][i], at most kTokCap / 8 = 64: one byte, no clearing
+// needed); after one barrier wave 0 adds the eight counts and places each
+// key.  Only wave 0 reads `out` (in LDS order after its own writes).
+__device__ __forceinline__ void token_sort(const uint64_t* in, uint64_t* out, uint8_t* part, int c) {
+  static_assert(kTokCap / (kNT / kWave) <= 255, "partial ranks fit a byte");
   constexpr int NW = kNT / kWave;
   const int lane = lane_id(), w = wave_id();
   const int j0 = (w * c) / NW, j1 = ((w + 1) * c) / NW;
@@ -49,7 +50,7 @@ __device__ __forceinline__ void token_sort(const uint64_t* in, uint64_t* out, ui
     const uint64_t ki = in[i];
     uint32_t r = 0;
     for (int j = j0; j < j1; ++j) r += in[j] < ki ? 1u : 0u;
-    part[w * kTokCap + i] = (uint16_t)r;
+    part[w * kTokCap + i] = (uint8_t)r;
   }
   lds_barrier();
   if (w == 0) {
@@ -91,16 +92,62 @@ __device__ __forceinline__ double wave_incl_scan_f64(double x) {
   return s;
 }
 
+// Typical-p on the token path (sampler.zig:128-154).  The entropy is that
+// of the row's terms e_i <= 1 (their real sum S):
+//   H* = ln S - (1/S) sum_i e_i ln e_i = ln 2 (log2 S - Y / S),
+//   Y = sum_i e_i log2 e_i <= 0.
+// Each wave sums q (log2 q + aw) over its estimates (q R_w = e (1 + d),
+// |d| <= de = 2^-14 + est_xe, R_w = exp2(aw)), with the hardware log2 (within
+// 2^-18 max(1, |log2 q|) of log2 q) and the magnitudes of those terms (A_w).
+// Per element, with the computed term's roundings (one for the sum in the
+// brackets, one for the product, about 260 for the lane's and the wave's
+// sums), the distance to e log2 e is within de e |log2 e| + e (1.5 de +
+// 2^-17.9 (1 + |log2 e| + |aw|)) + 2^-15 |term|, so |Y - sum_w R_w X_w| <=
+// sum_w R_w (A_w (de + 2^-14.47) + Q_w (1.5 de + 2^-14.47 (1 + |aw|)))
+// (Q_w: the wave's sum of q), widened by 2^-8 of itself for the use of the
+// estimates in place of the terms; terms with q < 2^-100 are left out (far
+// below 2^-60 in all).  S lies within s_est / (1 +- de).
+__device__ __forceinline__ void entropy_star(const RowParams& P, const float* tx, const float* txa, const float* qsum,
+                                          const float* cwv, int nw, int G, float m, float s_est, double* lo,
+                                          double* hi) {
+  const double de = 0x1p-14 + (double)P.est_xe;
+  double X = 0.0, B = 0.0;
+  for (int i = 0; i < nw; ++i) {
+    if (G > i) {
+      const float awi = fmaf(m, -P.l2e_t, cwv[i]);
+      const double ri = (double)__builtin_amdgcn_exp2f(awi);
+      X += ri * (double)tx[i];
+      B += ri * ((double)txa[i] * (de + 0x1.7p-15) + (double)qsum[i] * (1.5 * de + 0x1.7p-15 * (1.0 + fabs((double)awi))));
+    }
+  }
+  const double EY = B * (1.0 + 0x1p-8) + fabs(X) * 0x1p-40 + 0x1p-60;
+  const double Smin = (double)s_est / (1.0 + de) * (1.0 - 0x1p-50), Smax = (double)s_est / (1.0 - de) * (1.0 + 0x1p-50);
+  const double Nlo = -X - EY, Nhi = -X + EY;  // -Y lies in [Nlo, Nhi]
+  const double Alo = log2(Smin) + (Nlo >= 0.0 ? Nlo / Smax : Nlo / Smin);
+  const double Ahi = log2(Smax) + (Nhi >= 0.0 ? Nhi / Smin : Nhi / Smax);
+  const double ln2 = 0.69314718055994530942;
+  *lo = ln2 * Alo - 0x1p-40 * (fabs(Alo) + 1.0);
+  *hi = ln2 * Ahi + 0x1p-40 * (fabs(Ahi) + 1.0);
+  if (!(Smin > 0.0) || !(*lo <= *hi) || !(fabs(*hi) < 1.0e30)) {
+    *lo = 0.0;
+    *hi = -1.0;
+  }
+}
+
 // Wave 0: the chain's decisions (sampler.zig:100-168) for a token-only row
 // from its candidates srt[0, c), sorted (e desc, id asc) -- every term e >=
 // theta, all of them exact -- and the estimate s_est of the normaliser
-// (w_est: of sum_j e_j (n - j), an upper bound's estimate; 0: unknown).
-// Writes the token, the draw flag, the kept count and ids; sets *tfail
-// instead when a decision does not hold over the interval of S.
+// (w_est: of sum_j e_j (n - j), an upper bound's estimate; 0: unknown), and
+// for typical-p the interval [hs_lo, hs_hi] of the row's entropy H*
+// (entropy_star; empty: unknown, and then only rows that keep nothing
+// before typical-p are decided).  Writes the token, the draw flag, the kept
+// count and ids; sets *tfail instead when a decision does not hold over the
+// intervals.
 // Out of line; the launch's arguments come through the kernel's argument
 // segment (as the other out-of-line paths take them).
 __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint64_t* srt, int c, float s_est,
-                                          float w_est, float u, float theta, uint32_t* tfail) {
+                                          float w_est, double hs_lo, double hs_hi, float u, float theta,
+                                          uint32_t* tfail) {
   const RowParams& P = A->P;
   const RowPtrs& Q = A->Q;
   const int lane = lane_id();
@@ -201,37 +248,137 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   if (open_end && cut < 0) ok = false;  // the kept prefix may reach past the list
   const int K = cut >= 0 ? min(L, cut) : L;
   LLZ_STAMP(row, 36);
-  uint32_t token = c >= 1 ? readlane_u32((uint32_t)k0, 0) : 0u, consumed = 0;  // indices[0]
-  if (ok && K > 0) {
-    // total and draw (sampler.zig:156-168): E = C_{K-1}; the draw stops at
-    // the first q with u E - C_q below -margin (none of them within it)
-    double E;
-    if (K <= kWave) {
-      E = readlane_f64(C0, K - 1);
-    } else {
-      E = 0.0;
-      for (int b = 0; b < K; b += kWave) {
-        const int q = b + lane;
-        E += readlane_f64(wave_incl_scan_f64(q < K ? (double)e_at(q) : 0.0), kWave - 1);
-      }
+  // C_j = e_0 + ... + e_j for j < K (exact in double: at most kTokCap f32
+  // terms in [theta, 1], theta >= 2^-11)
+  auto prefix = [&](int j) -> double {
+    if (j < kWave) return readlane_f64(C0, j);
+    double acc = 0.0;
+    for (int b = 0; b <= j; b += kWave) {
+      const int q = b + lane;
+      acc += readlane_f64(wave_incl_scan_f64(q <= j ? (double)e_at(q) : 0.0), kWave - 1);
     }
+    return acc;
+  };
+  // typical-p (sampler.zig:128-154) over the kept positions [0, K); the
+  // positions kept after it are [a, b)
+  int a = 0, b = K;
+  if (ok && K > 0 && P.typical_p > 0.0f && P.typical_p < 1.0f) {
+    // The reference's entropy H^ (sampler.zig:129-132): the sequential sum of
+    // t_i = -RN(p_i logf(p_i)), p_i = RN(e_i / S^).  With pi_i = e_i / S^ and
+    // h_i = -pi_i ln pi_i, |t_i - h_i| <= 2^-21.9 h_i + 2^-23.9 pi_i (p's,
+    // logf's and the product's roundings); sum_i h_i = c (H* - ln c), c = S /
+    // S^ in [1 / (1 + rs), 1 / (1 - rs)]; the sum's roundings add
+    // gamma_{n-1} of it (all t_i >= 0).
+    bool known = hs_lo <= hs_hi;
+    const double c_lo = 1.0 / (1.0 + rs), c_hi = 1.0 / (1.0 - rs);
+    const double kap = c_hi * fmax(fabs(log(c_lo)), fabs(log(c_hi)));
+    const double sh_lo = fmin(c_lo * hs_lo, c_hi * hs_lo) - kap, sh_hi = fmax(c_lo * hs_hi, c_hi * hs_hi) + kap;
+    const double t_lo = sh_lo - fabs(sh_lo) * 0x1.2p-22 - 0x1.2p-24 * c_hi - 0x1p-100;
+    const double t_hi = sh_hi + fabs(sh_hi) * 0x1.2p-22 + 0x1.2p-24 * c_hi + 0x1p-100;
+    const double gn1 = (double)(n - 1) * 0x1p-24;
+    const double gH = gn1 / (1.0 - gn1) * (1.0 + 0x1p-40);
+    const double H_lo = t_lo - fabs(t_lo) * gH, H_hi = t_hi + fabs(t_hi) * gH;
+    known = known && gn1 < 0.5;
+    // surprises s_j = -logf(p_j) (sampler.zig:140): -ln p_j lies within
+    // ln S^ - ln e_j +- 1.01 2^-24, logf within 2^-23 of ln; s_j grows with j
+    const double u24 = 0x1p-24;
+    const double le0 = log((double)e_of(srt[0])), leK = log((double)e_of(srt[K - 1]));
+    const double lSlo = log(S_lo), lShi = log(S_hi);
+    const double s0_lo = (lSlo - le0 - 1.01 * u24) * (1.0 - 0x1p-23) - 0x1p-45 * (fabs(lSlo) + fabs(le0) + 1.0);
+    const double sK_hi = (lShi - leK + 1.01 * u24) * (1.0 + 0x1p-23) + 0x1p-45 * (fabs(lShi) + fabs(leK) + 1.0);
+    // every kept surprise below the entropy (dev_j = H^ - s_j: the typical
+    // order is positions K-1 .. 0) or every one above it (dev_j = s_j - H^:
+    // positions 0 .. K-1), whatever S^ and H^ in their intervals
+    const bool below = known && sK_hi < H_lo;
+    const bool above = known && s0_lo > H_hi;
+    if (!below && !above) ok = false;
+    // no two kept devs round to one float (a tie would take the lower id
+    // first): adjacent terms apart by mu relative put their surprises more
+    // than 2^-21 max dev apart
+    const double mu = 0x1p-20 * (fmax(H_hi, sK_hi) + sK_hi + 1.0);
+    for (int bb = 0; bb < K - 1 && ok; bb += kWave) {
+      const int q = bb + lane;
+      const bool bad = q < K - 1 && !((double)e_at(q) > (double)e_next(q) * (1.0 + mu));
+      if (bal64(bad) != 0ull) ok = false;
+    }
+    // the cut (sampler.zig:148-153): the running sum of p over the kept
+    // terms in the typical order, within (2r + 4) 2^-24 of the terms' sum /
+    // S^ after r of them, against typical_p; the term that takes it over and
+    // every later one are dropped
+    const double tp = (double)P.typical_p;
+    if (ok && above) {
+      double carry = 0.0;
+      int bc = -1;
+      for (int bb = 0; bb < K && ok && bc < 0; bb += kWave) {
+        const int q = bb + lane;
+        const double C = carry + wave_incl_scan_f64(q < K ? (double)e_at(q) : 0.0);
+        const double rel = (2.0 * q + 4.0) * u24;
+        const bool lo_over = q < K && C * iS_hi * (1.0 - rel) > tp;
+        const bool hi_over = q < K && C * iS_lo * (1.0 + rel) > tp;
+        const uint64_t mh = bal64(hi_over);
+        if (mh != 0ull) {
+          const int fq = __ffsll((long long)mh) - 1;
+          if ((bal64(lo_over) >> fq) & 1ull)
+            bc = bb + fq;
+          else
+            ok = false;
+        }
+        carry = readlane_f64(C, kWave - 1);
+      }
+      b = bc >= 0 ? bc : K;
+    } else if (ok) {
+      // positions K-1 .. j hold D_j = E_K - C_j + e_j; the last position
+      // whose sum may exceed typical_p is where the cut falls
+      const double EK = prefix(K - 1);
+      double carry = 0.0;
+      int jh = -1;
+      bool jlo = false;
+      for (int bb = 0; bb < K; bb += kWave) {
+        const int q = bb + lane;
+        const double eq = q < K ? (double)e_at(q) : 0.0;
+        const double C = carry + wave_incl_scan_f64(eq);
+        const double D = EK - C + eq;
+        const double rel = (2.0 * (K - q) + 4.0) * u24;
+        const bool hi_over = q < K && D * iS_lo * (1.0 + rel) > tp;
+        const bool lo_over = q < K && D * iS_hi * (1.0 - rel) > tp;
+        const uint64_t mh = bal64(hi_over);
+        if (mh != 0ull) {
+          const int fq = 63 - __clzll((long long)mh);
+          jh = bb + fq;
+          jlo = ((bal64(lo_over) >> fq) & 1ull) != 0ull;
+        }
+        carry = readlane_f64(C, kWave - 1);
+      }
+      if (jh >= 0 && !jlo) ok = false;
+      a = jh + 1;
+    }
+  }
+  const int Kp = b - a;  // the kept count
+  uint32_t token = c >= 1 ? readlane_u32((uint32_t)k0, 0) : 0u, consumed = 0;  // indices[0]
+  if (ok && Kp > 0) {
+    // total and draw (sampler.zig:156-168) over positions [a, b): E = C_{b-1}
+    // - C_{a-1}; the draw stops at the first q with u E - (C_q - C_{a-1})
+    // below -margin (none of them within it)
+    const double Ca = a > 0 ? prefix(a - 1) : 0.0;
+    const double E = prefix(b - 1) - Ca;
     const double Au = (double)u * E;
-    const double margin = (4.0 * K + 16.0) * 0x1p-24 * E;
+    const double margin = (4.0 * Kp + 16.0) * 0x1p-24 * E;
     int st = -1;
     double dcarry = 0.0;
-    for (int b = 0; b < K && st < 0 && ok; b += kWave) {
-      const int q = b + lane;
-      const double C = b == 0 ? C0 : dcarry + wave_incl_scan_f64(q < K ? (double)e_at(q) : 0.0);
-      const double dq = Au - C;
-      const bool unc = q < K && fabs(dq) <= margin;
-      const bool stp = q < K && dq < -margin;
+    for (int bb = 0; bb < b && st < 0 && ok; bb += kWave) {
+      const int q = bb + lane;
+      const double C = bb == 0 ? C0 : dcarry + wave_incl_scan_f64(q < K ? (double)e_at(q) : 0.0);
+      const double dq = Au - (C - Ca);
+      const bool in = q >= a && q < b;
+      const bool unc = in && fabs(dq) <= margin;
+      const bool stp = in && dq < -margin;
       const uint64_t mk = bal64(unc || stp);
       if (mk != 0ull) {
         const int fq = __ffsll((long long)mk) - 1;
         if ((bal64(unc) >> fq) & 1ull)
           ok = false;
         else
-          st = b + fq;
+          st = bb + fq;
       }
       dcarry = readlane_f64(C, kWave - 1);
     }
@@ -244,12 +391,12 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
     return;
   }
   if (Q.kept_ids)
-    for (int q = lane; q < K && q < P.kept_cap; q += kWave)
-      Q.kept_ids[(int64_t)row * P.kept_cap + q] = q < kWave ? (uint32_t)k0 : id_at(q);
+    for (int q = lane; q < Kp && q < P.kept_cap; q += kWave)
+      Q.kept_ids[(int64_t)row * P.kept_cap + q] = (a == 0 && q < kWave) ? (uint32_t)k0 : id_at(a + q);
   if (lane == 0) {
     Q.tokens[row] = token;
     if (Q.consumed) Q.consumed[row] = (uint8_t)consumed;
-    if (Q.kept_count) Q.kept_count[row] = (uint32_t)K;
+    if (Q.kept_count) Q.kept_count[row] = (uint32_t)Kp;
     if (Q.status) Q.status[row] = kPathTokenOnly;
   }
 }

@@ -8,6 +8,9 @@
   that keep something) and the kept total, bit for bit.
 * Configuration 2's 64 rows in a token-only call (the benchmark's call):
   token, draw flag, kept count and kept ids, every row on the token path.
+* Configuration 5's 4,096 rows in a token-only call (the benchmark's call,
+  typical-p decided on the token path): token, draw flag and kept count of
+  every row, kept ids of every eighth.
 
 Parity over the batch is the bar, whatever path each row takes.
 """
@@ -90,3 +93,36 @@ def test_c2_full_batch_token_only(cuda):
         assert (tok[r], con[r], kept[r]) == (o.token, o.consumed, o.kept_count), f"row {r}"
         k = min(o.kept_count, cap)
         assert np.array_equal(ids[r, :k], o.kept_ids()[:k]), f"row {r}: kept ids"
+
+
+def test_c5_full_batch_token_only(cuda):
+    import torch
+
+    w = WORKLOADS["c5"]
+    x = w.logits(w.rows)
+    u = llz.rng_uniforms(w.uniform_seed, w.rows)
+    cfg = llz.SamplerConfig.of(w.params)
+    cap = 64
+    print(f"c5 token-only: {w.rows} x {w.vocab}", flush=True)
+    res = llz.sample_rows(torch.from_numpy(x).to(cuda), cfg, torch.from_numpy(u).to(cuda), kept_cap=cap,
+                          probs=False, path=True)
+    torch.cuda.synchronize()
+    tok = res.tokens.cpu().numpy().view(np.uint32)
+    con = res.consumed.cpu().numpy()
+    kept = res.kept_count.cpu().numpy().view(np.uint32)
+    ids = res.kept_ids.cpu().numpy().view(np.uint32)
+    path = res.row_path.cpu().numpy().view(np.uint32)
+    del res
+    torch.cuda.empty_cache()
+    ot, oc, ok = O.sample_rows(x, w.params, u, threads=HOST_THREADS)
+    for what, a, b in (("token", tok, ot), ("draw flag", con, oc), ("kept count", kept, ok)):
+        bad = np.flatnonzero(a != b)
+        assert bad.size == 0, f"c5: {bad.size} rows differ in {what}; first row {bad[0]} (path {path[bad[0]]:#x})"
+    for r in range(0, w.rows, 8):
+        o = O.sample_row(x[r], w.params, u[r])
+        k = min(o.kept_count, cap)
+        assert np.array_equal(ids[r, :k], o.kept_ids()[:k]), f"row {r} (path {path[r]:#x}): kept ids"
+    # the rows off the token path: N(0, 2) rows with more than 512 terms above
+    # min-p's threshold (about one in nine rows)
+    on_tok = (path & PATH_TOKEN_ONLY) != 0
+    assert on_tok.mean() >= 0.85, f"{int((~on_tok).sum())} rows off the token path"

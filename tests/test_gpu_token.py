@@ -21,6 +21,7 @@ from llz.workloads import WORKLOADS
 pytestmark = pytest.mark.gpu
 
 PATH_TOKEN_ONLY = 128
+PATH_SPLIT = 1 << 17
 
 
 def _run(cuda, x, params, u, stats=False, cap=64):
@@ -210,8 +211,8 @@ def test_token_only_kept_ids_without_cap(cuda):
 @pytest.mark.parametrize("kind", ["flat", "many"])
 def test_token_only_overflow_falls_back(cuda, kind):
     """Min-p rows whose candidates overflow the token path: a flat row (its
-    candidate lanes overflow every wave's queue) and 300 terms near the
-    maximum over a low floor (the lanes fit, the 256-entry list does not).
+    candidate lanes overflow every wave's queue) and 600 terms near the
+    maximum over a low floor (the lanes fit, the 512-entry list does not).
     The exact phases follow, with the oracle's results."""
     w = WORKLOADS["headline"]
     rows = 4
@@ -219,13 +220,38 @@ def test_token_only_overflow_falls_back(cuda, kind):
     if kind == "flat":
         x = rng.normal(0.0, 0.3, size=(rows, w.vocab)).astype(np.float32)
     else:
-        x = rng.normal(-30.0, 1.0, size=(rows, w.vocab)).astype(np.float32)
-        for r in range(rows):
-            idx = rng.choice(w.vocab, 300, replace=False)
-            x[r, idx] = rng.uniform(-1.0, 0.0, 300).astype(np.float32)
+        x = _many_near_max(rng, rows, w.vocab, 600)
     u = llz.rng_uniforms(w.uniform_seed, rows)
     g = _run(cuda, x, w.params, u, cap=256)
     assert not np.any(g["path"] & PATH_TOKEN_ONLY)
+    _check_oracle(x, w.params, u, g)
+
+
+def _many_near_max(rng, rows, n, k):
+    x = rng.normal(-30.0, 1.0, size=(rows, n)).astype(np.float32)
+    for r in range(rows):
+        idx = rng.choice(n, k, replace=False)
+        x[r, idx] = rng.uniform(-1.0, 0.0, k).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_token_only_long_list(cuda, split):
+    """300 terms near the maximum over a low floor: a list between 256 and
+    512 terms (rank sort with two keys a lane and up to 38 a wave's eighth),
+    decided on the token path, with one workgroup per row or split rows."""
+    w = WORKLOADS["headline"]
+    rows = 4
+    x = _many_near_max(np.random.default_rng(7), rows, w.vocab, 300)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    if not split:
+        llz.debug_set_split(1)
+    try:
+        g = _run(cuda, x, w.params, u, cap=256)
+    finally:
+        llz.debug_set_split(0)
+    assert np.all(g["path"] & PATH_TOKEN_ONLY)
+    assert np.all(((g["path"] & PATH_SPLIT) != 0) == split)
     _check_oracle(x, w.params, u, g)
 
 
@@ -249,3 +275,42 @@ def test_token_only_wave_with_many_candidates(cuda):
     g = _run(cuda, x, w.params, u)
     assert np.all(g["path"] & PATH_TOKEN_ONLY), f"rows off the token path: {g['path']}"
     _check_oracle(x, w.params, u, g)
+
+
+def test_token_only_typical_rows(cuda):
+    """Typical-p on the token path (configuration 5: top-k 50, top-p 0.9,
+    min-p 0.02, typical-p 0.98): the kept terms in the order of their
+    distance to an interval of the row's entropy, every decision checked over
+    the intervals.  Every row against the oracle; the rows decide on the
+    token path (the N(0, 2) rows' kept surprises lie far below their entropy,
+    the peaked rows keep nothing before typical-p)."""
+    w = WORKLOADS["c5"]
+    rows = 64
+    x = w.logits(rows)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    g = _run(cuda, x, w.params, u)
+    _check_oracle(x, w.params, u, g)
+    tok = (g["path"] & PATH_TOKEN_ONLY) != 0
+    assert tok.mean() >= 0.9, f"{int((~tok).sum())} rows took the exact phases"
+
+
+def test_token_only_typical_entropy_among_kept_falls_back(cuda):
+    """Rows whose entropy lies among the kept terms' surprises (30 tokens near
+    +10 over N(0, 1) logits): their typical order depends on the exact
+    entropy, so they take the exact phases.  Every row against the oracle."""
+    rng = np.random.default_rng(7)
+    rows, n = 8, 32768
+    x = rng.normal(0.0, 1.0, (rows, n)).astype(np.float32)
+    for r in range(rows):
+        ids = rng.choice(n, 30, replace=False)
+        x[r, ids] = (10.0 + rng.normal(0.0, 0.5, 30)).astype(np.float32)
+    params = WORKLOADS["c5"].params
+    u = llz.rng_uniforms(5, rows)
+    g = _run(cuda, x, params, u)
+    _check_oracle(x, params, u, g)
+    # the premise, from the oracle: the entropy lies inside the kept surprises
+    for r in range(rows):
+        o = O.sample_row(x[r], params, u[r])
+        s = -np.log(o.probs[o.order[:20]].astype(np.float64))
+        assert s.min() < o.entropy < s.max()
+    assert np.all((g["path"] & PATH_TOKEN_ONLY) == 0)
