@@ -151,6 +151,7 @@ struct FastShared {
   float qsum[fastp::W];  // token-only rows: per wave, the sum of its estimates q
   float tx[fastp::W];    // token-only typical-p rows: per wave, sum of q (log2 q + aw)
   float txa[fastp::W];   //   and of its terms' magnitudes
+  float theta2;          // token-only rows: the threshold of a list collected again
   float qwsum[fastp::W];  // token-only rows: per wave, its segments' sums of q times n - their first position
   uint32_t tcand; // token-only rows: candidates collected
   uint32_t tfail; // token-only rows: not certified (the exact phases follow)

@@ -1078,13 +1078,20 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     }
     if (!tbad) {
       const float Rw_t = __builtin_amdgcn_exp2f(fmaf(m, -l2e_t, cw));
-      const float theta_t = P.tok_theta;
+      uint64_t* const tl = reinterpret_cast<uint64_t*>(&F.v);  // [kTokCap] collected, then [kTokCap] sorted
+      static_assert(sizeof(F.qpos) >= (size_t)(kNT / kWave) * kTokCap * sizeof(uint8_t), "partial ranks fit the queue rows");
+      static_assert(sizeof(F.v) >= 2 * kTokCap * sizeof(uint64_t), "the list and its sorted copy fit F.v");
+      // Round 0 collects the terms e >= tok_theta.  A list that overflows
+      // under a top-k of at most kTokCap / 4 is collected again (round 1)
+      // above theta2: just below the (top_k + 1)-th largest of the terms
+      // collected (a subset's order statistic, at most the row's), so the
+      // top_k + 1 largest terms lie clear above it
+      auto collect = [&](const float theta_t) {
       const float thr_e = theta_t * (1.0f - 0x1p-10f);
       if (tq < 0) tq = tqueue(Rw_t, thr_e);
       LLZ_STAMP(row, 39);
       LLZ_STAMP(row, 32);
       if (tq > QCAP && lane == 0) atomicOr(&F.tfail, 1u);
-      uint64_t* const tl = reinterpret_cast<uint64_t*>(&F.v);  // [kTokCap] collected, then [kTokCap] sorted
       // The queued lanes' elements that may be candidates: the lane test
       // (tqueue against the row's maximum) element by element, on the same
       // estimates exp2(fma(v, l2e_t, -cw)) phase L computed.  When a wave
@@ -1196,10 +1203,25 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       }
       lds_barrier();  // the list complete (LDS only: the re-reads were consumed above)
       LLZ_STAMP(row, 33);
+      };
+      collect(P.tok_theta);
+      float theta_t = P.tok_theta;
+      const uint32_t kk = P.top_k;
+      if (F.tcand > (uint32_t)kTokCap && F.tfail == 0u && kk >= 1u && kk <= (uint32_t)(kTokCap / 4) &&
+          kk < (uint32_t)n) {
+        token_sort(tl, tl + kTokCap, reinterpret_cast<uint8_t*>(&F.qpos[0][0]), kTokCap);
+        if (t == 0) {  // wave 0 placed the sorted keys
+          const float e1 = __uint_as_float(~(uint32_t)(tl[kTokCap + kk] >> 32));
+          F.theta2 = fmaxf(e1 * (1.0f - 0x1p-19f), P.tok_theta);
+          F.tcand = 0u;
+        }
+        lds_barrier();
+        theta_t = F.theta2;
+        tq = -1;
+        collect(theta_t);
+      }
       const int tc = (int)F.tcand;
       if (tc <= kTokCap && F.tfail == 0u) {
-        static_assert(sizeof(F.qpos) >= (size_t)(kNT / kWave) * kTokCap * sizeof(uint8_t), "partial ranks fit the queue rows");
-        static_assert(sizeof(F.v) >= 2 * kTokCap * sizeof(uint64_t), "the list and its sorted copy fit F.v");
         token_sort(tl, tl + kTokCap, reinterpret_cast<uint8_t*>(&F.qpos[0][0]), tc);
         LLZ_STAMP(row, 34);
         if (w == 0) {

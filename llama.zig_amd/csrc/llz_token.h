@@ -177,7 +177,11 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
     Km += __popcll(bal64(inM && e > mp_hi));
     if (mp && bal64(inM && !(e > mp_hi) && !(e < mp_lo)) != 0ull) ok = false;
   }
-  if (!mp) Km = n;
+  // a list collected again above theta > tok_theta (top-k) may leave out
+  // terms that pass min-p: when every certified term passes it, min-p's
+  // count is unknown beyond the list (the kept prefix then ends at top-k
+  // inside it, or at top-p's cut)
+  if (!mp || (theta > P.tok_theta && Km == M)) Km = n;
   LLZ_STAMP(row, 35);
   const int Kk = (P.top_k > 0 && P.top_k < (uint32_t)n) ? (int)P.top_k : n;
   const int L = min(Kk, Km);

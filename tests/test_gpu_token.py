@@ -212,19 +212,42 @@ def test_token_only_kept_ids_without_cap(cuda):
 def test_token_only_overflow_falls_back(cuda, kind):
     """Min-p rows whose candidates overflow the token path: a flat row (its
     candidate lanes overflow every wave's queue) and 600 terms near the
-    maximum over a low floor (the lanes fit, the 512-entry list does not).
-    The exact phases follow, with the oracle's results."""
+    maximum over a low floor without top-k (the lanes fit, the 512-entry list
+    does not, and no top-k lets it be collected again).  The exact phases
+    follow, with the oracle's results."""
     w = WORKLOADS["headline"]
     rows = 4
     rng = np.random.default_rng(7)
+    params = w.params
     if kind == "flat":
         x = rng.normal(0.0, 0.3, size=(rows, w.vocab)).astype(np.float32)
     else:
         x = _many_near_max(rng, rows, w.vocab, 600)
+        params = dataclasses.replace(params, top_k=0)
     u = llz.rng_uniforms(w.uniform_seed, rows)
-    g = _run(cuda, x, w.params, u, cap=256)
+    g = _run(cuda, x, params, u, cap=256)
     assert not np.any(g["path"] & PATH_TOKEN_ONLY)
+    _check_oracle(x, params, u, g)
+
+
+@pytest.mark.parametrize("terms", [600, 700])
+def test_token_only_list_collected_again(cuda, terms):
+    """Terms near the maximum over a low floor, more than the 512-entry list
+    holds, under top-k 40: the list is collected again above just below the
+    41st largest term collected, and the row decides on the token path (min-p's
+    count beyond the list unknown: top-k cuts inside it).  Every row against
+    the oracle."""
+    w = WORKLOADS["headline"]
+    rows = 4
+    x = _many_near_max(np.random.default_rng(11), rows, w.vocab, terms)
+    u = llz.rng_uniforms(w.uniform_seed, rows)
+    llz.debug_set_split(1)
+    try:
+        g = _run(cuda, x, w.params, u, cap=256)
+    finally:
+        llz.debug_set_split(0)
     _check_oracle(x, w.params, u, g)
+    assert np.all(g["path"] & PATH_TOKEN_ONLY)
 
 
 def _many_near_max(rng, rows, n, k):
