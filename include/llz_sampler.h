@@ -236,10 +236,12 @@ int llz_debug_math(const float *d_in, float *d_exp, float *d_log, float *d_expm1
 /* Test hook (no counterpart in the reference): the largest relative error,
  * in units of 2^-23, of the hardware exp2 (op 0), log2 (op 1) or reciprocal
  * (op 2) that the kernels' estimates use, over the `count` floats whose bit
- * patterns start at `first_bits`, against double precision.  Writes
+ * patterns start at `first_bits`, against double precision; op 3: the
+ * hardware log2's error relative to max(1, |log2 x|).  Writes
  * round-toward-zero(error * 2^20), saturated at 0xffffffff, to *d_max_err
  * (device memory, one u32, overwritten).  The estimates' error bounds assume
- * at most 1 unit (1 ulp) on the ranges the kernels evaluate. */
+ * at most 1 unit (1 ulp) for ops 0-2 on the ranges the kernels evaluate, and
+ * at most 32 units for op 3 (the token path's entropy estimate). */
 int llz_debug_hw_error(int32_t op, uint32_t first_bits, uint32_t count, uint32_t *d_max_err, void *stream);
 
 /* Measurement hook (no counterpart in the reference): while set, every

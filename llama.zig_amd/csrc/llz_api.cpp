@@ -286,7 +286,8 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   // the token alone: no probabilities and no row statistics asked for.  With
   // typical-p, k_stats's token path orders the kept terms by their distance
   // to an interval of the reference's entropy (rows it cannot decide take the
-  // exact phases); split rows do not take typical-p.  The token path's list
+  // exact phases); neither split rows nor soft-capped rows take it with
+  // typical-p.  The token path's list
   // holds the terms e >= tok_theta: min-p's candidate threshold when it is at
   // least 2^-10; without min-p (the reference's default chain), 2^-10 with
   // top-p, whose cut must then fall inside the list.  Below 2^-10 the list
@@ -297,7 +298,8 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
                         vocab > kCandCap;
   P.tok_theta = tok_minp ? P.cand_theta : (tok_topp ? 0x1p-10f : 0.0f);
   const bool typical_on = cfg->typical_p > 0.0f && cfg->typical_p < 1.0f;
-  const bool tok_only = !(extras && (extras->d_kept_probs || extras->d_row_stats)) && (tok_minp || tok_topp);
+  const bool tok_only = !(extras && (extras->d_kept_probs || extras->d_row_stats)) && (tok_minp || tok_topp) &&
+                        !(typical_on && (xf_src & kXfCap));
   P.flags = (cfg->temperature == 1.0f ? kFlagTIsOne : 0u) | (vec ? kFlagVecSrc : 0u) | kFlagFallback |
             (tok_only ? kFlagTokenOnly : 0u);
   P.xf_src = xf_src;
@@ -501,7 +503,7 @@ int llz_debug_math(const float* d_in, float* d_exp, float* d_log, float* d_expm1
 }
 
 int llz_debug_hw_error(int32_t op, uint32_t first_bits, uint32_t count, uint32_t* d_max_err, void* stream) {
-  if (!d_max_err || op < 0 || op > 2 || count == 0) return LLZ_E_INVALID_ARG;
+  if (!d_max_err || op < 0 || op > 3 || count == 0) return LLZ_E_INVALID_ARG;
   hipError_t e = launch_hw_error(op, first_bits, count, d_max_err, (hipStream_t)stream);
   return e == hipSuccess ? LLZ_OK : LLZ_E_HIP;
 }

@@ -91,7 +91,7 @@ __global__ __launch_bounds__(256) void k_math_probe(const float* __restrict__ in
 // k_hw_error: the largest relative error of the hardware exp2 (op 0), log2
 // (op 1) or reciprocal (op 2) over a range of float bit patterns, against
 // double precision, as error * 2^43 (units of 2^-23, times 2^20) folded into
-// *max_err.
+// *max_err; op 3: the log2's error relative to max(1, |log2 x|).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_hw_error(int op, uint32_t first, uint32_t count,
                                                   uint32_t* __restrict__ max_err) {
@@ -104,14 +104,14 @@ __global__ __launch_bounds__(256) void k_hw_error(int op, uint32_t first, uint32
     if (op == 0) {
       r = __builtin_amdgcn_exp2f(x);
       y = exp2((double)x);
-    } else if (op == 1) {
+    } else if (op == 1 || op == 3) {
       r = __builtin_amdgcn_logf(x);
       y = log2((double)x);
     } else {
       r = __builtin_amdgcn_rcpf(x);
       y = 1.0 / (double)x;
     }
-    const double q = fabs((double)r - y) / fabs(y) * 0x1p43;
+    const double q = fabs((double)r - y) / (op == 3 ? fmax(1.0, fabs(y)) : fabs(y)) * 0x1p43;
     worst = max(worst, q < 4.0e9 ? (uint32_t)q : 0xffffffffu);  // NaN -> saturated
   }
 #pragma unroll

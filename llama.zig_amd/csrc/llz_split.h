@@ -468,7 +468,7 @@ __device__ __forceinline__ bool split_merge(const KArgs& A, int row, SplitShared
     ok = tc <= kTokCap;
     if (ok) {
       token_sort(S.tl, S.tl + kTokCap, S.part, tc);
-      if (w == 0) token_select(kernel_args_ptr(), row, S.tl + kTokCap, tc, S.s_est, S.w_est, 0.0, -1.0, u_row, theta, &S.tfail);
+      if (w == 0) token_select<false>(kernel_args_ptr(), row, S.tl + kTokCap, tc, S.s_est, S.w_est, 0.0, -1.0, u_row, theta, &S.tfail);
       lds_barrier();
       LLZ_STAMP(sr, 10);
       ok = S.tfail == 0u;

@@ -1041,7 +1041,9 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       s_est += G > i ? F.qsum[i] * ri : 0.0f;
       w_est += G > i ? F.qwsum[i] * ri : 0.0f;
     }
-    const bool typ = P.typical_p > 0.0f && P.typical_p < 1.0f;
+    // (soft-capped rows leave typical-p to the exact phases: the register
+    // pressure of its code spilled in the capped kernel's token path)
+    const bool typ = XM != kXmCap && P.typical_p > 0.0f && P.typical_p < 1.0f;
     if (!tbad && typ) {
       // typical-p (sampler.zig:128-132): this wave's part of sum_i e_i log2
       // e_i, from its estimates (e_i ~ q_i R_w, log2 e_i ~ log2 q_i + aw),
@@ -1207,7 +1209,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       collect(P.tok_theta);
       float theta_t = P.tok_theta;
       const uint32_t kk = P.top_k;
-      if (F.tcand > (uint32_t)kTokCap && F.tfail == 0u && kk >= 1u && kk <= (uint32_t)(kTokCap / 4) &&
+      if (XM != kXmCap && F.tcand > (uint32_t)kTokCap && F.tfail == 0u && kk >= 1u && kk <= (uint32_t)(kTokCap / 4) &&
           kk < (uint32_t)n) {
         token_sort(tl, tl + kTokCap, reinterpret_cast<uint8_t*>(&F.qpos[0][0]), kTokCap);
         if (t == 0) {  // wave 0 placed the sorted keys
@@ -1227,7 +1229,8 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         if (w == 0) {
           double hs_lo = 0.0, hs_hi = -1.0;  // the row's entropy (typical-p rows)
           if (typ) entropy_star(P, F.tx, F.txa, F.qsum, F.cw, W, G, m, s_est, &hs_lo, &hs_hi);
-          token_select(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, w_est, hs_lo, hs_hi, u_row, theta_t, &F.tfail);
+          token_select<XM != kXmCap>(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, w_est, hs_lo, hs_hi, u_row, theta_t,
+                                     &F.tfail);
         }
       } else if (t == 0) {
         F.tfail = 1u;

@@ -143,8 +143,11 @@ __device__ __forceinline__ void entropy_star(const RowParams& P, const float* tx
 // before typical-p are decided).  Writes the token, the draw flag, the kept
 // count and ids; sets *tfail instead when a decision does not hold over the
 // intervals.
+// TYP false leaves typical-p's decisions out of the code (its rows are then
+// decided only when they keep nothing before typical-p).
 // Out of line; the launch's arguments come through the kernel's argument
 // segment (as the other out-of-line paths take them).
+template <bool TYP>
 __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint64_t* srt, int c, float s_est,
                                           float w_est, double hs_lo, double hs_hi, float u, float theta,
                                           uint32_t* tfail) {
@@ -266,7 +269,8 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   // typical-p (sampler.zig:128-154) over the kept positions [0, K); the
   // positions kept after it are [a, b)
   int a = 0, b = K;
-  if (ok && K > 0 && P.typical_p > 0.0f && P.typical_p < 1.0f) {
+  if (!TYP && K > 0 && P.typical_p > 0.0f && P.typical_p < 1.0f) ok = false;
+  if constexpr (TYP) if (ok && K > 0 && P.typical_p > 0.0f && P.typical_p < 1.0f) {
     // The reference's entropy H^ (sampler.zig:129-132): the sequential sum of
     // t_i = -RN(p_i logf(p_i)), p_i = RN(e_i / S^).  With pi_i = e_i / S^ and
     // h_i = -pi_i ln pi_i, |t_i - h_i| <= 2^-21.9 h_i + 2^-23.9 pi_i (p's,
@@ -359,23 +363,60 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   }
   const int Kp = b - a;  // the kept count
   uint32_t token = c >= 1 ? readlane_u32((uint32_t)k0, 0) : 0u, consumed = 0;  // indices[0]
-  if (ok && Kp > 0) {
-    // total and draw (sampler.zig:156-168) over positions [a, b): E = C_{b-1}
-    // - C_{a-1}; the draw stops at the first q with u E - (C_q - C_{a-1})
-    // below -margin (none of them within it)
-    const double Ca = a > 0 ? prefix(a - 1) : 0.0;
-    const double E = prefix(b - 1) - Ca;
+  if constexpr (TYP) {
+    if (ok && Kp > 0) {
+      // total and draw (sampler.zig:156-168) over positions [a, b): E = C_{b-1}
+      // - C_{a-1}; the draw stops at the first q with u E - (C_q - C_{a-1})
+      // below -margin (none of them within it)
+      const double Ca = a > 0 ? prefix(a - 1) : 0.0;
+      const double E = prefix(b - 1) - Ca;
+      const double Au = (double)u * E;
+      const double margin = (4.0 * Kp + 16.0) * 0x1p-24 * E;
+      int st = -1;
+      double dcarry = 0.0;
+      for (int bb = 0; bb < b && st < 0 && ok; bb += kWave) {
+        const int q = bb + lane;
+        const double C = bb == 0 ? C0 : dcarry + wave_incl_scan_f64(q < K ? (double)e_at(q) : 0.0);
+        const double dq = Au - (C - Ca);
+        const bool in = q >= a && q < b;
+        const bool unc = in && fabs(dq) <= margin;
+        const bool stp = in && dq < -margin;
+        const uint64_t mk = bal64(unc || stp);
+        if (mk != 0ull) {
+          const int fq = __ffsll((long long)mk) - 1;
+          if ((bal64(unc) >> fq) & 1ull)
+            ok = false;
+          else
+            st = bb + fq;
+        }
+        dcarry = readlane_f64(C, kWave - 1);
+      }
+      consumed = 1;
+      if (st >= 0) token = st < kWave ? readlane_u32((uint32_t)k0, st) : id_at(st);
+    }
+  } else if (ok && K > 0) {
+    // total and draw (sampler.zig:156-168): E = C_{K-1}; the draw stops at
+    // the first q with u E - C_q below -margin (none of them within it)
+    double E;
+    if (K <= kWave) {
+      E = readlane_f64(C0, K - 1);
+    } else {
+      E = 0.0;
+      for (int bb = 0; bb < K; bb += kWave) {
+        const int q = bb + lane;
+        E += readlane_f64(wave_incl_scan_f64(q < K ? (double)e_at(q) : 0.0), kWave - 1);
+      }
+    }
     const double Au = (double)u * E;
-    const double margin = (4.0 * Kp + 16.0) * 0x1p-24 * E;
+    const double margin = (4.0 * K + 16.0) * 0x1p-24 * E;
     int st = -1;
     double dcarry = 0.0;
-    for (int bb = 0; bb < b && st < 0 && ok; bb += kWave) {
+    for (int bb = 0; bb < K && st < 0 && ok; bb += kWave) {
       const int q = bb + lane;
       const double C = bb == 0 ? C0 : dcarry + wave_incl_scan_f64(q < K ? (double)e_at(q) : 0.0);
-      const double dq = Au - (C - Ca);
-      const bool in = q >= a && q < b;
-      const bool unc = in && fabs(dq) <= margin;
-      const bool stp = in && dq < -margin;
+      const double dq = Au - C;
+      const bool unc = q < K && fabs(dq) <= margin;
+      const bool stp = q < K && dq < -margin;
       const uint64_t mk = bal64(unc || stp);
       if (mk != 0ull) {
         const int fq = __ffsll((long long)mk) - 1;

@@ -422,7 +422,7 @@ def debug_math(x, extra: bool = False):
 def debug_hw_error(op: int, first_bits: int, count: int) -> float:
     """Largest relative error, in units of 2^-23, of the hardware exp2 (op 0),
     log2 (op 1) or reciprocal (op 2) over `count` float bit patterns from
-    `first_bits`."""
+    `first_bits`; op 3: the log2's error relative to max(1, |log2 x|)."""
     torch = _torch()
     out = torch.zeros(1, dtype=torch.int32, device="cuda")
     rc = _lib().llz_debug_hw_error(op, first_bits, count, out.data_ptr(), _stream_ptr(None))

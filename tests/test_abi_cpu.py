@@ -136,7 +136,7 @@ def test_argument_validation_without_gpu():
     assert L.llz_argmax_rows(fake, 16, 1, 16, None, None, None) == llz.LLZ_E_INVALID_ARG
     assert L.llz_debug_math(None, None, None, None, None, 4, None) == llz.LLZ_E_INVALID_ARG
     assert L.llz_debug_hw_error(0, 0, 16, None, None) == llz.LLZ_E_INVALID_ARG
-    assert L.llz_debug_hw_error(3, 0, 16, fake, None) == llz.LLZ_E_INVALID_ARG
+    assert L.llz_debug_hw_error(4, 0, 16, fake, None) == llz.LLZ_E_INVALID_ARG
     assert L.llz_debug_hw_error(0, 0, 0, fake, None) == llz.LLZ_E_INVALID_ARG
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert L.llz_strerror(code)

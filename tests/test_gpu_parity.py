@@ -129,6 +129,16 @@ def test_hardware_exp2_log2_within_one_ulp(cuda, name, op, lo, hi):
     assert err <= 1.0, f"{name}: {err} units of 2^-23"
 
 
+def test_hardware_log2_entropy_estimate(cuda):
+    """The token path's entropy estimate takes the hardware log2 of every
+    estimate q in [2^-100, 2^64] (q < 2^-100 is left out) to be within
+    2^-18 max(1, |log2 q|) of log2 q (32 units of 2^-23 relative to
+    max(1, |log2 q|)); checked on every float of that range."""
+    err = llz.debug_hw_error(3, 0x0D800000, 0x5F800000 - 0x0D800000 + 1)
+    assert err <= 32.0, f"log2: {err} units of 2^-23 relative to max(1, |log2 x|)"
+
+
+
 # ---------------------------------------------------------------------------
 # the five configurations and the headline batch, full vocab
 # ---------------------------------------------------------------------------
