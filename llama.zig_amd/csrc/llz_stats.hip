@@ -540,7 +540,7 @@ __device__ __noinline__ int claim_row(unsigned long long* word, unsigned long lo
 // read through post-processing and/or the fused repetition penalty
 // (llz_xform.h); otherwise as they are.
 // wslot: the workgroup's block of the special-queue overflow area.
-template <bool FASTLD, int XM>
+template <bool FASTLD, int XM, bool EXT = false>
 __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& U, PenShared& pen_sh, int wslot) {
   constexpr bool XF = XM != kXmNone;
   const RowParams P = A.P;
@@ -1043,7 +1043,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
     }
     // (soft-capped rows leave typical-p to the exact phases: the register
     // pressure of its code spilled in the capped kernel's token path)
-    const bool typ = XM != kXmCap && P.typical_p > 0.0f && P.typical_p < 1.0f;
+    const bool typ = EXT && XM != kXmCap && P.typical_p > 0.0f && P.typical_p < 1.0f;
     if (!tbad && typ) {
       // typical-p (sampler.zig:128-132): this wave's part of sum_i e_i log2
       // e_i, from its estimates (e_i ~ q_i R_w, log2 e_i ~ log2 q_i + aw),
@@ -1209,7 +1209,7 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
       collect(P.tok_theta);
       float theta_t = P.tok_theta;
       const uint32_t kk = P.top_k;
-      if (XM != kXmCap && F.tcand > (uint32_t)kTokCap && F.tfail == 0u && kk >= 1u && kk <= (uint32_t)(kTokCap / 4) &&
+      if (EXT && XM != kXmCap && F.tcand > (uint32_t)kTokCap && F.tfail == 0u && kk >= 1u && kk <= (uint32_t)(kTokCap / 4) &&
           kk < (uint32_t)n) {
         token_sort(tl, tl + kTokCap, reinterpret_cast<uint8_t*>(&F.qpos[0][0]), kTokCap);
         if (t == 0) {  // wave 0 placed the sorted keys
@@ -1227,10 +1227,17 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
         token_sort(tl, tl + kTokCap, reinterpret_cast<uint8_t*>(&F.qpos[0][0]), tc);
         LLZ_STAMP(row, 34);
         if (w == 0) {
-          double hs_lo = 0.0, hs_hi = -1.0;  // the row's entropy (typical-p rows)
-          if (typ) entropy_star(P, F.tx, F.txa, F.qsum, F.cw, W, G, m, s_est, &hs_lo, &hs_hi);
-          token_select<XM != kXmCap>(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, w_est, hs_lo, hs_hi, u_row, theta_t,
-                                     &F.tfail);
+          // typical-p rows take their own copy of the decisions, so that the
+          // others keep the shorter chain
+          if (typ) {
+            double hs_lo = 0.0, hs_hi = -1.0;  // the row's entropy
+            entropy_star(P, F.tx, F.txa, F.qsum, F.cw, W, G, m, s_est, &hs_lo, &hs_hi);
+            token_select<true>(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, w_est, hs_lo, hs_hi, u_row, theta_t,
+                               &F.tfail);
+          } else {
+            token_select<false>(kernel_args_ptr(), row, tl + kTokCap, tc, s_est, w_est, 0.0, -1.0, u_row, theta_t,
+                                &F.tfail);
+          }
         }
       } else if (t == 0) {
         F.tfail = 1u;
@@ -1827,11 +1834,11 @@ __device__ __forceinline__ void stats_row(const KArgs& A, int row, StatsShared& 
 }
 
 // One row per workgroup: launches whose rows fit the CUs at once.
-template <bool FASTLD, int XM>
+template <bool FASTLD, int XM, bool EXT>
 __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
   __shared__ StatsShared U;
   __shared__ PenShared pen_sh;  // kXfPen: the row's penalised positions
-  stats_row<FASTLD, XM>(A, (int)blockIdx.x, U, pen_sh, (int)blockIdx.x);
+  stats_row<FASTLD, XM, EXT>(A, (int)blockIdx.x, U, pen_sh, (int)blockIdx.x);
 }
 
 // More rows than CUs: one workgroup per CU (all resident), each taking rows
@@ -1839,7 +1846,7 @@ __global__ __launch_bounds__(NT) void k_stats(KArgs A) {
 // left, so rows of unequal cost spread over every CU.  (Launched one row per
 // workgroup instead, the hardware hands workgroups to the XCDs in turn, so a
 // batch whose cost alternates from row to row loads half of the XCDs only.)
-template <bool FASTLD, int XM>
+template <bool FASTLD, int XM, bool EXT>
 __global__ __launch_bounds__(NT) void k_stats_rows(KArgs A) {
   __shared__ StatsShared U;
   __shared__ PenShared pen_sh;
@@ -1851,7 +1858,7 @@ __global__ __launch_bounds__(NT) void k_stats_rows(KArgs A) {
     const __attribute__((address_space(4))) KArgs* Ap =
         (const __attribute__((address_space(4))) KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(Ap));
-    stats_row<FASTLD, XM>(*(const KArgs*)Ap, row, U, pen_sh, (int)blockIdx.x);
+    stats_row<FASTLD, XM, EXT>(*(const KArgs*)Ap, row, U, pen_sh, (int)blockIdx.x);
     if (threadIdx.x == 0) next_row = claim_row(A.Q.claim, A.P.epoch, A.P.grid);
     __syncthreads();  // also: every wave is done with this row's shared memory
     row = next_row;
@@ -1898,6 +1905,10 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
   // transformed rows split with chunks of at most 2 float4 per thread (each
   // logit's exact post-processing is then a few per thread)
   const bool split = P.split_s >= 2 && fastld && P.rows <= kSplitRows && (xm == kXmNone || P.split_nv <= 2);
+  // token-only calls with typical-p (not soft-capped) take the instantiation
+  // that carries typical-p's decisions and the list's second collection
+  // round; the others keep the shorter code
+  const bool ext = (P.flags & kFlagTokenOnly) != 0u && P.typical_p > 0.0f && P.typical_p < 1.0f && xm != kXmCap;
   const dim3 grid(split ? P.rows * P.split_s : (claim ? P.grid : P.rows)), block(NT);
   void (*kern)(KArgs) = nullptr;
   if (split) {
@@ -1915,18 +1926,25 @@ hipError_t launch_sample(const RowParams& P, const RowPtrs& Q, hipEvent_t ev_beg
       kern = P.split_nv == 1 ? k_split<1, kXmCap> : k_split<2, kXmCap>;
     }
   } else if (claim) {
-    if (fastld)
-      kern = xm == kXmNone ? k_stats_rows<true, kXmNone> : xm == kXmLight ? k_stats_rows<true, kXmLight>
-                                                                          : k_stats_rows<true, kXmCap>;
+    if (ext)
+      kern = fastld ? (xm == kXmNone ? k_stats_rows<true, kXmNone, true> : k_stats_rows<true, kXmLight, true>)
+                    : (xm == kXmNone ? k_stats_rows<false, kXmNone, true> : k_stats_rows<false, kXmLight, true>);
+    else if (fastld)
+      kern = xm == kXmNone ? k_stats_rows<true, kXmNone, false> : xm == kXmLight ? k_stats_rows<true, kXmLight, false>
+                                                                                 : k_stats_rows<true, kXmCap, false>;
     else
-      kern = xm == kXmNone ? k_stats_rows<false, kXmNone> : xm == kXmLight ? k_stats_rows<false, kXmLight>
-                                                                           : k_stats_rows<false, kXmCap>;
+      kern = xm == kXmNone ? k_stats_rows<false, kXmNone, false> : xm == kXmLight ? k_stats_rows<false, kXmLight, false>
+                                                                                  : k_stats_rows<false, kXmCap, false>;
   } else {
-    if (fastld)
-      kern = xm == kXmNone ? k_stats<true, kXmNone> : xm == kXmLight ? k_stats<true, kXmLight> : k_stats<true, kXmCap>;
+    if (ext)
+      kern = fastld ? (xm == kXmNone ? k_stats<true, kXmNone, true> : k_stats<true, kXmLight, true>)
+                    : (xm == kXmNone ? k_stats<false, kXmNone, true> : k_stats<false, kXmLight, true>);
+    else if (fastld)
+      kern = xm == kXmNone ? k_stats<true, kXmNone, false> : xm == kXmLight ? k_stats<true, kXmLight, false>
+                                                                            : k_stats<true, kXmCap, false>;
     else
-      kern = xm == kXmNone ? k_stats<false, kXmNone> : xm == kXmLight ? k_stats<false, kXmLight>
-                                                                      : k_stats<false, kXmCap>;
+      kern = xm == kXmNone ? k_stats<false, kXmNone, false> : xm == kXmLight ? k_stats<false, kXmLight, false>
+                                                                             : k_stats<false, kXmCap, false>;
   }
   void* args[] = {const_cast<KArgs*>(&A)};
   if (hipLaunchKernel((const void*)kern, grid, block, args, 0, st) != hipSuccess) return hipErrorLaunchFailure;

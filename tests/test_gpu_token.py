@@ -232,22 +232,31 @@ def test_token_only_overflow_falls_back(cuda, kind):
 
 @pytest.mark.parametrize("terms", [600, 700])
 def test_token_only_list_collected_again(cuda, terms):
-    """Terms near the maximum over a low floor, more than the 512-entry list
-    holds, under top-k 40: the list is collected again above just below the
-    41st largest term collected, and the row decides on the token path (min-p's
-    count beyond the list unknown: top-k cuts inside it).  Every row against
-    the oracle."""
+    """More terms above min-p's threshold than the 512-entry list holds (40
+    of them 1% apart at the top, the rest in [-1.5, -0.5] below the maximum,
+    over a low floor), under top-k 40 and typical-p 0.98 (the token call's
+    second collection round is built into the typical-p instantiation): the
+    list is collected again above just below the 41st largest term
+    collected, and every row decides on the token path (min-p's count beyond
+    the list unknown: top-k cuts inside it; the kept surprises lie below the
+    entropy).  Every row against the oracle; without typical-p the same rows
+    take the exact phases, also against the oracle."""
     w = WORKLOADS["headline"]
     rows = 4
-    x = _many_near_max(np.random.default_rng(11), rows, w.vocab, terms)
+    rng = np.random.default_rng(11)
+    x = rng.normal(-30.0, 1.0, size=(rows, w.vocab)).astype(np.float32)
+    for r in range(rows):
+        idx = rng.choice(w.vocab, terms, replace=False)
+        x[r, idx[:40]] = (-0.01 * np.arange(40)).astype(np.float32)
+        x[r, idx[40:]] = rng.uniform(-1.5, -0.5, terms - 40).astype(np.float32)
     u = llz.rng_uniforms(w.uniform_seed, rows)
-    llz.debug_set_split(1)
-    try:
-        g = _run(cuda, x, w.params, u, cap=256)
-    finally:
-        llz.debug_set_split(0)
-    _check_oracle(x, w.params, u, g)
-    assert np.all(g["path"] & PATH_TOKEN_ONLY)
+    params = dataclasses.replace(w.params, typical_p=0.98)
+    g = _run(cuda, x, params, u, cap=256)
+    _check_oracle(x, params, u, g)
+    assert np.all(g["path"] & PATH_TOKEN_ONLY), f"paths {g['path']}"
+    g0 = _run(cuda, x, w.params, u, cap=256)
+    _check_oracle(x, w.params, u, g0)
+    assert not np.any(g0["path"] & PATH_TOKEN_ONLY), f"paths {g0['path']}"
 
 
 def _many_near_max(rng, rows, n, k):
