@@ -270,7 +270,15 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   // positions kept after it are [a, b)
   int a = 0, b = K;
   if (!TYP && K > 0 && P.typical_p > 0.0f && P.typical_p < 1.0f) ok = false;
-  if constexpr (TYP) if (ok && K > 0 && P.typical_p > 0.0f && P.typical_p < 1.0f) {
+  // When the running sum of all K kept terms stays at most typical_p
+  // whatever S (the largest of the running sums in any order), typical-p
+  // drops nothing, and neither the entropy nor the order matters
+  bool typ_cut = false;
+  if constexpr (TYP) {
+    if (ok && K > 0 && P.typical_p > 0.0f && P.typical_p < 1.0f)
+      typ_cut = !(prefix(K - 1) * iS_lo * (1.0 + (2.0 * K + 4.0) * 0x1p-24) <= (double)P.typical_p);
+  }
+  if constexpr (TYP) if (typ_cut) {
     // The reference's entropy H^ (sampler.zig:129-132): the sequential sum of
     // t_i = -RN(p_i logf(p_i)), p_i = RN(e_i / S^).  With pi_i = e_i / S^ and
     // h_i = -pi_i ln pi_i, |t_i - h_i| <= 2^-21.9 h_i + 2^-23.9 pi_i (p's,

@@ -328,15 +328,19 @@ def test_token_only_typical_rows(cuda):
 
 def test_token_only_typical_entropy_among_kept_falls_back(cuda):
     """Rows whose entropy lies among the kept terms' surprises (30 tokens near
-    +10 over N(0, 1) logits): their typical order depends on the exact
-    entropy, so they take the exact phases.  Every row against the oracle."""
+    +10 over N(0, 1) logits) and whose typical-p cut falls inside the kept
+    terms (typical-p 0.5): their typical order depends on the exact entropy,
+    so they take the exact phases.  With typical-p 0.98 nothing is cut (the
+    kept terms' sum stays below it whatever the normaliser), the order does
+    not matter, and the same rows decide on the token path (most of them).
+    Every row against the oracle."""
     rng = np.random.default_rng(7)
     rows, n = 8, 32768
     x = rng.normal(0.0, 1.0, (rows, n)).astype(np.float32)
     for r in range(rows):
         ids = rng.choice(n, 30, replace=False)
         x[r, ids] = (10.0 + rng.normal(0.0, 0.5, 30)).astype(np.float32)
-    params = WORKLOADS["c5"].params
+    params = dataclasses.replace(WORKLOADS["c5"].params, typical_p=0.5)
     u = llz.rng_uniforms(5, rows)
     g = _run(cuda, x, params, u)
     _check_oracle(x, params, u, g)
@@ -346,3 +350,8 @@ def test_token_only_typical_entropy_among_kept_falls_back(cuda):
         s = -np.log(o.probs[o.order[:20]].astype(np.float64))
         assert s.min() < o.entropy < s.max()
     assert np.all((g["path"] & PATH_TOKEN_ONLY) == 0)
+    p98 = WORKLOADS["c5"].params
+    g98 = _run(cuda, x, p98, u)
+    _check_oracle(x, p98, u, g98)
+    # (a row may still leave the token path for another decision, e.g. top-p's cut near S's interval)
+    assert np.mean((g98["path"] & PATH_TOKEN_ONLY) != 0) >= 0.75, f"paths {g98['path']}"
