@@ -297,6 +297,13 @@ static int sample_rows_impl(const float* d_logits, int64_t row_stride, int32_t r
   const bool tok_topp = !tok_minp && !(cfg->min_p > 0.0f) && cfg->top_p > 0.0f && cfg->top_p < 1.0f &&
                         vocab > kCandCap;
   P.tok_theta = tok_minp ? P.cand_theta : (tok_topp ? 0x1p-10f : 0.0f);
+  {
+    // the token path's interval of S: the factors that depend on n alone
+    // (IEEE double, the same values the device would compute)
+    const double g1 = (double)(vocab - 1) * 0x1p-24, gn = (double)vocab * 0x1p-24;
+    P.tok_rs = g1 / (1.0 - g1);
+    P.tok_rwk = gn < 0.5 ? 0x1p-24 / (1.0 - 0x1p-24) * (1.0 + gn / (1.0 - gn)) * (1.0 + 0x1p-9) : 0.0;
+  }
   const bool typical_on = cfg->typical_p > 0.0f && cfg->typical_p < 1.0f;
   const bool tok_only = !(extras && (extras->d_kept_probs || extras->d_row_stats)) && (tok_minp || tok_topp) &&
                         !(typical_on && (xf_src & kXfCap));

@@ -109,6 +109,8 @@ struct RowParams {
   int32_t fb_slots;  // full-row fallback buffers in the workspace
   int32_t grid;      // k_stats workgroups: rows [0, grid) one each, the rest claimed (Q.claim)
   uint64_t epoch;    // this call's tag: a fallback slot whose owner word holds it is in use
+  double tok_rs;     // token path: the recursive-summation bound g / (1 - g), g = (n - 1) 2^-24
+  double tok_rwk;    // token path: u / (1 - u) (1 + gamma_n) (1 + 2^-9), the weighted bound's factor (0: gamma_n >= 1/2)
   int32_t split_s;   // split rows: chunks per row (0: rows are not split)
   int32_t split_nv;  // split rows: float4 per thread per chunk (chunk = 2048 split_nv logits)
   float split_b;     // split rows: a chunk's elements with (m_c - v) l2e_t < split_b may be candidates

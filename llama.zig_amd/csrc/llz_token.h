@@ -195,8 +195,7 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   const bool open_end = L > M;
   const int Lc = open_end ? M : L;
   // the interval of the reference's normaliser
-  const double g = (double)(n - 1) * 0x1p-24;
-  double rs = g / (1.0 - g);
+  double rs = P.tok_rs;  // g / (1 - g), g = (n - 1) 2^-24 (host)
   // The same bound by where the mass lies (w_est > 0): the computed partial
   // sums of positive terms satisfy S^_i <= S_i (1 + gamma_i), so |S^ - S| <=
   // u / (1 - u) sum_{i>=2} S^_i <= u / (1 - u) (1 + gamma_n) sum_i S_i, and
@@ -205,11 +204,12 @@ __device__ __forceinline__ void token_select(const KArgs* A, int row, const uint
   // so W / S <= (w_est / s_est) (1 + e) / (1 - e) <= (w_est / s_est) (1 +
   // 2^-9) (e = 2^-14 + est_xe <= 2^-10.8).  With the row's mass spread
   // evenly this halves the interval; with it near the row's end, far more.
-  if (w_est > 0.0f) {
-    const double gn = (double)n * 0x1p-24;
-    const double rw = 0x1p-24 / (1.0 - 0x1p-24) * (1.0 + gn / (1.0 - gn)) * ((double)w_est / (double)s_est) *
-                      (1.0 + 0x1p-9);
-    if (gn < 0.5 && rw < rs) rs = rw;
+  // (tok_rwk = u / (1 - u) (1 + gamma_n) (1 + 2^-9) from the host, 0 when
+  // gamma_n >= 1/2; the ratio from above: a correctly rounded f32 quotient
+  // widened by its half ulp)
+  if (w_est > 0.0f && P.tok_rwk > 0.0) {
+    const double rw = P.tok_rwk * ((double)(w_est / s_est) * (1.0 + 0x1p-23));
+    if (rw < rs) rs = rw;
   }
   // the estimate's own error e; S^ in s_est [(1 - rs)(1 - e), (1 + rs)(1 + e)]
   const double e_est = 0x1p-14 + (double)P.est_xe;  // est_xe: soft-capped rows' estimates
